@@ -1,0 +1,250 @@
+"""Benchmark of the paged GQA decode hot path on one MI355X.
+
+Workload: paged GQA decode attention at TinyLlama
+geometry -- 64 rows with context U[128, 2048] plus 8 zero-length rows,
+32 query / 4 KV heads, head_dim 64, 16-token pages on a seeded permutation,
+bf16, N(0,1) inputs, scale 1/8.  A step is one attention call (split stage +
+log-sum-exp merge) over one batch.  To keep the 256 MB Infinity Cache from
+serving the K/V pages, steps rotate over several independent copies of the
+page pool (``--pools``), so every step streams its pages from HBM.
+
+Prints ONE JSON line.  ``value`` is algorithmic GB/s of the whole call
+(byte model of benchmark/attention_benchmark.py:148-161: q, K, V, tables,
+output of the active rows) over the timed steps; ``roofline`` reports the
+dominant (split-stage) kernel alone, timed with HIP events recorded around
+it on the launch stream inside the same timed region.  ``cpu_baseline`` is
+the CPU oracle on a bounded sample of the same rows, on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+REPO_ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO_ROOT))
+
+METRIC = "paged GQA decode HBM GB/s (% peak) + decode tokens/s, TinyLlama-geom b=64"
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = REPO_ROOT / "profiles" / "paged_decode_tinyllama_b64_traffic.json"
+
+
+def parse_args() -> argparse.Namespace:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--pools", type=int, default=6, help="rotated K/V page pools")
+    parser.add_argument("--split-size", type=int, default=256)
+    parser.add_argument("--cpu-seconds", type=float, default=10.0,
+                        help="target CPU time of the oracle baseline sample")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    return parser.parse_args()
+
+
+def cpu_baseline(case, rows: list[int], seconds: float) -> dict:
+    """Time the CPU oracle (fp32 torch on the host cores) on ``rows``."""
+
+    from oracle.reference import paged_gqa_decode_reference
+    from tensorforge_amd.workloads import decode_attention_bytes
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cpu = case.to("cpu")
+    args = (cpu.query[rows], cpu.key_cache, cpu.value_cache, cpu.block_tables[rows],
+            cpu.context_lengths[rows])
+    paged_gqa_decode_reference(*args, scale=case.scale)  # warmup
+    samples = []
+    started = time.perf_counter()
+    while True:
+        t0 = time.perf_counter_ns()
+        paged_gqa_decode_reference(*args, scale=case.scale)
+        samples.append((time.perf_counter_ns() - t0) / 1e9)
+        if len(samples) >= 5 and time.perf_counter() - started >= seconds:
+            break
+        if len(samples) >= 200:
+            break
+    samples.sort()
+    p50 = samples[len(samples) // 2]
+    lengths = [case.lengths[r] for r in rows]
+    nbytes = decode_attention_bytes(lengths, 32, 4, 64, 16, 2)
+    return {
+        "value": round(nbytes / p50 / 1e9, 4),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (
+            f"CPU oracle paged_gqa_decode_reference (fp32 torch {torch.__version__}) on "
+            f"{len(rows)} of the 64 active rows (sum ctx {sum(lengths)}), p50 of "
+            f"{len(samples)} reps = {p50 * 1e3:.2f} ms; {platform.processor() or platform.machine()}"
+        ),
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            json.dumps({
+                "error": "this build runs on one GPU; multi-GPU sharding of the decode path "
+                         "is design-only (see the sharding section of the design notes)",
+                "n_gpus": args.gpus,
+            })
+        )
+        return 2
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 1
+
+    from tensorforge_amd import _native
+    from tensorforge_amd.kernels import PagedAttentionWorkspace, set_attention_split_size
+    from tensorforge_amd.workloads import decode_attention_bytes, tinyllama_decode_case
+
+    device = torch.device("cuda", 0)
+    lib = _native.library()
+    set_attention_split_size(args.split_size)
+
+    case = tinyllama_decode_case(seed=0, dtype=torch.bfloat16)
+    gpu = case.to(device)
+    pools = [(gpu.key_cache, gpu.value_cache)]
+    for _ in range(args.pools - 1):
+        pools.append((gpu.key_cache.clone(), gpu.value_cache.clone()))
+    batch, query_heads, head_dim = gpu.query.shape
+    num_blocks, block_size, kv_heads, _ = gpu.key_cache.shape
+    table_width = gpu.block_tables.shape[1]
+    max_context = 2048
+    split_size = args.split_size
+    num_splits = math.ceil(max_context / split_size)
+    workspace = PagedAttentionWorkspace.allocate(
+        batch_capacity=batch, query_heads=query_heads, head_dim=head_dim,
+        max_context_length=num_splits * 256, device=device,
+    )
+    head_bucket = workspace.partial_accumulator.shape[1]
+    capacity = workspace.partial_max.numel()
+    output = torch.empty_like(gpu.query)
+    dtype = _native.dtype_code(gpu.query.dtype)
+    stream = torch.cuda.current_stream(device)
+    handle = stream.cuda_stream
+    variant = lib.tf_paged_gqa_decode_variant(dtype, head_dim, query_heads // kv_heads, 0)
+
+    def split_stage(pool: int) -> None:
+        key_cache, value_cache = pools[pool]
+        _native.check(lib.tf_paged_gqa_decode_partials(
+            gpu.query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+            gpu.block_tables.data_ptr(), gpu.context_lengths.data_ptr(),
+            workspace.partial_max.data_ptr(), workspace.partial_sum.data_ptr(),
+            workspace.partial_accumulator.data_ptr(), capacity, head_bucket, batch,
+            query_heads, kv_heads, head_dim, num_blocks, block_size, table_width, split_size,
+            num_splits, case.scale, dtype, 0, handle), "partials")
+
+    def merge_stage() -> None:
+        _native.check(lib.tf_paged_gqa_decode_merge(
+            workspace.partial_max.data_ptr(), workspace.partial_sum.data_ptr(),
+            workspace.partial_accumulator.data_ptr(), gpu.context_lengths.data_ptr(),
+            output.data_ptr(), capacity, head_bucket, batch, query_heads, head_dim, split_size,
+            num_splits, table_width * block_size, dtype, handle), "merge")
+
+    # Parity gate before timing: the benchmarked output must match the oracle.
+    split_stage(0)
+    merge_stage()
+    torch.cuda.synchronize()
+    from tensorforge_amd.kernels import paged_gqa_decode_attention
+
+    check = paged_gqa_decode_attention(
+        gpu.query, gpu.key_cache, gpu.value_cache, gpu.block_tables, gpu.context_lengths,
+        scale=case.scale, max_context_length=max_context, workspace=workspace,
+    )
+    torch.cuda.synchronize()
+    if not torch.equal(check.view(torch.int16), output.view(torch.int16)):
+        print(json.dumps({"error": "raw C-ABI stages and the Python entry point disagree"}))
+        return 1
+
+    for step in range(args.warmup):
+        split_stage(step % args.pools)
+        merge_stage()
+    torch.cuda.synchronize()
+
+    begin = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    split_end = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    for step in range(args.steps):
+        begin[step].record(stream)
+        split_stage(step % args.pools)
+        split_end[step].record(stream)
+        merge_stage()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = begin[0].elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    split_ms = sum(begin[i].elapsed_time(split_end[i]) for i in range(args.steps)) / args.steps
+
+    lengths = case.lengths
+    nbytes = decode_attention_bytes(lengths, query_heads, kv_heads, head_dim, block_size, 2)
+    value = nbytes / (ms_per_step * 1e-3) / 1e9
+    achieved = nbytes / (split_ms * 1e-3) / 1e9
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "paged GQA decode attention, TinyLlama geometry (BASELINE config 2)",
+            "batch": 64,
+            "padded_rows": 8,
+            "query_heads": query_heads,
+            "kv_heads": kv_heads,
+            "head_dim": head_dim,
+            "page_size": block_size,
+            "context": "U[128,2048], seed 0",
+            "sum_context": sum(lengths),
+            "kernel": "mfma" if variant == _native.TF_ATTENTION_MFMA else "generic",
+            "split_size": split_size,
+            "num_splits": num_splits,
+            "kv_pools_rotated": args.pools,
+            "algorithmic_bytes_per_call": nbytes,
+        },
+        "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "paged_decode_mfma_kernel (split stage)",
+            "kernel_ms": round(split_ms, 6),
+        },
+        "wall_s_timed_loop": round(wall, 4),
+    }
+    if not args.no_cpu_baseline:
+        active = [row for row, ctx in enumerate(lengths) if ctx > 0]
+        result["cpu_baseline"] = cpu_baseline(case, active[:8], args.cpu_seconds)
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

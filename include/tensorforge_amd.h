@@ -1,0 +1,183 @@
+/*
+ * tensorforge_amd.h -- C ABI of the MI355X (gfx950) batched-decode hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream passed
+ * as `void *` (a hipStream_t; NULL selects the default stream).  Kernels are
+ * enqueued asynchronously on that stream; nothing here allocates, frees or
+ * synchronises, so every call is safe inside HIP graph capture.  Tensors are
+ * dense row-major (C-contiguous) in the layouts documented per function.
+ *
+ * Return value: TF_SUCCESS (0) or a nonzero tf_status; tf_last_error() then
+ * holds a message for the calling thread.
+ *
+ * Reference interfaces replaced (Kakarottoooo/TensorForge, paths relative to
+ * the repository root):
+ *   tf_paged_gqa_decode*     tensorforge/kernels/triton_attention.py:326-518
+ *                            (kernels :67-171 one-pass, :173-266 split,
+ *                            :268-316 log-sum-exp reduce)
+ *   tf_paged_kv_write_token  tensorforge/kernels/triton_cache.py:68-133
+ *                            (kernel :23-63)
+ *   tf_paged_kv_write_slots  tensorforge/cache/paged.py:191-236
+ *                            (PagedKVCache.write_layer multi-token scatter)
+ *   tf_rms_norm              tensorforge/kernels/triton_ops.py:179-205
+ *   tf_residual_rms_norm     tensorforge/kernels/triton_ops.py:208-243
+ *   tf_swiglu                tensorforge/kernels/triton_ops.py:246-260
+ */
+#ifndef TENSORFORGE_AMD_H_
+#define TENSORFORGE_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Floating-point element types of the payload tensors. */
+enum tf_dtype {
+  TF_DTYPE_FLOAT32 = 0,
+  TF_DTYPE_FLOAT16 = 1,
+  TF_DTYPE_BFLOAT16 = 2
+};
+
+enum tf_status {
+  TF_SUCCESS = 0,
+  TF_ERROR_INVALID_ARGUMENT = 1, /* a size, pointer or dtype is out of range */
+  TF_ERROR_UNSUPPORTED = 2,      /* valid request this build cannot serve   */
+  TF_ERROR_LAUNCH = 3            /* the HIP runtime rejected a launch        */
+};
+
+/* Attention kernel families (tf_paged_gqa_decode_variant). */
+enum tf_attention_variant {
+  TF_ATTENTION_GENERIC = 0, /* any dtype, head_dim <= 256, group <= 64     */
+  TF_ATTENTION_MFMA = 1     /* bf16/fp16, head_dim in {32,64,128}, group<=16 */
+};
+
+/* tf_paged_gqa_decode* flags. */
+#define TF_ATTENTION_FLAG_FORCE_GENERIC 1
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char *tf_last_error(void);
+
+/* Version of this ABI; bumped on any signature change. */
+int32_t tf_abi_version(void);
+
+/* Which kernel family tf_paged_gqa_decode uses for these parameters. */
+int32_t tf_paged_gqa_decode_variant(int32_t dtype, int32_t head_dim,
+                                    int32_t group_size, int32_t flags);
+
+/*
+ * Paged GQA decode attention: one query token per sequence.
+ *   query           [batch, query_heads, head_dim]            dtype
+ *   key/value_cache [num_blocks, block_size, kv_heads, head_dim] dtype
+ *   block_tables    [batch, table_width] int32 (physical page of each
+ *                   logical page; entries outside [0, num_blocks) are skipped)
+ *   context_lengths [batch] int32 (<= 0: the output row is written as zeros)
+ *   output          [batch, query_heads, head_dim]            dtype
+ * Query head h reads KV head h / (query_heads / kv_heads).  The context of a
+ * row is split into num_splits partitions of split_size tokens; tokens past
+ * num_splits * split_size or past table_width * block_size are ignored.
+ * num_splits == 1 computes each row in one pass and the partial buffers may be
+ * NULL.  Otherwise fp32 partials are written at index
+ * (b * query_heads + h) * num_splits + s (partial_accumulator rows are
+ * partial_row_stride floats apart) and merged by log-sum-exp; partial_capacity
+ * is the number of partial rows the buffers hold.  scale multiplies q.k.
+ * Replaces triton_attention.py:326-518.
+ */
+int32_t tf_paged_gqa_decode(
+    const void *query, const void *key_cache, const void *value_cache,
+    const int32_t *block_tables, const int32_t *context_lengths, void *output,
+    float *partial_max, float *partial_sum, float *partial_accumulator,
+    int64_t partial_capacity, int32_t partial_row_stride, int32_t batch,
+    int32_t query_heads, int32_t kv_heads, int32_t head_dim,
+    int32_t num_blocks, int32_t block_size, int32_t table_width,
+    int32_t split_size, int32_t num_splits, float scale, int32_t dtype,
+    int32_t flags, void *stream);
+
+/*
+ * First stage of tf_paged_gqa_decode alone (num_splits >= 1): writes the
+ * partials of every non-empty split.  Partial max values are base-2
+ * logarithms of the unnormalised scores (score * scale * log2(e)).
+ * Replaces the split kernel launch, triton_attention.py:433-460.
+ */
+int32_t tf_paged_gqa_decode_partials(
+    const void *query, const void *key_cache, const void *value_cache,
+    const int32_t *block_tables, const int32_t *context_lengths,
+    float *partial_max, float *partial_sum, float *partial_accumulator,
+    int64_t partial_capacity, int32_t partial_row_stride, int32_t batch,
+    int32_t query_heads, int32_t kv_heads, int32_t head_dim,
+    int32_t num_blocks, int32_t block_size, int32_t table_width,
+    int32_t split_size, int32_t num_splits, float scale, int32_t dtype,
+    int32_t flags, void *stream);
+
+/*
+ * Second stage: log-sum-exp merge of the partials of each (row, query head)
+ * into output.  Reads only the ceil(context / split_size) splits a row owns.
+ * Replaces the reduce kernel launch, triton_attention.py:461-474.
+ */
+int32_t tf_paged_gqa_decode_merge(
+    const float *partial_max, const float *partial_sum,
+    const float *partial_accumulator, const int32_t *context_lengths,
+    void *output, int64_t partial_capacity, int32_t partial_row_stride,
+    int32_t batch, int32_t query_heads, int32_t head_dim, int32_t split_size,
+    int32_t num_splits, int32_t max_tokens, int32_t dtype, void *stream);
+
+/*
+ * One KV token per batch lane:
+ *   if active_mask[b] != 0:
+ *     key_cache[physical_blocks[b], block_offsets[b], :, :] = keys[b]
+ *     value_cache[...] = values[b]
+ * keys/values [batch, kv_heads, head_dim]; caches as in tf_paged_gqa_decode.
+ * A bit-exact copy; lanes whose destination lies outside the cache are
+ * skipped.  Replaces triton_cache.py:68-133.
+ */
+int32_t tf_paged_kv_write_token(
+    const void *keys, const void *values, void *key_cache, void *value_cache,
+    const int32_t *physical_blocks, const int32_t *block_offsets,
+    const int32_t *active_mask, int32_t batch, int32_t kv_heads,
+    int32_t head_dim, int32_t num_blocks, int32_t block_size, int32_t dtype,
+    void *stream);
+
+/*
+ * Multi-token append through a slot mapping:
+ *   slot = slot_mapping[t] (= physical_block * block_size + offset)
+ *   if 0 <= slot < num_blocks * block_size: cache token row `slot` = row t
+ * keys/values [tokens, kv_heads, head_dim]; slot -1 marks padded lanes.
+ * A bit-exact copy.  Replaces the index_put of cache/paged.py:221-235.
+ */
+int32_t tf_paged_kv_write_slots(
+    const void *keys, const void *values, void *key_cache, void *value_cache,
+    const int64_t *slot_mapping, int32_t tokens, int32_t kv_heads,
+    int32_t head_dim, int32_t num_blocks, int32_t block_size, int32_t dtype,
+    void *stream);
+
+/*
+ * Row-wise RMSNorm over [rows, columns]: y = x * rsqrt(mean(x^2) + eps) * w,
+ * fp32 arithmetic, one rounding.  columns <= 16384.
+ * Replaces triton_ops.py:179-205.
+ */
+int32_t tf_rms_norm(const void *inputs, const void *weight, void *output,
+                    int64_t rows, int32_t columns, float eps, int32_t dtype,
+                    void *stream);
+
+/*
+ * s = x + r in fp32; residual_output = round(s);
+ * norm_output = round(s * rsqrt(mean(s^2) + eps) * w) (normalises the fp32
+ * sum).  Replaces triton_ops.py:208-243.
+ */
+int32_t tf_residual_rms_norm(const void *inputs, const void *residual,
+                             const void *weight, void *residual_output,
+                             void *norm_output, int64_t rows, int32_t columns,
+                             float eps, int32_t dtype, void *stream);
+
+/*
+ * Elementwise SwiGLU: output = g * sigmoid(g) * u in fp32, one rounding.
+ * Replaces triton_ops.py:246-260.
+ */
+int32_t tf_swiglu(const void *gate, const void *up, void *output,
+                  int64_t numel, int32_t dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TENSORFORGE_AMD_H_ */

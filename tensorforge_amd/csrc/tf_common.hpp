@@ -1,0 +1,75 @@
+// Shared device helpers and host error plumbing for the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdarg>
+
+#include "../../include/tensorforge_amd.h"
+
+namespace tf {
+
+// ---------------------------------------------------------------------------
+// Host-side status plumbing.  The message buffer is thread-local so that
+// concurrent callers (one per host thread) never see each other's errors.
+// ---------------------------------------------------------------------------
+void set_error(const char *fmt, ...);
+void clear_error();
+
+inline int32_t fail(int32_t status, const char *what) {
+  set_error("%s", what);
+  return status;
+}
+
+inline int32_t check_launch(const char *kernel) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    set_error("%s launch failed: %s", kernel, hipGetErrorString(err));
+    return TF_ERROR_LAUNCH;
+  }
+  return TF_SUCCESS;
+}
+
+inline bool valid_dtype(int32_t dtype) {
+  return dtype == TF_DTYPE_FLOAT32 || dtype == TF_DTYPE_FLOAT16 ||
+         dtype == TF_DTYPE_BFLOAT16;
+}
+
+inline int32_t dtype_size(int32_t dtype) {
+  return dtype == TF_DTYPE_FLOAT32 ? 4 : 2;
+}
+
+// ---------------------------------------------------------------------------
+// Element conversions.  Storage types are float, _Float16 and __bf16; the
+// narrowing casts compile to the gfx950 round-to-nearest-even converts.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float to_float(T v) {
+  return static_cast<float>(v);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_float(float v) {
+  return static_cast<T>(v);
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Wavefront (64-lane) reductions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
+  return v;
+}
+
+}  // namespace tf

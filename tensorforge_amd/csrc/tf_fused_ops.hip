@@ -1,0 +1,249 @@
+// Row-wise RMSNorm, fused residual-add + RMSNorm and elementwise SwiGLU.
+//
+// All three are HBM-bound streaming kernels.  A row of the norms is held in
+// registers (up to kMaxVecs 16-byte vectors per lane) so each input byte is
+// read once; the sum of squares is reduced across the wavefront with lane
+// shuffles and across wavefronts through LDS.  Arithmetic is fp32 and every
+// output is rounded once to the storage type.
+//
+// Reference semantics:
+//   rms_norm           tensorforge/kernels/triton_ops.py:36-66 (kernel),
+//                      :179-205 (host); oracle kernels/reference.py:10-15
+//   residual_rms_norm  triton_ops.py:68-97, :208-243 -- the residual sum is
+//                      stored rounded, the norm uses the fp32 sum
+//   swiglu             triton_ops.py:106-122, :246-260 -- g*sigmoid(g)*u in
+//                      fp32, one rounding
+#include "tf_common.hpp"
+
+namespace tf {
+namespace {
+
+// Register-cache capacity (vectors per lane) of the norm kernels: 8 x 16-byte
+// vectors for the vector path, 16 scalars for odd widths; with 1024 lanes
+// both cover the 16384-column limit of the reference contract.
+template <int VEC>
+constexpr int max_vecs() { return VEC == 1 ? 16 : 8; }
+
+template <typename T, int VEC>
+struct alignas(sizeof(T) * VEC) Vec {
+  T v[VEC];
+};
+
+// Sum across the whole workgroup (blockDim.x multiple of 64, <= 1024).
+__device__ __forceinline__ float block_sum(float v, float *scratch) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int waves = blockDim.x >> 6;
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float total = 0.f;
+  for (int w = 0; w < waves; ++w) total += scratch[w];
+  return total;
+}
+
+// One workgroup per row.  RESIDUAL selects the fused residual variant.
+template <typename T, int VEC, bool RESIDUAL>
+__global__ void __launch_bounds__(1024)
+rms_norm_kernel(const T *__restrict__ inputs, const T *__restrict__ residual,
+                const T *__restrict__ weight, T *__restrict__ residual_output,
+                T *__restrict__ output, int32_t columns, float eps) {
+  __shared__ float scratch[16];
+  using V = Vec<T, VEC>;
+  const int64_t row = blockIdx.x;
+  const int32_t nvec = columns / VEC;
+  const V *x = reinterpret_cast<const V *>(inputs + row * columns);
+  const V *r = reinterpret_cast<const V *>(residual + (RESIDUAL ? row * columns : 0));
+  V *ro = reinterpret_cast<V *>(residual_output + (RESIDUAL ? row * columns : 0));
+  V *y = reinterpret_cast<V *>(output + row * columns);
+  const V *w = reinterpret_cast<const V *>(weight);
+
+  constexpr int kMaxVecs = max_vecs<VEC>();
+  float cache[kMaxVecs][VEC];
+  float sq = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxVecs; ++k) {
+    const int32_t idx = threadIdx.x + k * blockDim.x;
+    if (idx < nvec) {
+      V xv = x[idx];
+      V rv;
+      if constexpr (RESIDUAL) rv = r[idx];
+      V sv;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float s = to_float(xv.v[e]);
+        if constexpr (RESIDUAL) {
+          s += to_float(rv.v[e]);
+          sv.v[e] = from_float<T>(s);
+        }
+        cache[k][e] = s;
+        sq += s * s;
+      }
+      if constexpr (RESIDUAL) ro[idx] = sv;
+    }
+  }
+  const float inv_rms = rsqrtf(block_sum(sq, scratch) / static_cast<float>(columns) + eps);
+#pragma unroll
+  for (int k = 0; k < kMaxVecs; ++k) {
+    const int32_t idx = threadIdx.x + k * blockDim.x;
+    if (idx < nvec) {
+      V wv = w[idx];
+      V out;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) out.v[e] = from_float<T>(cache[k][e] * inv_rms * to_float(wv.v[e]));
+      y[idx] = out;
+    }
+  }
+}
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256)
+swiglu_kernel(const T *__restrict__ gate, const T *__restrict__ up, T *__restrict__ output,
+              int64_t nvec) {
+  using V = Vec<T, VEC>;
+  const V *g = reinterpret_cast<const V *>(gate);
+  const V *u = reinterpret_cast<const V *>(up);
+  V *o = reinterpret_cast<V *>(output);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec; i += stride) {
+    V gv = g[i];
+    V uv = u[i];
+    V out;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float x = to_float(gv.v[e]);
+      const float silu = x / (1.0f + expf(-x));
+      out.v[e] = from_float<T>(silu * to_float(uv.v[e]));
+    }
+    o[i] = out;
+  }
+}
+
+template <typename T, int VEC, bool RESIDUAL>
+void launch_norm(const void *inputs, const void *residual, const void *weight,
+                 void *residual_output, void *output, int64_t rows, int32_t columns,
+                 float eps, hipStream_t stream) {
+  constexpr int kMaxVecs = max_vecs<VEC>();
+  const int32_t nvec = columns / VEC;
+  // Two vectors per lane where possible; the register cache holds kMaxVecs.
+  int threads = ((nvec + 1) / 2 + 63) / 64 * 64;
+  const int min_threads = ((nvec + kMaxVecs - 1) / kMaxVecs + 63) / 64 * 64;
+  if (threads < min_threads) threads = min_threads;
+  if (threads < 64) threads = 64;
+  if (threads > 1024) threads = 1024;
+  hipLaunchKernelGGL((rms_norm_kernel<T, VEC, RESIDUAL>), dim3(static_cast<unsigned>(rows)),
+                     dim3(threads), 0, stream, static_cast<const T *>(inputs),
+                     static_cast<const T *>(residual), static_cast<const T *>(weight),
+                     static_cast<T *>(residual_output), static_cast<T *>(output), columns, eps);
+}
+
+template <typename T, bool RESIDUAL>
+int32_t dispatch_norm(const void *inputs, const void *residual, const void *weight,
+                      void *residual_output, void *output, int64_t rows, int32_t columns,
+                      float eps, hipStream_t stream) {
+  constexpr int kVec = 16 / sizeof(T);
+  uintptr_t align = reinterpret_cast<uintptr_t>(inputs) | reinterpret_cast<uintptr_t>(weight) |
+                    reinterpret_cast<uintptr_t>(output);
+  if (RESIDUAL)
+    align |= reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(residual_output);
+  const bool vectorised = columns % kVec == 0 && align % 16 == 0 &&
+                          columns / kVec <= 1024 * max_vecs<kVec>();
+  if (vectorised) {
+    launch_norm<T, kVec, RESIDUAL>(inputs, residual, weight, residual_output, output, rows,
+                                   columns, eps, stream);
+  } else if (columns <= 1024 * max_vecs<1>()) {
+    launch_norm<T, 1, RESIDUAL>(inputs, residual, weight, residual_output, output, rows,
+                                columns, eps, stream);
+  } else {
+    return fail(TF_ERROR_UNSUPPORTED, "RMSNorm row does not fit the register cache");
+  }
+  return check_launch(RESIDUAL ? "residual_rms_norm" : "rms_norm");
+}
+
+template <bool RESIDUAL>
+int32_t norm_entry(const void *inputs, const void *residual, const void *weight,
+                   void *residual_output, void *output, int64_t rows, int32_t columns,
+                   float eps, int32_t dtype, void *stream) {
+  clear_error();
+  if (!valid_dtype(dtype)) return fail(TF_ERROR_INVALID_ARGUMENT, "unsupported dtype code");
+  if (rows < 0 || columns <= 0 || columns > 16384)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "RMSNorm needs 0 <= rows and 0 < columns <= 16384");
+  if (rows > 0x7fffffff) return fail(TF_ERROR_UNSUPPORTED, "too many rows for one launch");
+  if (!(eps > 0.f)) return fail(TF_ERROR_INVALID_ARGUMENT, "eps must be positive");
+  if (!inputs || !weight || !output || (RESIDUAL && (!residual || !residual_output)))
+    return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  if (rows == 0) return TF_SUCCESS;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TF_DTYPE_FLOAT32:
+      return dispatch_norm<float, RESIDUAL>(inputs, residual, weight, residual_output, output,
+                                            rows, columns, eps, s);
+    case TF_DTYPE_FLOAT16:
+      return dispatch_norm<_Float16, RESIDUAL>(inputs, residual, weight, residual_output,
+                                               output, rows, columns, eps, s);
+    default:
+      return dispatch_norm<__bf16, RESIDUAL>(inputs, residual, weight, residual_output, output,
+                                             rows, columns, eps, s);
+  }
+}
+
+template <typename T>
+int32_t swiglu_dispatch(const void *gate, const void *up, void *output, int64_t numel,
+                        hipStream_t stream) {
+  constexpr int kVec = 16 / sizeof(T);
+  const uintptr_t align = reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up) |
+                          reinterpret_cast<uintptr_t>(output);
+  const int threads = 256;
+  if (numel % kVec == 0 && align % 16 == 0) {
+    const int64_t nvec = numel / kVec;
+    int64_t blocks = (nvec + threads - 1) / threads;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL((swiglu_kernel<T, kVec>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(threads), 0, stream, static_cast<const T *>(gate),
+                       static_cast<const T *>(up), static_cast<T *>(output), nvec);
+  } else {
+    int64_t blocks = (numel + threads - 1) / threads;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL((swiglu_kernel<T, 1>), dim3(static_cast<unsigned>(blocks)), dim3(threads),
+                       0, stream, static_cast<const T *>(gate), static_cast<const T *>(up),
+                       static_cast<T *>(output), numel);
+  }
+  return check_launch("swiglu");
+}
+
+}  // namespace
+}  // namespace tf
+
+extern "C" int32_t tf_rms_norm(const void *inputs, const void *weight, void *output,
+                               int64_t rows, int32_t columns, float eps, int32_t dtype,
+                               void *stream) {
+  return tf::norm_entry<false>(inputs, nullptr, weight, nullptr, output, rows, columns, eps,
+                               dtype, stream);
+}
+
+extern "C" int32_t tf_residual_rms_norm(const void *inputs, const void *residual,
+                                        const void *weight, void *residual_output,
+                                        void *norm_output, int64_t rows, int32_t columns,
+                                        float eps, int32_t dtype, void *stream) {
+  return tf::norm_entry<true>(inputs, residual, weight, residual_output, norm_output, rows,
+                              columns, eps, dtype, stream);
+}
+
+extern "C" int32_t tf_swiglu(const void *gate, const void *up, void *output, int64_t numel,
+                             int32_t dtype, void *stream) {
+  using namespace tf;
+  clear_error();
+  if (!valid_dtype(dtype)) return fail(TF_ERROR_INVALID_ARGUMENT, "unsupported dtype code");
+  if (numel < 0) return fail(TF_ERROR_INVALID_ARGUMENT, "numel must be non-negative");
+  if (numel == 0) return TF_SUCCESS;
+  if (!gate || !up || !output) return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TF_DTYPE_FLOAT32:
+      return swiglu_dispatch<float>(gate, up, output, numel, s);
+    case TF_DTYPE_FLOAT16:
+      return swiglu_dispatch<_Float16>(gate, up, output, numel, s);
+    default:
+      return swiglu_dispatch<__bf16>(gate, up, output, numel, s);
+  }
+}

@@ -1,0 +1,315 @@
+"""Paged GQA decode attention over a paged KV cache, on gfx950 HIP kernels.
+
+Drop-in counterpart of ``tensorforge/kernels/triton_attention.py``: the
+public names, the call signature, the validation order, exception types and
+messages, the caller-owned ``output``/``workspace`` contract and the dispatch
+record are those of the reference (file:line cited per function).  The
+kernels behind it are the hand-written HIP kernels of
+``tensorforge_amd/csrc/tf_paged_attention.hip`` called through the C ABI on
+torch's current stream; nothing here synchronises with the device when
+``max_context_length`` is given, so a call can be captured in a HIP graph.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+from torch import Tensor
+
+from tensorforge_amd import _native
+
+# Tokens per split-KV partition (reference: triton_attention.py:46,406).  The
+# workspace capacity contract is sized for this value, so a smaller split
+# needs a workspace allocated for it.
+REFERENCE_SPLIT_SIZE = 256
+
+_SPLIT_SIZE = REFERENCE_SPLIT_SIZE
+_LAST_ATTENTION_CONFIG: dict[str, Any] | None = None
+_LAST_ATTENTION_LAUNCH: dict[str, Any] | None = None
+
+
+def _next_power_of_2(value: int) -> int:
+    return 1 << (value - 1).bit_length() if value > 1 else 1
+
+
+@dataclass(frozen=True, slots=True)
+class PagedAttentionWorkspace:
+    """Caller-owned split-KV buffers whose addresses can remain graph-stable.
+
+    Same fields and capacity rule as ``triton_attention.py:25-57``: buffers
+    hold ``batch_capacity * query_heads * ceil(max_context_length / 256)``
+    fp32 partial rows, accumulator rows padded to ``next_pow2(head_dim)``.
+    """
+
+    partial_max: Tensor
+    partial_sum: Tensor
+    partial_accumulator: Tensor
+
+    @classmethod
+    def allocate(
+        cls,
+        *,
+        batch_capacity: int,
+        query_heads: int,
+        head_dim: int,
+        max_context_length: int,
+        device: torch.device,
+    ) -> PagedAttentionWorkspace:
+        dimensions = (batch_capacity, query_heads, head_dim, max_context_length)
+        if any(value <= 0 for value in dimensions):
+            raise ValueError("workspace dimensions must be positive")
+        num_splits = (max_context_length + REFERENCE_SPLIT_SIZE - 1) // REFERENCE_SPLIT_SIZE
+        programs = batch_capacity * query_heads * num_splits
+        head_bucket = _next_power_of_2(head_dim)
+        partial_max = torch.empty(programs, device=device, dtype=torch.float32)
+        return cls(
+            partial_max=partial_max,
+            partial_sum=torch.empty_like(partial_max),
+            partial_accumulator=torch.empty(
+                (programs, head_bucket), device=device, dtype=torch.float32
+            ),
+        )
+
+
+def is_hip_attention_available() -> bool:
+    """True when the gfx950 attention library is built and loadable."""
+
+    return _native.is_available()
+
+
+def set_attention_split_size(split_size: int) -> int:
+    """Set the split-KV partition size (tokens) and return the previous one.
+
+    Must be a positive multiple of 32.  Sizes below 256 need a workspace
+    allocated with at least ``ceil(context / split_size)`` partials per head.
+    """
+
+    global _SPLIT_SIZE
+    if split_size <= 0 or split_size % 32 != 0:
+        raise ValueError("split_size must be a positive multiple of 32")
+    previous = _SPLIT_SIZE
+    _SPLIT_SIZE = split_size
+    return previous
+
+
+def attention_split_size() -> int:
+    return _SPLIT_SIZE
+
+
+def paged_gqa_decode_attention(
+    query: Tensor,
+    key_cache: Tensor,
+    value_cache: Tensor,
+    block_tables: Tensor,
+    context_lengths: Tensor,
+    *,
+    scale: float | None = None,
+    max_context_length: int | None = None,
+    output: Tensor | None = None,
+    workspace: PagedAttentionWorkspace | None = None,
+    attention_path: str = "auto",
+) -> Tensor:
+    """Attend one query token per sequence over logically ordered physical KV pages.
+
+    Mirrors ``triton_attention.py:326-518``.  Differences, all on inputs the
+    reference leaves undefined: rows with ``context_lengths <= 0`` produce
+    zeros (reference: 0/0); tokens whose block-table entry lies outside the
+    cache are skipped instead of read out of bounds.
+    """
+
+    global _LAST_ATTENTION_CONFIG, _LAST_ATTENTION_LAUNCH
+    if not _native.is_available():
+        raise RuntimeError(
+            "the gfx950 attention library is unavailable; build it with "
+            "`python -m tensorforge_amd.build`"
+        )
+    tensors = (query, key_cache, value_cache, block_tables, context_lengths)
+    if any(not tensor.is_cuda for tensor in tensors):
+        raise ValueError("paged GQA attention requires CUDA tensors")
+    if any(not tensor.is_contiguous() for tensor in tensors):
+        raise ValueError("paged GQA attention requires contiguous tensors")
+    if query.ndim != 3:
+        raise ValueError("query must have shape [batch, query_heads, head_dim]")
+    if key_cache.ndim != 4 or value_cache.shape != key_cache.shape:
+        raise ValueError("key/value cache must share [blocks, block_size, kv_heads, head_dim]")
+    if query.dtype not in _native.DTYPE_CODES:
+        raise TypeError(f"unsupported query dtype: {query.dtype}")
+    if key_cache.dtype != query.dtype or value_cache.dtype != query.dtype:
+        raise ValueError("query, key cache, and value cache must share dtype")
+    if block_tables.dtype != torch.int32 or context_lengths.dtype != torch.int32:
+        raise TypeError("block tables and context lengths must use torch.int32")
+    batch, query_heads, head_dim = query.shape
+    num_blocks, block_size, kv_heads, cache_head_dim = key_cache.shape
+    if head_dim != cache_head_dim or query_heads % kv_heads != 0:
+        raise ValueError("query/cache head dimensions do not form valid GQA groups")
+    if head_dim > 256:
+        raise ValueError("decode attention supports head dimensions up to 256")
+    if block_tables.ndim != 2 or block_tables.shape[0] != batch:
+        raise ValueError("block_tables must have one row per query")
+    if context_lengths.shape != (batch,):
+        raise ValueError("context_lengths must have one value per query")
+    if query.requires_grad and torch.is_grad_enabled():
+        raise RuntimeError("TensorForge HIP kernels are inference-only")
+    if attention_path not in {"auto", "one_pass", "split_kv"}:
+        raise ValueError("attention_path must be auto, one_pass, or split_kv")
+
+    table_width = block_tables.shape[1]
+    context_capacity = table_width * block_size
+    if max_context_length is None:
+        # Host synchronisation, as in the reference (:375); give a bucket to
+        # keep the call capture-safe.
+        launch_context = int(context_lengths.max().item()) if batch > 0 else 0
+        if launch_context <= 0:
+            raise ValueError("context lengths must be positive")
+    else:
+        launch_context = max_context_length
+    if launch_context <= 0 or launch_context > context_capacity:
+        raise ValueError("max_context_length must be positive and within table capacity")
+    head_bucket = _next_power_of_2(head_dim)
+    if output is None:
+        output = torch.empty_like(query)
+    elif (
+        output.shape != query.shape
+        or output.dtype != query.dtype
+        or output.device != query.device
+        or not output.is_contiguous()
+    ):
+        raise ValueError("output must be contiguous and share query shape, dtype, and device")
+    attention_scale = head_dim**-0.5 if scale is None else scale
+
+    split_size = _SPLIT_SIZE
+    use_split_kv = attention_path == "split_kv" or (
+        attention_path == "auto" and launch_context > split_size
+    )
+    dtype = _native.dtype_code(query.dtype)
+    group = query_heads // kv_heads
+    variant = _native.library().tf_paged_gqa_decode_variant(dtype, head_dim, group, 0)
+    kernel = "mfma" if variant == _native.TF_ATTENTION_MFMA else "generic"
+    device = query.device
+    stream = _native.current_stream(device)
+    if use_split_kv:
+        num_splits = (launch_context + split_size - 1) // split_size
+        partial_programs = batch * query_heads * num_splits
+        if workspace is None:
+            workspace = PagedAttentionWorkspace.allocate(
+                batch_capacity=max(batch, 1),
+                query_heads=query_heads,
+                head_dim=head_dim,
+                max_context_length=num_splits * REFERENCE_SPLIT_SIZE,
+                device=device,
+            )
+        if (
+            workspace.partial_max.device != device
+            or workspace.partial_sum.device != device
+            or workspace.partial_accumulator.device != device
+            or workspace.partial_max.dtype != torch.float32
+            or workspace.partial_sum.dtype != torch.float32
+            or workspace.partial_accumulator.dtype != torch.float32
+            or workspace.partial_max.numel() < partial_programs
+            or workspace.partial_sum.numel() < partial_programs
+            or workspace.partial_accumulator.shape[0] < partial_programs
+            or workspace.partial_accumulator.shape[1] != head_bucket
+            or not workspace.partial_max.is_contiguous()
+            or not workspace.partial_sum.is_contiguous()
+            or not workspace.partial_accumulator.is_contiguous()
+        ):
+            raise ValueError("split-KV workspace has insufficient or incompatible capacity")
+        capacity = min(
+            workspace.partial_max.numel(),
+            workspace.partial_sum.numel(),
+            workspace.partial_accumulator.shape[0],
+        )
+        _native.check(
+            _native.library().tf_paged_gqa_decode(
+                query.data_ptr(),
+                key_cache.data_ptr(),
+                value_cache.data_ptr(),
+                block_tables.data_ptr(),
+                context_lengths.data_ptr(),
+                output.data_ptr(),
+                workspace.partial_max.data_ptr(),
+                workspace.partial_sum.data_ptr(),
+                workspace.partial_accumulator.data_ptr(),
+                capacity,
+                head_bucket,
+                batch,
+                query_heads,
+                kv_heads,
+                head_dim,
+                num_blocks,
+                block_size,
+                table_width,
+                split_size,
+                num_splits,
+                attention_scale,
+                dtype,
+                0,
+                stream,
+            ),
+            "paged_gqa_decode_attention",
+        )
+        _LAST_ATTENTION_CONFIG = {
+            "path": "split_kv",
+            "split_size": split_size,
+            "num_splits": num_splits,
+        }
+    else:
+        # One partition spanning the whole table: every present token of a
+        # row is visited by one workgroup per (row, kv head).
+        one_pass_size = (context_capacity + 31) // 32 * 32
+        num_splits = 1
+        _native.check(
+            _native.library().tf_paged_gqa_decode(
+                query.data_ptr(),
+                key_cache.data_ptr(),
+                value_cache.data_ptr(),
+                block_tables.data_ptr(),
+                context_lengths.data_ptr(),
+                output.data_ptr(),
+                None,
+                None,
+                None,
+                0,
+                head_bucket,
+                batch,
+                query_heads,
+                kv_heads,
+                head_dim,
+                num_blocks,
+                block_size,
+                table_width,
+                one_pass_size,
+                1,
+                attention_scale,
+                dtype,
+                0,
+                stream,
+            ),
+            "paged_gqa_decode_attention",
+        )
+        _LAST_ATTENTION_CONFIG = {
+            "path": "one_pass",
+            "kernel": kernel,
+            "workgroup": "sequence x kv_head",
+        }
+    _LAST_ATTENTION_LAUNCH = {
+        "kernel": kernel,
+        "grid": (num_splits, kv_heads, batch),
+        "group_size": group,
+        "launch_context": launch_context,
+    }
+    return output
+
+
+def selected_attention_autotune_config() -> dict[str, Any] | None:
+    """Dispatch record of the last call (reference: triton_attention.py:521-522)."""
+
+    return _LAST_ATTENTION_CONFIG
+
+
+def selected_attention_launch() -> dict[str, Any] | None:
+    """Kernel family and grid of the last call (no reference counterpart)."""
+
+    return _LAST_ATTENTION_LAUNCH

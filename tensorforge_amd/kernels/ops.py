@@ -1,0 +1,236 @@
+"""RMSNorm, fused residual RMSNorm and SwiGLU on gfx950 HIP kernels.
+
+Drop-in counterpart of ``tensorforge/kernels/triton_ops.py``: same names,
+signatures, validation order, exception types and messages
+(``:129-176``), caller-owned outputs returned by identity, and the
+``selected_autotune_config`` / ``autotune_cache_size`` observability hooks
+(``:263-295``).  The kernels are in ``csrc/tf_fused_ops.hip``.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+from torch import Tensor
+
+from tensorforge_amd import _native
+
+_OPERATIONS = ("rms_norm", "residual_rms_norm", "swiglu")
+# Launch shapes chosen per (operation, rows, columns, dtype), kept as the
+# observable equivalent of the reference's autotune cache.
+_LAUNCH_CACHE: dict[str, dict[tuple[Any, ...], dict[str, Any]]] = {
+    name: {} for name in _OPERATIONS
+}
+_LAST_CONFIG: dict[str, dict[str, Any] | None] = {name: None for name in _OPERATIONS}
+
+
+def is_hip_available() -> bool:
+    return _native.is_available()
+
+
+def _require_library() -> None:
+    if not _native.is_available():
+        raise RuntimeError(
+            "the gfx950 kernel library is unavailable; build it with "
+            "`python -m tensorforge_amd.build`"
+        )
+
+
+def _validate_common(inputs: Tensor, weight: Tensor | None = None) -> None:
+    if not inputs.is_cuda:
+        raise ValueError("HIP kernels require CUDA tensors")
+    if inputs.dtype not in _native.DTYPE_CODES:
+        raise TypeError(f"unsupported dtype: {inputs.dtype}")
+    if inputs.numel() == 0 or inputs.ndim == 0:
+        raise ValueError("inputs must be a non-empty tensor with a hidden dimension")
+    if not inputs.is_contiguous():
+        raise ValueError("inputs must be contiguous")
+    if inputs.requires_grad and torch.is_grad_enabled():
+        raise RuntimeError("TensorForge HIP kernels are inference-only")
+    if weight is not None:
+        if weight.shape != (inputs.shape[-1],):
+            raise ValueError("weight must match the final input dimension")
+        if weight.device != inputs.device or weight.dtype != inputs.dtype:
+            raise ValueError("weight must share input device and dtype")
+        if not weight.is_contiguous():
+            raise ValueError("weight must be contiguous")
+
+
+def _norm_launch_shape(inputs: Tensor) -> tuple[int, int]:
+    columns = inputs.shape[-1]
+    if columns > 16_384:
+        raise ValueError("single-program RMSNorm supports at most 16,384 columns")
+    return inputs.numel() // columns, columns
+
+
+def _output_or_empty(output: Tensor | None, reference: Tensor, name: str) -> Tensor:
+    if output is None:
+        return torch.empty_like(reference)
+    if (
+        output.shape != reference.shape
+        or output.dtype != reference.dtype
+        or output.device != reference.device
+        or not output.is_contiguous()
+    ):
+        raise ValueError(f"{name} must be contiguous and share input shape, dtype, and device")
+    return output
+
+
+def _norm_config(columns: int, dtype: torch.dtype, aligned: bool) -> dict[str, Any]:
+    vector = 16 // torch.empty((), dtype=dtype).element_size()
+    vectorised = aligned and columns % vector == 0
+    width = vector if vectorised else 1
+    per_lane = 8 if vectorised else 16
+    units = columns // width
+    threads = max(((units + 1) // 2 + 63) // 64 * 64, ((units + per_lane - 1) // per_lane + 63) // 64 * 64, 64)
+    threads = min(threads, 1024)
+    return {"kwargs": {"VECTOR": width}, "num_warps": threads // 64, "wave_size": 64}
+
+
+def _record(operation: str, key: tuple[Any, ...], config: dict[str, Any]) -> None:
+    _LAUNCH_CACHE[operation].setdefault(key, config)
+    _LAST_CONFIG[operation] = config
+
+
+def _aligned(*tensors: Tensor) -> bool:
+    return all(tensor.data_ptr() % 16 == 0 for tensor in tensors)
+
+
+def rms_norm(
+    inputs: Tensor,
+    weight: Tensor,
+    eps: float = 1e-6,
+    *,
+    output: Tensor | None = None,
+) -> Tensor:
+    """RMSNorm over the last dimension (reference: triton_ops.py:179-205)."""
+
+    _require_library()
+    _validate_common(inputs, weight)
+    if eps <= 0:
+        raise ValueError("eps must be positive")
+    rows, columns = _norm_launch_shape(inputs)
+    output = _output_or_empty(output, inputs, "output")
+    _native.check(
+        _native.library().tf_rms_norm(
+            inputs.data_ptr(),
+            weight.data_ptr(),
+            output.data_ptr(),
+            rows,
+            columns,
+            eps,
+            _native.dtype_code(inputs.dtype),
+            _native.current_stream(inputs.device),
+        ),
+        "rms_norm",
+    )
+    _record(
+        "rms_norm",
+        (rows, columns, inputs.dtype),
+        _norm_config(columns, inputs.dtype, _aligned(inputs, weight, output)),
+    )
+    return output
+
+
+def residual_rms_norm(
+    inputs: Tensor,
+    residual: Tensor,
+    weight: Tensor,
+    eps: float = 1e-6,
+    *,
+    residual_output: Tensor | None = None,
+    norm_output: Tensor | None = None,
+) -> tuple[Tensor, Tensor]:
+    """Fuse residual addition and RMSNorm (reference: triton_ops.py:208-243).
+
+    ``residual_output`` is the rounded sum; the norm is taken of the fp32 sum
+    (the reference kernel's semantics, triton_ops.py:89-97).
+    """
+
+    _require_library()
+    _validate_common(inputs, weight)
+    _validate_common(residual)
+    if residual.shape != inputs.shape or residual.dtype != inputs.dtype:
+        raise ValueError("residual must share input shape and dtype")
+    if residual.device != inputs.device:
+        raise ValueError("residual must share input device")
+    if eps <= 0:
+        raise ValueError("eps must be positive")
+    rows, columns = _norm_launch_shape(inputs)
+    residual_output = _output_or_empty(residual_output, inputs, "residual_output")
+    norm_output = _output_or_empty(norm_output, inputs, "norm_output")
+    _native.check(
+        _native.library().tf_residual_rms_norm(
+            inputs.data_ptr(),
+            residual.data_ptr(),
+            weight.data_ptr(),
+            residual_output.data_ptr(),
+            norm_output.data_ptr(),
+            rows,
+            columns,
+            eps,
+            _native.dtype_code(inputs.dtype),
+            _native.current_stream(inputs.device),
+        ),
+        "residual_rms_norm",
+    )
+    _record(
+        "residual_rms_norm",
+        (rows, columns, inputs.dtype),
+        _norm_config(
+            columns,
+            inputs.dtype,
+            _aligned(inputs, residual, weight, residual_output, norm_output),
+        ),
+    )
+    return residual_output, norm_output
+
+
+def swiglu(gate: Tensor, up: Tensor, *, output: Tensor | None = None) -> Tensor:
+    """Fuse SiLU and gating after the two projections (reference: triton_ops.py:246-260)."""
+
+    _require_library()
+    _validate_common(gate)
+    _validate_common(up)
+    if up.shape != gate.shape or up.dtype != gate.dtype or up.device != gate.device:
+        raise ValueError("gate and up tensors must share shape, dtype, and device")
+    output = _output_or_empty(output, gate, "output")
+    numel = gate.numel()
+    _native.check(
+        _native.library().tf_swiglu(
+            gate.data_ptr(),
+            up.data_ptr(),
+            output.data_ptr(),
+            numel,
+            _native.dtype_code(gate.dtype),
+            _native.current_stream(gate.device),
+        ),
+        "swiglu",
+    )
+    vector = 16 // gate.element_size()
+    width = vector if numel % vector == 0 and _aligned(gate, up, output) else 1
+    blocks = min((numel // width + 255) // 256, 8192)
+    _record(
+        "swiglu",
+        (numel, gate.dtype),
+        {"kwargs": {"BLOCK_SIZE": 256 * width, "VECTOR": width, "BLOCKS": blocks},
+         "num_warps": 4, "wave_size": 64},
+    )
+    return output
+
+
+def selected_autotune_config(operation: str) -> dict[str, Any] | None:
+    """Most recent launch configuration of ``operation`` (reference: triton_ops.py:263-283)."""
+
+    if operation not in _LAST_CONFIG:
+        raise ValueError(f"unknown operation: {operation}")
+    return _LAST_CONFIG[operation]
+
+
+def autotune_cache_size(operation: str) -> int:
+    """Number of distinct launch shapes seen (reference: triton_ops.py:286-295)."""
+
+    if operation not in _LAUNCH_CACHE:
+        raise ValueError(f"unknown operation: {operation}")
+    return len(_LAUNCH_CACHE[operation])
