@@ -48,12 +48,23 @@ enum tf_status {
 
 /* Attention kernel families (tf_paged_gqa_decode_variant). */
 enum tf_attention_variant {
-  TF_ATTENTION_GENERIC = 0, /* any dtype, head_dim <= 256, group <= 64     */
-  TF_ATTENTION_MFMA = 1     /* bf16/fp16, head_dim in {32,64,128}, group<=16 */
+  TF_ATTENTION_GENERIC = 0, /* any dtype, head_dim <= 256, group <= 64,
+                               any block size                              */
+  TF_ATTENTION_MFMA = 1     /* bf16/fp16, head_dim in {32,64,128},
+                               group <= 16, block_size % 16 == 0, and
+                               split_size % 32 == 0 when num_splits > 1    */
 };
 
-/* tf_paged_gqa_decode* flags. */
+/* tf_paged_gqa_decode* flags.  With split_counters and the MFMA family the
+ * split stage is a balanced streaming kernel (equal contiguous token ranges
+ * per wavefront); FORCE_GRID selects the one-workgroup-per-split kernel
+ * instead.  Bits 8-15: streaming wavefronts per compute unit; bits 16-19:
+ * chunks in flight per streaming wavefront (2, 3, 4, 6 or 8); 0 selects the
+ * defaults. */
 #define TF_ATTENTION_FLAG_FORCE_GENERIC 1
+#define TF_ATTENTION_FLAG_FORCE_GRID 2
+#define TF_ATTENTION_WAVES_PER_CU_SHIFT 8
+#define TF_ATTENTION_DEPTH_SHIFT 16
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char *tf_last_error(void);
@@ -61,9 +72,11 @@ const char *tf_last_error(void);
 /* Version of this ABI; bumped on any signature change. */
 int32_t tf_abi_version(void);
 
-/* Which kernel family tf_paged_gqa_decode uses for these parameters. */
+/* Which kernel family tf_paged_gqa_decode uses for these parameters
+ * (a split_size that is not a multiple of 32 also selects the generic one). */
 int32_t tf_paged_gqa_decode_variant(int32_t dtype, int32_t head_dim,
-                                    int32_t group_size, int32_t flags);
+                                    int32_t group_size, int32_t block_size,
+                                    int32_t flags);
 
 /*
  * Paged GQA decode attention: one query token per sequence.
@@ -81,13 +94,19 @@ int32_t tf_paged_gqa_decode_variant(int32_t dtype, int32_t head_dim,
  * (b * query_heads + h) * num_splits + s (partial_accumulator rows are
  * partial_row_stride floats apart) and merged by log-sum-exp; partial_capacity
  * is the number of partial rows the buffers hold.  scale multiplies q.k.
+ * split_counters: NULL, or batch * kv_heads int32 counters that are zero
+ * before the first call.  With counters the last workgroup of each
+ * (row, kv head) merges the partials inside the split kernel (one launch)
+ * and returns its counter to zero; without them a merge kernel follows.
+ * Calls sharing partial buffers or counters must not overlap in time.
  * Replaces triton_attention.py:326-518.
  */
 int32_t tf_paged_gqa_decode(
     const void *query, const void *key_cache, const void *value_cache,
     const int32_t *block_tables, const int32_t *context_lengths, void *output,
     float *partial_max, float *partial_sum, float *partial_accumulator,
-    int64_t partial_capacity, int32_t partial_row_stride, int32_t batch,
+    int32_t *split_counters, int64_t partial_capacity, int32_t partial_row_stride,
+    int32_t batch,
     int32_t query_heads, int32_t kv_heads, int32_t head_dim,
     int32_t num_blocks, int32_t block_size, int32_t table_width,
     int32_t split_size, int32_t num_splits, float scale, int32_t dtype,

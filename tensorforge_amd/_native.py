@@ -23,6 +23,9 @@ TF_DTYPE_BFLOAT16 = 2
 TF_ATTENTION_GENERIC = 0
 TF_ATTENTION_MFMA = 1
 TF_ATTENTION_FLAG_FORCE_GENERIC = 1
+TF_ATTENTION_FLAG_FORCE_GRID = 2
+TF_ATTENTION_WAVES_PER_CU_SHIFT = 8
+TF_ATTENTION_DEPTH_SHIFT = 16
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: TF_DTYPE_FLOAT32,
@@ -39,10 +42,10 @@ _f32 = ctypes.c_float
 SIGNATURES: dict[str, tuple[Any, ...]] = {
     "tf_last_error": (),
     "tf_abi_version": (),
-    "tf_paged_gqa_decode_variant": (_i32, _i32, _i32, _i32),
+    "tf_paged_gqa_decode_variant": (_i32, _i32, _i32, _i32, _i32),
     "tf_paged_gqa_decode": (
         _p, _p, _p, _p, _p, _p,  # query, key/value cache, tables, lengths, output
-        _p, _p, _p, _i64, _i32,  # partials, capacity, row stride
+        _p, _p, _p, _p, _i64, _i32,  # partials, counters, capacity, row stride
         _i32, _i32, _i32, _i32,  # batch, query heads, kv heads, head dim
         _i32, _i32, _i32,  # num blocks, block size, table width
         _i32, _i32, _f32, _i32, _i32, _p,  # split size, splits, scale, dtype, flags, stream

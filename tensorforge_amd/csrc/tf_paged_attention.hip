@@ -48,6 +48,10 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
 
+// 2^x with the native v_exp_f32 (results below 2^-126 flush to zero, which
+// is harmless for softmax weights; exp2(-inf) = 0).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 struct AttnParams {
   const void *query;
   const void *key_cache;
@@ -58,6 +62,7 @@ struct AttnParams {
   float *partial_max;
   float *partial_sum;
   float *partial_acc;
+  int32_t *split_counters;  // per (row, kv head) arrival counters, or null
   int32_t batch;
   int32_t query_heads;
   int32_t kv_heads;
@@ -99,35 +104,122 @@ __device__ __forceinline__ int64_t token_offset(const AttnParams &p, const int32
          static_cast<int64_t>(p.kv_heads) * p.head_dim;
 }
 
-// Write the finished (max, sum, numerator) of one (row, query head) either
-// as the final output (one split) or as a partial.
-template <typename T>
-__device__ __forceinline__ void store_result(const AttnParams &p, int32_t b, int32_t qh,
-                                             int32_t split, int32_t d, float m, float l,
-                                             float num) {
-  if (p.num_splits == 1) {
-    const float o = l > 0.f ? num / l : 0.f;
-    static_cast<T *>(p.output)[(static_cast<int64_t>(b) * p.query_heads + qh) * p.head_dim + d] =
-        from_float<T>(o);
-  } else {
-    const int64_t row = (static_cast<int64_t>(b) * p.query_heads + qh) * p.num_splits + split;
-    p.partial_acc[row * p.partial_stride + d] = num;
-    if (d == 0) {
-      p.partial_max[row] = m;
-      p.partial_sum[row] = l;
-    }
-  }
+// True when no separate merge launch follows the split stage: one pass, or
+// split mode with arrival counters (the last workgroup of a row merges).
+__device__ __forceinline__ bool writes_output(const AttnParams &p) {
+  return p.num_splits == 1 || p.split_counters != nullptr;
 }
 
-// Rows of length zero get zeros in one-pass mode (the merge kernel handles
-// them in split mode).
+// Rows of length zero produce zeros, written by their split-0 workgroup
+// whenever no merge launch follows.
 template <typename T>
 __device__ void zero_rows(const AttnParams &p, int32_t b, int32_t kvh) {
-  if (p.num_splits != 1) return;
+  if (!writes_output(p)) return;
   T *out = static_cast<T *>(p.output) +
            (static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(kvh) * p.group) *
                p.head_dim;
   for (int i = threadIdx.x; i < p.group * p.head_dim; i += blockDim.x) out[i] = from_float<T>(0.f);
+}
+
+template <typename T>
+__device__ __forceinline__ T *output_row(const AttnParams &p, int32_t b, int32_t qh) {
+  return static_cast<T *>(p.output) + (static_cast<int64_t>(b) * p.query_heads + qh) * p.head_dim;
+}
+
+// Epilogue shared by both kernel families.  Every thread of the workgroup
+// calls it; thread t owns items idx = t + k * blockDim.x (k < MAXK) of the
+// group x head_dim result, and value_of(k, idx, m, l, num) yields the
+// workgroup's base-2 max, sum and unnormalised numerator for that item.
+//
+//  * one pass, or a row with a single non-empty split in counter mode:
+//    write num / l to the output directly;
+//  * otherwise store the partial; in counter mode the workgroup then counts
+//    itself in and the last of the row's ceil(ctx / split_size) workgroups
+//    merges all partials of its (row, kv head) by log-sum-exp and resets the
+//    counter to zero, leaving it ready for the next call (no memset, so the
+//    call is graph-replay safe).
+//
+// Cross-workgroup visibility without cache maintenance: partials are written
+// with agent-scope atomic stores, which on gfx950 write through the per-XCD
+// L2 to the coherent memory side; the workgroup waits for those stores to
+// complete before its single counter increment (an agent-scope atomic), and
+// the last workgroup reads the partials back with agent-scope atomic loads,
+// which bypass the non-coherent caches.  No agent-scope fence is issued: on a
+// multi-XCD part such a fence writes back and invalidates the whole L2.
+template <typename T, int MAXK, typename F>
+__device__ __forceinline__ void finish(const AttnParams &p, int32_t b, int32_t kvh,
+                                       int32_t split, int32_t ctx, F value_of) {
+  const int G = p.group;
+  const int D = p.head_dim;
+  const int32_t nvalid = (ctx + p.split_size - 1) / p.split_size;
+  const bool counters = p.num_splits > 1 && p.split_counters != nullptr;
+  const bool direct = p.num_splits == 1 || (counters && nvalid == 1);
+#pragma unroll
+  for (int k = 0; k < MAXK; ++k) {
+    const int idx = threadIdx.x + k * blockDim.x;
+    if (idx < G * D) {
+      float m, l, num;
+      value_of(k, idx, m, l, num);
+      const int g = idx / D;
+      const int d = idx - g * D;
+      const int32_t qh = kvh * G + g;
+      if (direct) {
+        output_row<T>(p, b, qh)[d] = from_float<T>(l > 0.f ? num / l : 0.f);
+      } else {
+        const int64_t row = (static_cast<int64_t>(b) * p.query_heads + qh) * p.num_splits + split;
+        if (counters) {
+          __hip_atomic_store(p.partial_acc + row * p.partial_stride + d, num, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+          if (d == 0) {
+            __hip_atomic_store(p.partial_max + row, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p.partial_sum + row, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        } else {
+          p.partial_acc[row * p.partial_stride + d] = num;
+          if (d == 0) {
+            p.partial_max[row] = m;
+            p.partial_sum[row] = l;
+          }
+        }
+      }
+    }
+  }
+  if (!counters || direct) return;
+
+  __shared__ int32_t is_last;
+  __builtin_amdgcn_s_waitcnt(0);  // this lane's partial stores have completed
+  __syncthreads();                // ... and so have every other lane's
+  if (threadIdx.x == 0) {
+    int32_t *counter = p.split_counters + static_cast<int64_t>(b) * p.kv_heads + kvh;
+    const int32_t prev =
+        __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == nvalid - 1;
+    if (is_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+    const int g = idx / D;
+    const int d = idx - g * D;
+    const int32_t qh = kvh * G + g;
+    const int64_t base = (static_cast<int64_t>(b) * p.query_heads + qh) * p.num_splits;
+    float gmax = kNegInf;
+    for (int32_t s = 0; s < nvalid; ++s)
+      gmax = fmaxf(gmax, __hip_atomic_load(p.partial_max + base + s, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT));
+    float num = 0.f, den = 0.f;
+    if (gmax != kNegInf) {
+      for (int32_t s = 0; s < nvalid; ++s) {
+        const float e = exp2f(__hip_atomic_load(p.partial_max + base + s, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT) - gmax);
+        den += e * __hip_atomic_load(p.partial_sum + base + s, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        num += e * __hip_atomic_load(p.partial_acc + (base + s) * p.partial_stride + d,
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    output_row<T>(p, b, qh)[d] = from_float<T>(den > 0.f ? num / den : 0.f);
+  }
 }
 
 // ===========================================================================
@@ -139,7 +231,6 @@ struct Mfma;
 template <>
 struct Mfma<__bf16> {
   typedef __bf16 vec8 __attribute__((ext_vector_type(8)));
-  typedef __bf16 vec4 __attribute__((ext_vector_type(4)));
   static __device__ __forceinline__ f32x4 mma(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
@@ -148,55 +239,87 @@ struct Mfma<__bf16> {
 template <>
 struct Mfma<_Float16> {
   typedef _Float16 vec8 __attribute__((ext_vector_type(8)));
-  typedef _Float16 vec4 __attribute__((ext_vector_type(4)));
   static __device__ __forceinline__ f32x4 mma(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
 
-constexpr int kChunk = 32;             // tokens per wavefront step (two 16-row tiles)
-constexpr int kVtStride = kChunk + 4;  // LDS row of the transposed V tile (elements)
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+constexpr int kChunk = 32;  // tokens per wavefront step (two 16-row tiles)
+
+// LDS row of the staged V tile: head_dim elements plus 16 bytes, which
+// staggers the rows of one transpose read over the banks.
+template <int D>
+constexpr int v_row_bytes() { return D * 2 + 16; }
 
 template <int D, int NW>
 constexpr int mfma_lds_bytes() {
-  // max(transposed V tiles, cross-wave merge buffers for 16 heads)
-  return (NW * D * kVtStride * 2) > (NW * (16 * D + 32) * 4) ? (NW * D * kVtStride * 2)
-                                                             : (NW * (16 * D + 32) * 4);
+  // max(per-wave V tiles, cross-wave merge buffers for 16 heads)
+  return (NW * kChunk * v_row_bytes<D>()) > (NW * (16 * D + 32) * 4)
+             ? (NW * kChunk * v_row_bytes<D>())
+             : (NW * (16 * D + 32) * 4);
 }
 
-template <typename T, int D, int NW, bool UNIFORM_PAGE>
+// Rescale threshold of the lazy online softmax (base-2 units): the running
+// max of a head is only raised -- and the accumulator rescaled -- when a
+// score exceeds it by more than this, so weights stay below 2^8 and the
+// rescale (with its cross-lane max) runs a handful of times per split.
+constexpr float kRescaleThreshold = 8.f;
+constexpr int kSegmentTiles = 64;  // page-window capacity: 64 tiles = 1024 tokens
+
+// Wave-level layout of one 32-token chunk (tiles j = 0, 1 of 16 tokens):
+//   loads    lane (l16, q4) holds K/V of token 16j + l16, head_dim elements
+//            [32ks + 8q4, +8) -- the A operand of the score MFMA;
+//   scores   lane holds S[token 16j + 4q4 + r][head l16], r = 0..3;
+//   P        B operand of the P.V MFMA, k = 8q4 + i <-> token 4q4 + i of
+//            tile 0 (i < 4) or 4q4 + i - 4 of tile 1 (i >= 4);
+//   V^T      A operand of the P.V MFMA (row = dim 16n + l16, same k order),
+//            produced by ds_read_b64_tr_b16 from V staged token-major: in a
+//            16-lane group, lane jj addresses the 4 elements
+//            V[4q4 + jj/4][16n + 4(jj%4) .. +4] and lane i receives
+//            V[4q4 + e][16n + i] for e = 0..3.
+// Requires block_size % 16 == 0 and split_size % 32 == 0 (a tile never
+// straddles a page), so each tile's page is wave-uniform.
+template <typename T, int D, int NW>
 __global__ void __launch_bounds__(NW * 64)
 paged_decode_mfma_kernel(AttnParams p) {
   using M = Mfma<T>;
   using vec8 = typename M::vec8;
-  using vec4 = typename M::vec4;
   constexpr int KS = D / 32;  // k-steps of the score product
   constexpr int NB = D / 16;  // 16-dim blocks of the output
+  constexpr int kRow = v_row_bytes<D>();
   __shared__ __attribute__((aligned(16))) unsigned char lds[mfma_lds_bytes<D, NW>()];
 
-  const int32_t split = blockIdx.x;
-  const int32_t kvh = blockIdx.y;
-  const int32_t b = blockIdx.z;
+  // blockIdx.x enumerates (row, kv head) so that consecutive workgroups --
+  // which the dispatcher deals round-robin to the 8 XCDs -- belong to
+  // different rows; the split index is the slow dimension.
+  const int32_t b = blockIdx.x / p.kv_heads;
+  const int32_t kvh = blockIdx.x - b * p.kv_heads;
+  const int32_t split = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l16 = lane & 15;
   const int q4 = lane >> 4;
-
-  const int32_t ctx = clamp_context(p, b);
   const int32_t s0 = split * p.split_size;
-  if (s0 >= ctx) {
-    if (split == 0) zero_rows<T>(p, b, kvh);
-    return;
-  }
-  const int32_t s1 = min(s0 + p.split_size, ctx);
-  const int32_t nchunks = (s1 - s0 + kChunk - 1) / kChunk;
+  const int32_t *table = p.block_tables + static_cast<int64_t>(b) * p.table_width;
 
-  // Query group as the B operand: lane holds q[head l16][32ks + 8q4 .. +8].
-  vec8 qf[KS];
+  // Page ids of up to 64 tiles starting at `first` (lane i: tile first + i).
+  auto load_window = [&](int32_t first) -> int32_t {
+    const int32_t t = s0 + 16 * (first + lane);
+    const int32_t logical = p.page_shift >= 0 ? (t >> p.page_shift) : (t / p.block_size);
+    return logical < p.table_width ? table[logical] : -1;
+  };
+
+  // Independent start-up loads: row length, query group, first page window.
+  const int32_t ctx = clamp_context(p, b);
+  vec8 qf[KS];  // B operand of the score MFMA: q[head l16][32ks + 8q4 .. +8]
   {
     const T *qrow = static_cast<const T *>(p.query) +
-                    (static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(kvh) * p.group +
-                     l16) * D;
+                    (static_cast<int64_t>(b) * p.query_heads +
+                     static_cast<int64_t>(kvh) * p.group + l16) * D;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (l16 < p.group)
@@ -205,153 +328,151 @@ paged_decode_mfma_kernel(AttnParams p) {
         qf[ks] = vec8{};
     }
   }
+  int32_t page_win = load_window(0);
 
-  const int32_t *table = p.block_tables + static_cast<int64_t>(b) * p.table_width;
-  const int64_t token_stride = static_cast<int64_t>(p.kv_heads) * D;
-  const T *kbase = static_cast<const T *>(p.key_cache) + static_cast<int64_t>(kvh) * D + 8 * q4;
-  const T *vbase = static_cast<const T *>(p.value_cache) + static_cast<int64_t>(kvh) * D + 8 * q4;
+  if (s0 >= ctx) {
+    if (split == 0) zero_rows<T>(p, b, kvh);
+    return;
+  }
+  const int32_t s1 = min(s0 + p.split_size, ctx);
 
-  // Physical page of tile j of chunk c.  With UNIFORM_PAGE (block_size a
-  // multiple of 16, so a 16-token tile never straddles pages) the page is
-  // wave-uniform and the table read is a scalar load; otherwise each lane
-  // reads the entry of its own token.
-  auto fetch_pages = [&](int32_t c, int32_t(&pg)[2]) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int32_t t = s0 + c * kChunk + 16 * j + (UNIFORM_PAGE ? 0 : l16);
-      pg[j] = -1;
-      if (t < s1) {
-        const int32_t logical = p.page_shift >= 0 ? (t >> p.page_shift) : (t / p.block_size);
-        pg[j] = table[logical];
-      }
-    }
-  };
-
-  // Issue the K/V loads of chunk c: lane covers token row l16 of tiles 0/1
-  // and head_dim elements [32ks + 8q4, +8).  Absent tokens load from the
-  // always-valid element 0 of the cache and are masked later, so every load
-  // is unconditional.  `valid` bit t of tile j marks token 16j + t present.
-  auto load_kv = [&](int32_t c, const int32_t(&pg)[2], vec8(&kf)[2][KS], vec8(&vf)[2][KS],
-                     uint32_t(&valid)[2]) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int32_t t = s0 + c * kChunk + 16 * j + l16;
-      const int32_t page = pg[j];
-      const bool ok = t < s1 && page >= 0 && page < p.num_blocks;
-      int32_t offset;
-      if (p.page_shift >= 0)
-        offset = t & (p.block_size - 1);
-      else
-        offset = t - (t / p.block_size) * p.block_size;
-      int64_t off = (static_cast<int64_t>(page) * p.block_size + offset) * token_stride;
-      if (!ok) off = -static_cast<int64_t>(kvh) * D - 8 * q4;
-      valid[j] = static_cast<uint32_t>(__ballot(ok) & 0xffffull);
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        kf[j][ks] = *reinterpret_cast<const vec8 *>(kbase + off + 32 * ks);
-        vf[j][ks] = *reinterpret_cast<const vec8 *>(vbase + off + 32 * ks);
-      }
-    }
-  };
+  const uint32_t token_bytes = static_cast<uint32_t>(p.kv_heads) * D * sizeof(T);
+  const unsigned char *kbytes = static_cast<const unsigned char *>(p.key_cache);
+  const unsigned char *vbytes = static_cast<const unsigned char *>(p.value_cache);
+  const int64_t head_bytes = static_cast<int64_t>(kvh) * D * sizeof(T);
+  const uint32_t lane_full = static_cast<uint32_t>(l16) * token_bytes + 16u * q4;
+  const uint32_t lane_first = 16u * q4;  // stand-in row for absent tokens
 
   f32x4 acc[NB];
 #pragma unroll
   for (int n = 0; n < NB; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegInf;  // running max of head l16 (base 2)
-  float l_run = 0.f;      // lane-partial running sum of head l16
+  float m_run = kNegInf;  // reference max of head l16 (base 2, scaled)
+  float l_run = 0.f;      // lane-partial sum of head l16
+  unsigned char *vt = lds + wave * kChunk * kRow;
 
-  T *vt = reinterpret_cast<T *>(lds) + wave * D * kVtStride;
+  // Issue the K/V loads of segment-relative chunk c (valid or not: absent
+  // tokens and chunks past the end read a stand-in row, so every load is
+  // unconditional and the wait counts stay exact).  Bit t of valid[j]
+  // marks token 16j + t present.
+  auto load_kv = [&](int32_t seg_first_tile, int32_t seg_s0, int32_t seg_s1, int32_t c,
+                     vec8(&kf)[2][KS], vec8(&vf)[2][KS], uint32_t(&valid)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int32_t t0 = seg_s0 + c * kChunk + 16 * j;
+      const int32_t tile = (t0 - s0) >> 4;
+      const int32_t slot = min(tile - seg_first_tile, kSegmentTiles - 1);
+      const int32_t page = __builtin_amdgcn_readlane(page_win, slot);
+      const bool tile_ok = t0 < seg_s1 && page >= 0 && page < p.num_blocks;
+      const int32_t ntok = tile_ok ? min(16, seg_s1 - t0) : 0;
+      valid[j] = ntok >= 16 ? 0xffffu : ((1u << ntok) - 1u);
+      const int32_t in_page = p.page_shift >= 0 ? (t0 & (p.block_size - 1))
+                                                : (t0 - (t0 / p.block_size) * p.block_size);
+      const int64_t tile_off =
+          tile_ok ? (static_cast<int64_t>(page) * p.block_size + in_page) * token_bytes + head_bytes
+                  : 0;
+      const uint32_t lane_off = l16 < ntok ? lane_full : lane_first;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        kf[j][ks] = *reinterpret_cast<const vec8 *>(kbytes + tile_off + lane_off + 64 * ks);
+        vf[j][ks] = *reinterpret_cast<const vec8 *>(vbytes + tile_off + lane_off + 64 * ks);
+      }
+    }
+  };
 
   auto compute = [&](vec8(&kf)[2][KS], vec8(&vf)[2][KS], const uint32_t(&valid)[2]) {
-    // Scores: lane holds S[token 16j + 4q4 + r][head l16].
-    float sc[8];
+    float sc[8];  // raw q.k of token 16j + 4q4 + r, head l16
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) s = M::mma(kf[j][ks], qf[ks], s);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bool ok = (valid[j] >> (4 * q4 + r)) & 1u;
-        sc[4 * j + r] = ok ? s[r] * p.scale_log2 : kNegInf;
+      for (int r = 0; r < 4; ++r) sc[4 * j + r] = s[r];
+    }
+    if ((valid[0] & valid[1]) != 0xffffu) {  // uniform: partial chunk
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (!((valid[j] >> (4 * q4 + r)) & 1u)) sc[4 * j + r] = kNegInf;
+      // Stand-in V rows of absent tokens are cleared so that 0 * (non-finite)
+      // cannot leak into the accumulator.
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const bool mine = (valid[j] >> l16) & 1u;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) vf[j][ks] = mine ? vf[j][ks] : vec8{};
       }
     }
-    float mx = sc[0];
+    float mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                     fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+    mx *= p.scale_log2;  // scale > 0 commutes with max
+    // Raise the reference max only when some score overshoots it by more
+    // than the threshold (uniform decision).
+    if (__ballot(mx > m_run + kRescaleThreshold) != 0) {
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      if (mx == kNegInf) return;  // uniform: no token of the chunk is present
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
 #pragma unroll
-    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sc[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    if (mx == kNegInf) return;  // uniform: no token of the chunk is present
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);
-    m_run = m_new;
+      for (int n = 0; n < NB; ++n) acc[n] *= alpha;
+    }
     vec8 pf;
     float psum = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float pr = exp2f(sc[i] - m_new);
+      const float pr = fast_exp2(__builtin_fmaf(sc[i], p.scale_log2, -m_run));
       psum += pr;
       pf[i] = static_cast<T>(pr);
     }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int n = 0; n < NB; ++n) acc[n] *= alpha;
+    l_run += psum;
 
-    // Absent tokens carry p = 0 but their V rows were loaded from a stand-in
-    // address; clear them so 0 * (non-finite) cannot leak in.
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      if (valid[j] != 0xffffu && !((valid[j] >> l16) & 1u)) {
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) vf[j][ks] = vec8{};
-      }
-    }
-    // Stage V^T[dim][token] for this chunk in the wave's LDS tile.  LDS
-    // requests of one wavefront are served in order, so the compiler
-    // barriers below are the only ordering needed.
+    // Stage V token-major (one 16-byte LDS write per load), then read V^T
+    // fragments with the transpose read.  LDS requests of one wavefront are
+    // served in order, so compiler barriers are the only ordering needed.
     __asm__ volatile("" ::: "memory");
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          vt[(32 * ks + 8 * q4 + e) * kVtStride + 16 * j + l16] = vf[j][ks][e];
+        *reinterpret_cast<vec8 *>(vt + (16 * j + l16) * kRow + (32 * ks + 8 * q4) * 2) = vf[j][ks];
     __asm__ volatile("" ::: "memory");
-    // P.V: A = V^T (row = dim 16n + l16, k = 8q4 + i -> token 4q4+i of tile
-    // 0 for i < 4, of tile 1 for i >= 4); B = P in the same k order.
+    const unsigned char *rd = vt + (4 * q4 + (l16 >> 2)) * kRow + (l16 & 3) * 8;
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
-      const T *row = vt + (16 * n + l16) * kVtStride + 4 * q4;
-      const vec4 lo = *reinterpret_cast<const vec4 *>(row);
-      const vec4 hi = *reinterpret_cast<const vec4 *>(row + 16);
-      const vec8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[n] = M::mma(a, pf, acc[n]);
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(rd + 32 * n));
+      const i16x4 hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(rd + 16 * kRow + 32 * n));
+      const i16x8 a16 = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[n] = M::mma(__builtin_bit_cast(vec8, a16), pf, acc[n]);
     }
     __asm__ volatile("" ::: "memory");
   };
 
-  // Two register sets alternate so a chunk's K/V stay in flight while the
-  // previous one is computed; page ids run one chunk further ahead.
+  // Segments of up to 1024 tokens share one page window; inside a segment
+  // two register sets alternate so the next chunk's K/V are in flight while
+  // the current one is computed.
   vec8 ka[2][KS], va[2][KS], kb[2][KS], vb[2][KS];
-  uint32_t vala[2] = {0u, 0u}, valb[2] = {0u, 0u};
-  int32_t pa[2] = {-1, -1}, pb[2] = {-1, -1};
-  int32_t c = wave;
-  if (c < nchunks) {
-    fetch_pages(c, pa);
-    if (c + NW < nchunks) fetch_pages(c + NW, pb);
-    load_kv(c, pa, ka, va, vala);
-  }
-  while (c < nchunks) {
-    if (c + 2 * NW < nchunks) fetch_pages(c + 2 * NW, pa);
-    if (c + NW < nchunks) load_kv(c + NW, pb, kb, vb, valb);
-    compute(ka, va, vala);
-    c += NW;
-    if (c >= nchunks) break;
-    if (c + 2 * NW < nchunks) fetch_pages(c + 2 * NW, pb);
-    if (c + NW < nchunks) load_kv(c + NW, pa, ka, va, vala);
-    compute(kb, vb, valb);
-    c += NW;
+  uint32_t vala[2], valb[2];
+  for (int32_t seg_s0 = s0; seg_s0 < s1; seg_s0 += 16 * kSegmentTiles) {
+    const int32_t seg_first_tile = (seg_s0 - s0) >> 4;
+    if (seg_first_tile != 0) page_win = load_window(seg_first_tile);
+    const int32_t seg_s1 = min(seg_s0 + 16 * kSegmentTiles, s1);
+    const int32_t seg_chunks = (seg_s1 - seg_s0 + kChunk - 1) / kChunk;
+    const int32_t mine = seg_chunks > wave ? (seg_chunks - wave + NW - 1) / NW : 0;
+    if (mine == 0) continue;
+    auto chunk = [&](int32_t i) { return i < mine ? wave + i * NW : seg_chunks; };
+    load_kv(seg_first_tile, seg_s0, seg_s1, chunk(0), ka, va, vala);
+    for (int32_t i = 0; i < mine; i += 2) {
+      load_kv(seg_first_tile, seg_s0, seg_s1, chunk(i + 1), kb, vb, valb);
+      compute(ka, va, vala);
+      if (i + 1 >= mine) break;
+      load_kv(seg_first_tile, seg_s0, seg_s1, chunk(i + 2), ka, va, vala);
+      compute(kb, vb, valb);
+    }
   }
 
   // Lane-partial sums -> per-head sums within the wave.
@@ -372,22 +493,547 @@ paged_decode_mfma_kernel(AttnParams p) {
     for (int r = 0; r < 4; ++r) red_acc[(wave * 16 + l16) * D + 16 * n + 4 * q4 + r] = acc[n][r];
   __syncthreads();
 
-  for (int idx = threadIdx.x; idx < p.group * D; idx += NW * 64) {
-    const int g = idx / D;
-    const int d = idx - g * D;
-    float mmax = kNegInf;
+  constexpr int kMaxItems = (16 * D + NW * 64 - 1) / (NW * 64);
+  finish<T, kMaxItems>(p, b, kvh, split, ctx,
+                       [&](int, int idx, float &m, float &l, float &num) {
+                         const int g = idx / D;
+                         const int d = idx - g * D;
+                         float mmax = kNegInf;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) mmax = fmaxf(mmax, red_ml[w * 32 + g]);
-    float num = 0.f, den = 0.f;
-    if (mmax != kNegInf) {
+                         for (int w = 0; w < NW; ++w) mmax = fmaxf(mmax, red_ml[w * 32 + g]);
+                         float acc_num = 0.f, den = 0.f;
+                         if (mmax != kNegInf) {
 #pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const float e = exp2f(red_ml[w * 32 + g] - mmax);
-        den += red_ml[w * 32 + 16 + g] * e;
-        num += red_acc[(w * 16 + g) * D + d] * e;
+                           for (int w = 0; w < NW; ++w) {
+                             const float e = fast_exp2(red_ml[w * 32 + g] - mmax);
+                             den += red_ml[w * 32 + 16 + g] * e;
+                             acc_num += red_acc[(w * 16 + g) * D + d] * e;
+                           }
+                         }
+                         m = mmax;
+                         l = den;
+                         num = acc_num;
+                       });
+}
+
+// ===========================================================================
+// Balanced streaming MFMA kernel (split mode with arrival counters)
+// ===========================================================================
+// One wavefront per workgroup.  The work is the global sequence of 16-token
+// tiles ordered by (row, kv-head group, tile).  A kv-head group is HG
+// adjacent kv heads whose slices of a token row form one contiguous run of
+// HG * head_dim elements (>= 512 bytes where the geometry allows): the
+// cache stores [page, token, kv head, head_dim], so a wavefront that reads
+// all heads of a group for a tile requests whole DRAM rows together instead
+// of scattering 128-byte pieces over time (measured: ~1.5x the bandwidth of
+// one head per wavefront).  A prefix sum of the device-side lengths
+// (computed by every wavefront; the lengths are a few hundred bytes) gives
+// each of the `nw` wavefronts an equal contiguous range of tiles, so there
+// are no empty or ragged workgroups whatever the length distribution.  A
+// wavefront streams its range with DEPTH tiles of K/V in flight, across
+// unit boundaries.  A unit (row, head group) wholly inside one range is
+// finished in place; one shared by several ranges leaves one partial per
+// range ("piece"), and the last wavefront to count itself in merges them.
+// Piece p of a unit lands in partial slot p of its rows, and the range
+// length is kept >= max tiles / (slots - 1) so a unit never spans more
+// pieces than there are slots.
+//
+// Per tile and head: scores S^T = K q^T with v_mfma_f32_16x16x32 (lane
+// (l16, q4) holds S[token 4q4 + r][query head l16]); P in that layout is
+// directly the B operand of v_mfma_f32_16x16x16 (k = the 4 tokens of the
+// lane group), and V^T (A operand: dim 16n + l16, tokens 4q4..4q4+3) is one
+// ds_read_b64_tr_b16 of V staged token-major in LDS.
+constexpr int kStreamMinTiles = 4;  // floor on tiles per wavefront range
+constexpr int kStreamMaxRows = 4096;
+constexpr int kStreamWavesPerCu = 4;  // default: one wavefront per SIMD
+
+__device__ __forceinline__ int32_t wave_of_tile(int64_t t, int32_t nw, int64_t total) {
+  // largest w with floor(w * total / nw) <= t
+  return static_cast<int32_t>(((t + 1) * nw - 1) / total);
+}
+
+template <typename T>
+struct Mfma16;
+
+template <>
+struct Mfma16<__bf16> {
+  static __device__ __forceinline__ f32x4 mma(i16x4 a, i16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ i16x4 pack(float a, float b, float c, float d) {
+    typedef __bf16 v4 __attribute__((ext_vector_type(4)));
+    const v4 v = {static_cast<__bf16>(a), static_cast<__bf16>(b), static_cast<__bf16>(c),
+                  static_cast<__bf16>(d)};
+    return __builtin_bit_cast(i16x4, v);
+  }
+};
+
+template <>
+struct Mfma16<_Float16> {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ f32x4 mma(i16x4 a, i16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a),
+                                                 __builtin_bit_cast(h4, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ i16x4 pack(float a, float b, float c, float d) {
+    const h4 v = {static_cast<_Float16>(a), static_cast<_Float16>(b), static_cast<_Float16>(c),
+                  static_cast<_Float16>(d)};
+    return __builtin_bit_cast(i16x4, v);
+  }
+};
+
+// Dynamic LDS of the streaming kernel: row starts (rows + 1 ints), row
+// lengths (rows ints), then a region shared by the V staging tiles (HG
+// heads x 16 tokens) and the merge weights (16 heads x 64 pieces floats).
+__host__ __device__ inline size_t stream_meta_bytes(int32_t rows) {
+  return (static_cast<size_t>(2 * rows + 1) * 4 + 15) / 16 * 16;
+}
+
+size_t stream_lds_bytes(int head_dim, int32_t heads_per_group, int32_t rows) {
+  const size_t vtiles = static_cast<size_t>(heads_per_group) * 16 * (head_dim * 2 + 16);
+  const size_t weights = 16 * 64 * sizeof(float);
+  return stream_meta_bytes(rows) + (vtiles > weights ? vtiles : weights);
+}
+
+template <typename T, int D, int HG, int DEPTH>
+__global__ void __launch_bounds__(64)
+paged_decode_stream_kernel(AttnParams p) {
+  using M = Mfma<T>;
+  using M16 = Mfma16<T>;
+  using vec8 = typename M::vec8;
+  constexpr int KS = D / 32;
+  constexpr int NB = D / 16;
+  constexpr int kRow = v_row_bytes<D>();
+  extern __shared__ __attribute__((aligned(16))) unsigned char stream_smem[];
+  const int lane = threadIdx.x;
+  const int l16 = lane & 15;
+  const int q4 = lane >> 4;
+  const int32_t R = p.batch;
+  const int32_t NG = p.kv_heads / HG;  // head groups per row
+  const int32_t G = p.group;
+  int32_t *rstart = reinterpret_cast<int32_t *>(stream_smem);  // [R + 1] first tile of row / NG
+  int32_t *rctx = rstart + R + 1;                               // [R] clamped row length
+  unsigned char *vt = stream_smem + stream_meta_bytes(R);
+  float *weights = reinterpret_cast<float *>(vt);               // merge weights (after streaming)
+
+  // ---- row lengths (all loads in flight together) and their prefix sum ------
+  // Unit u = b * NG + hg covers tiles [NG * rstart[b] + hg * n_b, + n_b) of
+  // the global tile sequence, n_b = ceil(ctx_b / 16).
+#pragma unroll 8
+  for (int32_t b = lane; b < R; b += 64) rctx[b] = clamp_context(p, b);
+  __asm__ volatile("" ::: "memory");
+  int32_t carry = 0, nmax = 0;
+  for (int32_t base = 0; base < R; base += 64) {
+    const int32_t b = base + lane;
+    const int32_t n = b < R ? (rctx[b] + 15) >> 4 : 0;
+    nmax = max(nmax, n);
+    int32_t x = n;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int32_t y = __shfl_up(x, off, 64);
+      if (lane >= off) x += y;
+    }
+    if (b < R) rstart[b + 1] = carry + x;
+    carry += __shfl(x, 63, 64);
+  }
+  if (lane == 0) rstart[0] = 0;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) nmax = max(nmax, __shfl_xor(nmax, off, 64));
+  const int64_t total = static_cast<int64_t>(carry) * NG;
+  __asm__ volatile("" ::: "memory");
+  auto unit_start = [&](int32_t u) -> int64_t {
+    const int32_t b = u / NG;
+    const int32_t hg = u - b * NG;
+    return static_cast<int64_t>(NG) * rstart[b] +
+           static_cast<int64_t>(hg) * (rstart[b + 1] - rstart[b]);
+  };
+
+  // Zero-length rows: outputs are zeros (spread over the wavefronts).
+  for (int32_t b = blockIdx.x; b < R; b += gridDim.x) {
+    if (rctx[b] != 0) continue;
+    T *out = static_cast<T *>(p.output) + static_cast<int64_t>(b) * p.query_heads * D;
+    for (int i = lane; i < p.query_heads * D; i += 64) out[i] = from_float<T>(0.f);
+  }
+  if (total == 0) return;
+
+  // ---- this wavefront's range ----------------------------------------------
+  // At most min(slots, 64) pieces per unit: the merge keeps one weight per
+  // (head, piece) in LDS.
+  const int32_t slots = min(p.num_splits, 64);
+  const int32_t min_tiles = max(kStreamMinTiles, (nmax + slots - 2) / (slots - 1));
+  int64_t nw64 = total / min_tiles;
+  if (nw64 < 1) nw64 = 1;
+  const int32_t nw = static_cast<int32_t>(min<int64_t>(nw64, gridDim.x));
+  const int32_t w = blockIdx.x;
+  if (w >= nw) return;
+  const int64_t t_begin = static_cast<int64_t>(w) * total / nw;
+  const int64_t t_end = static_cast<int64_t>(w + 1) * total / nw;
+  const int32_t range = static_cast<int32_t>(t_end - t_begin);
+
+  const uint32_t token_bytes = static_cast<uint32_t>(p.kv_heads) * D * sizeof(T);
+  const unsigned char *kbytes = static_cast<const unsigned char *>(p.key_cache);
+  const unsigned char *vbytes = static_cast<const unsigned char *>(p.value_cache);
+  const uint32_t lane_full = static_cast<uint32_t>(l16) * token_bytes + 16u * q4;
+  const uint32_t lane_first = 16u * q4;
+
+  // ---- tile window: lane i describes tile t_begin + win + i ---------------
+  int32_t win = 0;         // range-relative index of lane 0's tile
+  int32_t win_count = 0;   // tiles of the range inside the window
+  int32_t next = 0;        // next window slot to issue
+  int32_t w_unit = -1;     // unit of the tile
+  int32_t w_page = -1;     // physical page
+  int32_t w_inpage = 0;    // token offset of the tile inside its page
+  int32_t w_ntok = 0;      // present tokens of the tile (0..16)
+  int32_t cont_unit = -1;  // unit of the first tile after the window, if in range
+  auto find_unit = [&](int64_t g) {  // u with unit_start(u) <= g < unit_start(u + 1)
+    int32_t lo = 0, hi = R;  // row b with NG * rstart[b] <= g < NG * rstart[b + 1]
+    while (hi - lo > 1) {
+      const int32_t mid = (lo + hi) >> 1;
+      if (static_cast<int64_t>(NG) * rstart[mid] <= g) lo = mid; else hi = mid;
+    }
+    const int32_t n = rstart[lo + 1] - rstart[lo];
+    const int64_t rel = g - static_cast<int64_t>(NG) * rstart[lo];
+    return lo * NG + static_cast<int32_t>(n > 0 ? rel / n : 0);
+  };
+  auto load_window = [&](int32_t first) {
+    win = first;
+    win_count = min(64, range - first);
+    next = 0;
+    cont_unit = first + 64 < range ? find_unit(t_begin + first + 64) : -1;
+    const bool in_range = lane < win_count;
+    const int64_t g = t_begin + first + lane;
+    const int32_t u = in_range ? find_unit(g) : 0;
+    w_unit = in_range ? u : -1;
+    w_page = -1;
+    w_ntok = 0;
+    w_inpage = 0;
+    if (in_range) {
+      const int32_t tile = static_cast<int32_t>(g - unit_start(u));
+      const int32_t tok = 16 * tile;
+      const int32_t bb = u / NG;
+      const int32_t logical = p.page_shift >= 0 ? (tok >> p.page_shift) : (tok / p.block_size);
+      const int32_t page = p.block_tables[static_cast<int64_t>(bb) * p.table_width + logical];
+      w_inpage = tok - logical * p.block_size;
+      const bool ok = page >= 0 && page < p.num_blocks;
+      w_page = ok ? page : -1;
+      w_ntok = ok ? min(16, rctx[bb] - tok) : 0;
+    }
+    // Complete the window's loads here, where no tile is in flight: a load
+    // still pending at the streaming loop's entry would make the compiler
+    // wait for all loads at every use inside the loop.
+    __builtin_amdgcn_s_waitcnt(0);
+  };
+  load_window(0);
+
+  // ---- per-tile register sets -----------------------------------------------
+  struct Set {
+    vec8 k[HG][KS], v[HG][KS], q[HG][KS];
+    uint32_t valid;  // bit t: token t of the tile is present
+    int32_t unit;    // -1: no tile
+  };
+
+  // Issue the loads of the next tile of the window into `st`.  Past the end
+  // the same loads read a stand-in line (cache element 0), so the load
+  // sequence never branches and the wait counts stay exact.
+  auto issue = [&](Set &st) {
+    const bool have = next < win_count;  // uniform
+    const int f = have ? next : 0;
+    next += have ? 1 : 0;
+    const int32_t unit = have ? __builtin_amdgcn_readlane(w_unit, f) : -1;
+    const int32_t ntok = have ? __builtin_amdgcn_readlane(w_ntok, f) : 0;
+    const int32_t page = __builtin_amdgcn_readlane(w_page, f);
+    const int32_t inpage = __builtin_amdgcn_readlane(w_inpage, f);
+    st.unit = unit;
+    st.valid = ntok >= 16 ? 0xffffu : ((1u << ntok) - 1u);
+    const int32_t bb = have ? unit / NG : 0;
+    const int32_t hg = have ? unit - bb * NG : 0;
+    const int64_t tile_off =
+        ntok > 0 ? (static_cast<int64_t>(page) * p.block_size + inpage) * token_bytes +
+                       static_cast<int64_t>(hg) * HG * D * sizeof(T)
+                 : 0;
+    const uint32_t lane_off = l16 < ntok ? lane_full : lane_first;
+#pragma unroll
+    for (int h = 0; h < HG; ++h)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint32_t o = lane_off + (ntok > 0 ? h * D * sizeof(T) : 0) + 64 * ks;
+        st.k[h][ks] = *reinterpret_cast<const vec8 *>(kbytes + tile_off + o);
+        st.v[h][ks] = *reinterpret_cast<const vec8 *>(vbytes + tile_off + o);
+      }
+    // Columns l16 >= G of the score MFMA repeat query head 0 of the group;
+    // their results are never stored, so no select (which would wait on the
+    // load) is needed.
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+      const T *qrow = static_cast<const T *>(p.query) +
+                      (static_cast<int64_t>(bb) * p.query_heads +
+                       static_cast<int64_t>(hg * HG + h) * G + (l16 < G ? l16 : 0)) * D;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        st.q[h][ks] = *reinterpret_cast<const vec8 *>(qrow + 32 * ks + 8 * q4);
+    }
+  };
+
+  f32x4 acc[HG][NB];
+  float m_run[HG], l_run[HG];
+  auto reset = [&]() {
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+#pragma unroll
+      for (int n = 0; n < NB; ++n) acc[h][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m_run[h] = kNegInf;
+      l_run[h] = 0.f;
+    }
+  };
+  reset();
+  // Units whose piece was left as a partial: at most the first and the last
+  // unit of the range.
+  int32_t pending_first = -1, pending_last = -1;
+
+  auto compute = [&](Set &st) {
+    const bool partial = st.valid != 0xffffu;  // uniform
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) s = M::mma(st.k[h][ks], st.q[h][ks], s);
+      float sc[4] = {s[0], s[1], s[2], s[3]};  // token 4q4 + r, query head l16
+      if (partial) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (!((st.valid >> (4 * q4 + r)) & 1u)) sc[r] = kNegInf;
+        // Stand-in V rows of absent tokens are cleared so that 0 * (non-finite)
+        // cannot leak into the accumulator.
+        const bool mine = (st.valid >> l16) & 1u;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) st.v[h][ks] = mine ? st.v[h][ks] : vec8{};
+      }
+      float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])) * p.scale_log2;
+      if (__ballot(mx > m_run[h] + kRescaleThreshold) != 0) {
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run[h], mx);
+        if (m_new != kNegInf) {  // uniform
+          const float alpha = fast_exp2(m_run[h] - m_new);
+          m_run[h] = m_new;
+          l_run[h] *= alpha;
+#pragma unroll
+          for (int n = 0; n < NB; ++n) acc[h][n] *= alpha;
+        }
+      }
+      if (m_run[h] == kNegInf) continue;  // uniform: nothing present yet
+      float pr[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(__builtin_fmaf(sc[r], p.scale_log2, -m_run[h]));
+      l_run[h] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+      const i16x4 pf = M16::pack(pr[0], pr[1], pr[2], pr[3]);
+      unsigned char *vh = vt + h * 16 * kRow;
+      __asm__ volatile("" ::: "memory");
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        *reinterpret_cast<vec8 *>(vh + l16 * kRow + (32 * ks + 8 * q4) * 2) = st.v[h][ks];
+      __asm__ volatile("" ::: "memory");
+      const unsigned char *rd = vh + (4 * q4 + (l16 >> 2)) * kRow + (l16 & 3) * 8;
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        const i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(rd + 32 * n));
+        acc[h][n] = M16::mma(a, pf, acc[h][n]);
+      }
+      __asm__ volatile("" ::: "memory");
+    }
+  };
+
+  // Finish the piece of `unit` held in (m_run, l_run, acc).
+  auto flush = [&](int32_t unit) {
+    const int32_t bb = unit / NG;
+    const int32_t hg = unit - bb * NG;
+    const int64_t u_first = unit_start(unit);
+    const int32_t w0 = wave_of_tile(u_first, nw, total);
+    const int32_t w1 = wave_of_tile(u_first + (rstart[bb + 1] - rstart[bb]) - 1, nw, total);
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+      float l = l_run[h];
+      l += __shfl_xor(l, 16, 64);
+      l += __shfl_xor(l, 32, 64);
+      if (l16 < G) {
+        const int32_t qh = (hg * HG + h) * G + l16;
+        if (w0 == w1) {
+          T *out = output_row<T>(p, bb, qh);
+          const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+          for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) out[16 * n + 4 * q4 + r] = from_float<T>(acc[h][n][r] * inv);
+        } else {
+          const int64_t row =
+              (static_cast<int64_t>(bb) * p.query_heads + qh) * p.num_splits + (w - w0);
+          float *dst = p.partial_acc + row * p.partial_stride;
+#pragma unroll
+          for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              __hip_atomic_store(dst + 16 * n + 4 * q4 + r, acc[h][n][r], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+          if (q4 == 0) {
+            __hip_atomic_store(p.partial_max + row, m_run[h], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p.partial_sum + row, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
       }
     }
-    store_result<T>(p, b, kvh * p.group + g, split, d, mmax, den, num);
+    if (w0 != w1) {
+      if (pending_first < 0)
+        pending_first = unit;
+      else
+        pending_last = unit;
+    }
+    reset();
+  };
+
+  // Log-sum-exp merge of the `pieces` partials of unit (bb, hg) by the
+  // whole wavefront, 16 query heads at a time.  Pass 1: lanes (head, piece
+  // mod lph) load the partial maxima and sums (all in flight at once),
+  // reduce them per head and leave the weights exp2(m_s - M) / den in LDS.
+  // Pass 2: lanes over (head, dim) accumulate the weighted partial rows
+  // with independent loads.  Partials are read with agent-scope atomic
+  // loads (coherent across XCDs).
+  auto merge_unit = [&](int32_t bb, int32_t hg, int32_t pieces) {
+    const int32_t heads = HG * G;  // query heads of the unit
+    const int32_t qh0 = hg * HG * G;
+    for (int32_t hb = 0; hb < heads; hb += 16) {
+      const int32_t nh = min(16, heads - hb);
+      const int gp = nh <= 1 ? 1 : nh <= 2 ? 2 : nh <= 4 ? 4 : nh <= 8 ? 8 : 16;
+      const int lph = 64 / gp;  // lanes per head
+      const int g = lane / lph;
+      const int j = lane - g * lph;
+      const bool head_ok = g < nh;
+      const int64_t hbase =
+          (static_cast<int64_t>(bb) * p.query_heads + qh0 + hb + (head_ok ? g : 0)) * p.num_splits;
+      float pm[16], ps[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int32_t sidx = j + k * lph;
+        const bool ok = head_ok && sidx < pieces;
+        const int64_t at = hbase + (ok ? sidx : 0);
+        pm[k] = __hip_atomic_load(p.partial_max + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ps[k] = __hip_atomic_load(p.partial_sum + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (!ok) {
+          pm[k] = kNegInf;
+          ps[k] = 0.f;
+        }
+      }
+      float mloc = kNegInf;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) mloc = fmaxf(mloc, pm[k]);
+      for (int off = lph >> 1; off > 0; off >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off, 64));
+      float dloc = 0.f;
+      if (mloc != kNegInf) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) dloc += ps[k] * fast_exp2(pm[k] - mloc);
+      }
+      for (int off = lph >> 1; off > 0; off >>= 1) dloc += __shfl_xor(dloc, off, 64);
+      const float inv = dloc > 0.f ? 1.f / dloc : 0.f;
+      __asm__ volatile("" ::: "memory");
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int32_t sidx = j + k * lph;
+        if (head_ok && sidx < pieces)
+          weights[g * 64 + sidx] = mloc != kNegInf ? fast_exp2(pm[k] - mloc) * inv : 0.f;
+      }
+      __asm__ volatile("" ::: "memory");
+      constexpr int kItems = (16 * D + 63) / 64;
+      float num[kItems];
+#pragma unroll
+      for (int k = 0; k < kItems; ++k) num[k] = 0.f;
+      for (int32_t sidx = 0; sidx < pieces; ++sidx) {
+        float v[kItems];
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) {
+          const int idx = lane + 64 * k;
+          const int gg = min(idx / D, nh - 1);
+          const int d = idx - (idx / D) * D;
+          const int64_t row = (static_cast<int64_t>(bb) * p.query_heads + qh0 + hb + gg) * p.num_splits + sidx;
+          v[k] = __hip_atomic_load(p.partial_acc + row * p.partial_stride + d, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) {
+          const int idx = lane + 64 * k;
+          const int gg = min(idx / D, nh - 1);
+          num[k] += weights[gg * 64 + sidx] * v[k];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kItems; ++k) {
+        const int idx = lane + 64 * k;
+        if (idx < nh * D) output_row<T>(p, bb, qh0 + hb + idx / D)[idx - (idx / D) * D] = from_float<T>(num[k]);
+      }
+      __asm__ volatile("" ::: "memory");
+    }
+  };
+
+  // ---- stream the range ------------------------------------------------------
+  // DEPTH register sets rotate: while one tile is computed the next
+  // DEPTH - 1 are in flight.  step() computes `cur` and closes its unit's
+  // piece when the following tile (`nxt`) belongs elsewhere -- unless the
+  // window ends inside the unit, which then continues in the next window.
+  // It returns true once the window is exhausted.  Windows (64 tiles) are
+  // reloaded outside the pipelined loop, so the loop itself carries no
+  // conditional loads and its waits stay partial.  The rotation is spelled
+  // out with constant set indices so the sets stay in registers.
+  static_assert(DEPTH >= 2 && DEPTH <= 4, "2..4 tiles in flight");
+  Set st[DEPTH];
+  auto step = [&](Set &cur, const Set &nxt) -> bool {
+    if (cur.unit < 0) return true;
+    compute(cur);
+    const bool continues = nxt.unit < 0 && cur.unit == cont_unit;
+    if (nxt.unit != cur.unit && !continues) flush(cur.unit);
+    return false;
+  };
+  while (true) {
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i) issue(st[i]);
+    while (true) {
+      issue(st[DEPTH - 1]);
+      if (step(st[0], st[1 % DEPTH])) break;
+      issue(st[0]);
+      if (step(st[1], st[2 % DEPTH])) break;
+      if constexpr (DEPTH > 2) {
+        issue(st[1]);
+        if (step(st[2], st[3 % DEPTH])) break;
+      }
+      if constexpr (DEPTH > 3) {
+        issue(st[2]);
+        if (step(st[3], st[0])) break;
+      }
+    }
+    if (win + 64 >= range) break;
+    load_window(win + 64);
+  }
+
+  // ---- count the partial pieces in; the last arrival merges its unit ----------
+  if (pending_first < 0) return;
+  __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wavefront has completed
+  for (int i = 0; i < 2; ++i) {
+    const int32_t unit = i == 0 ? pending_first : pending_last;
+    if (unit < 0) continue;
+    const int32_t bb = unit / NG;
+    const int32_t hg = unit - bb * NG;
+    const int64_t u_first = unit_start(unit);
+    const int32_t w0 = wave_of_tile(u_first, nw, total);
+    const int32_t w1 = wave_of_tile(u_first + (rstart[bb + 1] - rstart[bb]) - 1, nw, total);
+    const int32_t pieces = w1 - w0 + 1;  // <= 64
+    int32_t last = 0;
+    if (lane == 0) {
+      const int32_t prev =
+          __hip_atomic_fetch_add(p.split_counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = prev == pieces - 1;
+      if (last) __hip_atomic_store(p.split_counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    last = __shfl(last, 0, 64);
+    if (!last) continue;
+    merge_unit(bb, hg, pieces);
   }
 }
 
@@ -401,7 +1047,8 @@ constexpr int kGenericMaxAcc = 32;  // group * head_dim <= 256 * 32
 template <typename T>
 __global__ void __launch_bounds__(kGenericThreads)
 paged_decode_generic_kernel(AttnParams p) {
-  extern __shared__ __attribute__((aligned(16))) float smem[];
+  extern __shared__ __attribute__((aligned(16))) unsigned char generic_smem[];
+  float *smem = reinterpret_cast<float *>(generic_smem);
   const int D = p.head_dim;
   const int G = p.group;
   float *ks = smem;                            // [tile][D + 1]
@@ -412,9 +1059,9 @@ paged_decode_generic_kernel(AttnParams p) {
   float *alpha = l_run + G;                    // [G]
   int *tok_ok = reinterpret_cast<int *>(alpha + G);  // [tile]
 
-  const int32_t split = blockIdx.x;
-  const int32_t kvh = blockIdx.y;
-  const int32_t b = blockIdx.z;
+  const int32_t b = blockIdx.x / p.kv_heads;
+  const int32_t kvh = blockIdx.x - b * p.kv_heads;
+  const int32_t split = blockIdx.y;
   const int32_t ctx = clamp_context(p, b);
   const int32_t s0 = split * p.split_size;
   if (s0 >= ctx) {
@@ -499,15 +1146,13 @@ paged_decode_generic_kernel(AttnParams p) {
     }
   }
   __syncthreads();
-#pragma unroll
-  for (int i = 0; i < kGenericMaxAcc; ++i) {
-    const int idx = threadIdx.x + i * kGenericThreads;
-    if (idx < G * D) {
-      const int g = idx / D;
-      const int d = idx - g * D;
-      store_result<T>(p, b, kvh * G + g, split, d, m_run[g], l_run[g], acc[i]);
-    }
-  }
+  finish<T, kGenericMaxAcc>(p, b, kvh, split, ctx,
+                            [&](int k, int idx, float &m, float &l, float &num) {
+                              const int g = idx / D;
+                              m = m_run[g];
+                              l = l_run[g];
+                              num = acc[k];
+                            });
 }
 
 size_t generic_lds_bytes(int D, int G) {
@@ -551,11 +1196,13 @@ merge_partials_kernel(const float *__restrict__ partial_max, const float *__rest
 // ===========================================================================
 // Host side
 // ===========================================================================
-int32_t choose_variant(int32_t dtype, int32_t head_dim, int32_t group, int32_t flags) {
+int32_t choose_variant(int32_t dtype, int32_t head_dim, int32_t group, int32_t block_size,
+                       int32_t flags) {
   if (flags & TF_ATTENTION_FLAG_FORCE_GENERIC) return TF_ATTENTION_GENERIC;
   if (dtype == TF_DTYPE_FLOAT32) return TF_ATTENTION_GENERIC;
   if (group > 16) return TF_ATTENTION_GENERIC;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128) return TF_ATTENTION_GENERIC;
+  if (block_size % 16 != 0) return TF_ATTENTION_GENERIC;
   return TF_ATTENTION_MFMA;
 }
 
@@ -563,15 +1210,8 @@ constexpr int kMfmaWaves = 4;
 
 template <typename T, int D>
 void launch_mfma(const AttnParams &p, dim3 grid, hipStream_t stream) {
-  // Whole-tile pages need 16-aligned tile starts: one pass starts at token 0,
-  // split mode at multiples of split_size.
-  const bool uniform = p.block_size % 16 == 0 && (p.num_splits == 1 || p.split_size % 16 == 0);
-  if (uniform)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves, true>), grid,
-                       dim3(kMfmaWaves * 64), 0, stream, p);
-  else
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves, false>), grid,
-                       dim3(kMfmaWaves * 64), 0, stream, p);
+  hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves>), grid, dim3(kMfmaWaves * 64), 0,
+                     stream, p);
 }
 
 template <typename T>
@@ -606,8 +1246,9 @@ int32_t validate(const void *query, const void *key_cache, const void *value_cac
 int32_t make_params(AttnParams &p, const void *query, const void *key_cache,
                     const void *value_cache, const int32_t *block_tables,
                     const int32_t *context_lengths, void *output, float *partial_max,
-                    float *partial_sum, float *partial_acc, int64_t partial_capacity,
-                    int32_t partial_row_stride, int32_t batch, int32_t query_heads,
+                    float *partial_sum, float *partial_acc, int32_t *split_counters,
+                    int64_t partial_capacity, int32_t partial_row_stride, int32_t batch,
+                    int32_t query_heads,
                     int32_t kv_heads, int32_t head_dim, int32_t num_blocks, int32_t block_size,
                     int32_t table_width, int32_t split_size, int32_t num_splits, float scale,
                     int32_t dtype) {
@@ -632,6 +1273,7 @@ int32_t make_params(AttnParams &p, const void *query, const void *key_cache,
   p.partial_max = partial_max;
   p.partial_sum = partial_sum;
   p.partial_acc = partial_acc;
+  p.split_counters = num_splits > 1 ? split_counters : nullptr;
   p.batch = batch;
   p.query_heads = query_heads;
   p.kv_heads = kv_heads;
@@ -654,11 +1296,89 @@ int32_t make_params(AttnParams &p, const void *query, const void *key_cache,
   return TF_SUCCESS;
 }
 
+// Compute units of the current device (cached per device id).
+int32_t device_compute_units() {
+  static int32_t cached[64] = {0};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0) return 256;
+  if (device < 64 && cached[device] > 0) return cached[device];
+  int count = 0;
+  if (hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      count <= 0)
+    count = 256;
+  if (device < 64) cached[device] = count;
+  return count;
+}
+
+// Heads per group: the largest power-of-two divisor of kv_heads whose
+// contiguous run of head_dim elements is at most 512 bytes... at least one
+// head; register sets then hold HG * head_dim elements per tile and lane.
+int32_t stream_heads_per_group(int32_t kv_heads, int32_t head_dim) {
+  int32_t hg = 1;
+  while (hg * 2 <= 4 && kv_heads % (hg * 2) == 0 && hg * 2 * head_dim * 2 <= 512) hg *= 2;
+  return hg;
+}
+
+template <typename T, int D, int HG>
+void launch_stream_hg(const AttnParams &p, int32_t waves, int32_t depth, size_t lds,
+                      hipStream_t stream) {
+  // Deeper pipelines for the smaller register footprints.
+  constexpr int kMaxDepth = (D * HG <= 128) ? 4 : 3;
+  if (depth <= 2)
+    hipLaunchKernelGGL((paged_decode_stream_kernel<T, D, HG, 2>), dim3(waves), dim3(64), lds, stream, p);
+  else if (depth == 3 || kMaxDepth == 3)
+    hipLaunchKernelGGL((paged_decode_stream_kernel<T, D, HG, 3>), dim3(waves), dim3(64), lds, stream, p);
+  else
+    hipLaunchKernelGGL((paged_decode_stream_kernel<T, D, HG, kMaxDepth>), dim3(waves), dim3(64), lds, stream, p);
+}
+
+template <typename T, int D>
+void launch_stream_dim(const AttnParams &p, int32_t waves, int32_t depth, hipStream_t stream) {
+  const int32_t hg = stream_heads_per_group(p.kv_heads, D);
+  const size_t lds = stream_lds_bytes(D, hg, p.batch);
+  if (hg == 1) {
+    launch_stream_hg<T, D, 1>(p, waves, depth, lds, stream);
+  } else if (hg == 2 || D == 128) {  // 128-dim heads group at most 2 (512 bytes)
+    launch_stream_hg<T, D, 2>(p, waves, depth, lds, stream);
+  } else if constexpr (D < 128) {
+    launch_stream_hg<T, D, 4>(p, waves, depth, lds, stream);
+  }
+}
+
+int32_t default_stream_depth(int32_t) { return 3; }
+
+template <typename T>
+void launch_stream(const AttnParams &p, int32_t waves, int32_t depth, hipStream_t stream) {
+  switch (p.head_dim) {
+    case 32: launch_stream_dim<T, 32>(p, waves, depth, stream); break;
+    case 64: launch_stream_dim<T, 64>(p, waves, depth, stream); break;
+    default: launch_stream_dim<T, 128>(p, waves, depth, stream); break;
+  }
+}
+
 int32_t launch_split_stage(const AttnParams &p, int32_t dtype, int32_t flags, hipStream_t stream) {
   if (p.batch == 0) return TF_SUCCESS;
-  const dim3 grid(static_cast<unsigned>(p.num_splits), static_cast<unsigned>(p.kv_heads),
-                  static_cast<unsigned>(p.batch));
-  const int32_t variant = choose_variant(dtype, p.head_dim, p.group, flags);
+  {
+    const int32_t variant = choose_variant(dtype, p.head_dim, p.group, p.block_size, flags);
+    if (variant == TF_ATTENTION_MFMA && p.num_splits >= 2 && p.split_counters != nullptr &&
+        !(flags & TF_ATTENTION_FLAG_FORCE_GRID) && p.batch <= kStreamMaxRows) {
+      int32_t per_cu = (flags >> 8) & 0xff;
+      if (per_cu == 0) per_cu = kStreamWavesPerCu;
+      const int32_t waves = device_compute_units() * per_cu;
+      int32_t depth = (flags >> 16) & 0xf;
+      if (depth == 0) depth = default_stream_depth(p.head_dim);
+      if (dtype == TF_DTYPE_BFLOAT16)
+        launch_stream<__bf16>(p, waves, depth, stream);
+      else
+        launch_stream<_Float16>(p, waves, depth, stream);
+      return check_launch("paged_gqa_decode (stream)");
+    }
+  }
+  const dim3 grid(static_cast<unsigned>(p.batch) * static_cast<unsigned>(p.kv_heads),
+                  static_cast<unsigned>(p.num_splits));
+  int32_t variant = choose_variant(dtype, p.head_dim, p.group, p.block_size, flags);
+  // The MFMA kernel's tiles start at multiples of 16 tokens of a split.
+  if (p.num_splits > 1 && p.split_size % 32 != 0) variant = TF_ATTENTION_GENERIC;
   if (variant == TF_ATTENTION_MFMA) {
     if (dtype == TF_DTYPE_BFLOAT16)
       launch_mfma_dim<__bf16>(p, grid, stream);
@@ -719,31 +1439,31 @@ int32_t launch_merge(const float *partial_max, const float *partial_sum, const f
 }  // namespace tf
 
 extern "C" int32_t tf_paged_gqa_decode_variant(int32_t dtype, int32_t head_dim, int32_t group_size,
-                                               int32_t flags) {
-  return tf::choose_variant(dtype, head_dim, group_size, flags);
+                                               int32_t block_size, int32_t flags) {
+  return tf::choose_variant(dtype, head_dim, group_size, block_size, flags);
 }
 
 extern "C" int32_t tf_paged_gqa_decode(
     const void *query, const void *key_cache, const void *value_cache,
     const int32_t *block_tables, const int32_t *context_lengths, void *output,
-    float *partial_max, float *partial_sum, float *partial_accumulator, int64_t partial_capacity,
-    int32_t partial_row_stride, int32_t batch, int32_t query_heads, int32_t kv_heads,
-    int32_t head_dim, int32_t num_blocks, int32_t block_size, int32_t table_width,
-    int32_t split_size, int32_t num_splits, float scale, int32_t dtype, int32_t flags,
-    void *stream) {
+    float *partial_max, float *partial_sum, float *partial_accumulator,
+    int32_t *split_counters, int64_t partial_capacity, int32_t partial_row_stride, int32_t batch,
+    int32_t query_heads, int32_t kv_heads, int32_t head_dim, int32_t num_blocks,
+    int32_t block_size, int32_t table_width, int32_t split_size, int32_t num_splits, float scale,
+    int32_t dtype, int32_t flags, void *stream) {
   using namespace tf;
   clear_error();
   if (batch > 0 && !output) return fail(TF_ERROR_INVALID_ARGUMENT, "null output pointer");
   AttnParams p;
   if (int32_t s = make_params(p, query, key_cache, value_cache, block_tables, context_lengths,
                               output, partial_max, partial_sum, partial_accumulator,
-                              partial_capacity, partial_row_stride, batch, query_heads, kv_heads,
+                              split_counters, partial_capacity, partial_row_stride, batch, query_heads, kv_heads,
                               head_dim, num_blocks, block_size, table_width, split_size,
                               num_splits, scale, dtype))
     return s;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (int32_t st = launch_split_stage(p, dtype, flags, s)) return st;
-  if (num_splits == 1) return TF_SUCCESS;
+  if (num_splits == 1 || split_counters != nullptr) return TF_SUCCESS;
   return launch_merge(partial_max, partial_sum, partial_accumulator, context_lengths, output,
                       batch, query_heads, head_dim, split_size, num_splits, partial_row_stride,
                       p.max_tokens, dtype, s);
@@ -765,7 +1485,7 @@ extern "C" int32_t tf_paged_gqa_decode_partials(
   AttnParams p;
   if (int32_t s = make_params(p, query, key_cache, value_cache, block_tables, context_lengths,
                               nullptr, partial_max, partial_sum, partial_accumulator,
-                              partial_capacity, partial_row_stride, batch, query_heads, kv_heads,
+                              nullptr, partial_capacity, partial_row_stride, batch, query_heads, kv_heads,
                               head_dim, num_blocks, block_size, table_width, split_size,
                               num_splits, scale, dtype))
     return s;

@@ -41,11 +41,17 @@ class PagedAttentionWorkspace:
     Same fields and capacity rule as ``triton_attention.py:25-57``: buffers
     hold ``batch_capacity * query_heads * ceil(max_context_length / 256)``
     fp32 partial rows, accumulator rows padded to ``next_pow2(head_dim)``.
+    ``split_counters`` (no reference counterpart; optional, so workspaces
+    built from the three reference fields still work) holds one zeroed int32
+    arrival counter per (row, head): with it the last workgroup of a row
+    merges the partials inside the split kernel and resets its counter, so
+    the call is one launch and stays graph-replay safe.
     """
 
     partial_max: Tensor
     partial_sum: Tensor
     partial_accumulator: Tensor
+    split_counters: Tensor | None = None
 
     @classmethod
     def allocate(
@@ -69,6 +75,9 @@ class PagedAttentionWorkspace:
             partial_sum=torch.empty_like(partial_max),
             partial_accumulator=torch.empty(
                 (programs, head_bucket), device=device, dtype=torch.float32
+            ),
+            split_counters=torch.zeros(
+                batch_capacity * query_heads, device=device, dtype=torch.int32
             ),
         )
 
@@ -185,10 +194,11 @@ def paged_gqa_decode_attention(
     )
     dtype = _native.dtype_code(query.dtype)
     group = query_heads // kv_heads
-    variant = _native.library().tf_paged_gqa_decode_variant(dtype, head_dim, group, 0)
+    variant = _native.library().tf_paged_gqa_decode_variant(dtype, head_dim, group, block_size, 0)
     kernel = "mfma" if variant == _native.TF_ATTENTION_MFMA else "generic"
     device = query.device
     stream = _native.current_stream(device)
+    counters_ptr = None
     if use_split_kv:
         num_splits = (launch_context + split_size - 1) // split_size
         partial_programs = batch * query_heads * num_splits
@@ -221,6 +231,16 @@ def paged_gqa_decode_attention(
             workspace.partial_sum.numel(),
             workspace.partial_accumulator.shape[0],
         )
+        counters = workspace.split_counters
+        counters_ptr = None
+        if (
+            counters is not None
+            and counters.device == device
+            and counters.dtype == torch.int32
+            and counters.is_contiguous()
+            and counters.numel() >= batch * kv_heads
+        ):
+            counters_ptr = counters.data_ptr()
         _native.check(
             _native.library().tf_paged_gqa_decode(
                 query.data_ptr(),
@@ -232,6 +252,7 @@ def paged_gqa_decode_attention(
                 workspace.partial_max.data_ptr(),
                 workspace.partial_sum.data_ptr(),
                 workspace.partial_accumulator.data_ptr(),
+                counters_ptr,
                 capacity,
                 head_bucket,
                 batch,
@@ -271,6 +292,7 @@ def paged_gqa_decode_attention(
                 None,
                 None,
                 None,
+                None,
                 0,
                 head_bucket,
                 batch,
@@ -296,7 +318,8 @@ def paged_gqa_decode_attention(
         }
     _LAST_ATTENTION_LAUNCH = {
         "kernel": kernel,
-        "grid": (num_splits, kv_heads, batch),
+        "grid": (batch * kv_heads, num_splits),
+        "in_kernel_merge": bool(use_split_kv and counters_ptr is not None),
         "group_size": group,
         "launch_context": launch_context,
     }

@@ -203,7 +203,7 @@ def test_group_and_head_dim_variants(device, query_heads, kv_heads, head_dim):
     _check_against_oracle(case, output.cpu(), 3e-3, 3e-3, f"G={query_heads // kv_heads} D={head_dim}")
 
 
-def _raw_decode(gpu, out, flags, split_size, num_splits, workspace):
+def _raw_decode(gpu, out, flags, split_size, num_splits, workspace, counters=None):
     head_bucket = workspace.partial_accumulator.shape[1]
     batch, query_heads, head_dim = gpu.query.shape
     num_blocks, block_size, kv_heads, _ = gpu.key_cache.shape
@@ -211,7 +211,8 @@ def _raw_decode(gpu, out, flags, split_size, num_splits, workspace):
         gpu.query.data_ptr(), gpu.key_cache.data_ptr(), gpu.value_cache.data_ptr(),
         gpu.block_tables.data_ptr(), gpu.context_lengths.data_ptr(), out.data_ptr(),
         workspace.partial_max.data_ptr(), workspace.partial_sum.data_ptr(),
-        workspace.partial_accumulator.data_ptr(), workspace.partial_max.numel(), head_bucket,
+        workspace.partial_accumulator.data_ptr(), counters, workspace.partial_max.numel(),
+        head_bucket,
         batch, query_heads, kv_heads, head_dim, num_blocks, block_size,
         gpu.block_tables.shape[1], split_size, num_splits, ctypes.c_float(gpu.scale),
         _native.dtype_code(gpu.query.dtype), flags, _native.current_stream(gpu.query.device),
@@ -230,13 +231,27 @@ def test_mfma_and_generic_kernels_agree_through_the_c_abi(device):
         batch_capacity=len(lengths), query_heads=32, head_dim=64, max_context_length=2048,
         device=device,
     )
-    fast = torch.empty_like(gpu.query)
-    slow = torch.empty_like(gpu.query)
-    _raw_decode(gpu, fast, 0, 256, 8, workspace)
-    _raw_decode(gpu, slow, _native.TF_ATTENTION_FLAG_FORCE_GENERIC, 256, 8, workspace)
-    torch.cuda.synchronize()
-    assert_close(fast.cpu(), slow.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, "mfma vs generic")
-    _check_against_oracle(case, slow.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, "generic")
+    counters = workspace.split_counters.data_ptr()
+    outputs = {}
+    for name, flags, counter_ptr in (
+        ("mfma, merge kernel", 0, None),
+        ("mfma stream, in-kernel merge", 0, counters),
+        ("mfma grid, in-kernel merge", _native.TF_ATTENTION_FLAG_FORCE_GRID, counters),
+        ("generic, merge kernel", _native.TF_ATTENTION_FLAG_FORCE_GENERIC, None),
+        ("generic, in-kernel merge", _native.TF_ATTENTION_FLAG_FORCE_GENERIC, counters),
+    ):
+        out = torch.full_like(gpu.query, float("nan"))
+        _raw_decode(gpu, out, flags, 256, 8, workspace, counter_ptr)
+        torch.cuda.synchronize()
+        outputs[name] = out.cpu()
+        _check_against_oracle(case, outputs[name], NORTH_STAR_ATOL, NORTH_STAR_RTOL, name)
+    assert int(workspace.split_counters.sum()) == 0, "arrival counters were not reset"
+    assert_close(outputs["mfma, merge kernel"], outputs["generic, merge kernel"],
+                 NORTH_STAR_ATOL, NORTH_STAR_RTOL, "mfma vs generic")
+    assert_close(outputs["mfma, merge kernel"], outputs["mfma stream, in-kernel merge"],
+                 1e-2, 1e-2, "merge kernel vs streaming kernel")
+    assert_close(outputs["mfma, merge kernel"], outputs["mfma grid, in-kernel merge"],
+                 1e-2, 1e-2, "merge kernel vs grid kernel with in-kernel merge")
 
 
 def test_split_partials_follow_split_oracle(device):
@@ -330,3 +345,85 @@ def test_validation_matches_reference_messages(device):
     grad_query = query.clone().requires_grad_(True)
     with pytest.raises(RuntimeError, match="inference-only"):
         paged_gqa_decode_attention(grad_query, key_cache, key_cache, tables, lengths)
+
+
+def test_in_kernel_merge_is_fresh_on_every_call(device):
+    """Back-to-back calls on one workspace with changing inputs: every call
+    must merge its own partials (counters reset, no stale partial reads)."""
+
+    lengths = [2048, 1500, 700, 129, 0, 1999, 256, 257]
+    case = make_decode_attention_case(
+        lengths, query_heads=32, kv_heads=4, head_dim=64, block_size=16, dtype=torch.bfloat16,
+        seed=21,
+    )
+    gpu = case.to(device)
+    workspace = PagedAttentionWorkspace.allocate(
+        batch_capacity=len(lengths), query_heads=32, head_dim=64, max_context_length=2048,
+        device=device,
+    )
+    plain = PagedAttentionWorkspace(workspace.partial_max.clone(), workspace.partial_sum.clone(),
+                                    workspace.partial_accumulator.clone())
+    generator = torch.Generator().manual_seed(5)
+    queries = [torch.randn(case.query.shape, generator=generator).to(torch.bfloat16).to(device)
+               for _ in range(6)]
+    fused_out = [torch.empty_like(gpu.query) for _ in queries]
+    for q, out in zip(queries, fused_out):
+        paged_gqa_decode_attention(q, gpu.key_cache, gpu.value_cache, gpu.block_tables,
+                                   gpu.context_lengths, max_context_length=2048, output=out,
+                                   workspace=workspace)
+    assert selected_attention_launch()["in_kernel_merge"] is True
+    for index, (q, out) in enumerate(zip(queries, fused_out)):
+        separate = paged_gqa_decode_attention(q, gpu.key_cache, gpu.value_cache,
+                                              gpu.block_tables, gpu.context_lengths,
+                                              max_context_length=2048, workspace=plain)
+        assert selected_attention_launch()["in_kernel_merge"] is False
+        assert_close(out.cpu(), separate.cpu(), 1e-2, 1e-2, f"call {index}")
+    torch.cuda.synchronize()
+    assert int(workspace.split_counters.sum()) == 0
+    case.query = queries[-1].cpu()
+    _check_against_oracle(case, fused_out[-1].cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, "last call")
+
+
+@pytest.mark.parametrize("waves_per_cu", [1, 4, 8])
+def test_stream_kernel_long_ranges_cross_page_windows(device, waves_per_cu):
+    """Two partial slots per row force wavefront ranges of >= 2048 tiles:
+    the 64-tile page windows are reloaded and rows continue across them."""
+
+    lengths = [32768, 100, 5000, 0, 17]
+    case = make_decode_attention_case(
+        lengths, query_heads=8, kv_heads=2, head_dim=64, block_size=16, dtype=torch.bfloat16,
+        seed=9,
+    )
+    gpu = case.to(device)
+    workspace = PagedAttentionWorkspace.allocate(
+        batch_capacity=len(lengths), query_heads=8, head_dim=64, max_context_length=32768,
+        device=device,
+    )
+    out = torch.full_like(gpu.query, float("nan"))
+    flags = waves_per_cu << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT
+    _raw_decode(gpu, out, flags, 16384, 2, workspace, workspace.split_counters.data_ptr())
+    torch.cuda.synchronize()
+    assert int(workspace.split_counters.sum()) == 0
+    _check_against_oracle(case, out.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL,
+                          f"stream kernel, {waves_per_cu} waves/CU")
+
+
+@pytest.mark.parametrize("head_dim", [32, 64, 128])
+@pytest.mark.parametrize("block_size", [16, 32, 48])
+def test_stream_kernel_head_dims_and_pages(device, head_dim, block_size):
+    lengths = [1, 16, 31, 33, 700, 64, 0, 1025]
+    case = make_decode_attention_case(
+        lengths, query_heads=16, kv_heads=4, head_dim=head_dim, block_size=block_size,
+        dtype=torch.float16, seed=head_dim + block_size,
+    )
+    gpu = case.to(device)
+    workspace = PagedAttentionWorkspace.allocate(
+        batch_capacity=len(lengths), query_heads=16, head_dim=head_dim,
+        max_context_length=1025, device=device,
+    )
+    output = paged_gqa_decode_attention(
+        gpu.query, gpu.key_cache, gpu.value_cache, gpu.block_tables, gpu.context_lengths,
+        max_context_length=1025, workspace=workspace,
+    )
+    assert selected_attention_launch()["in_kernel_merge"] is True
+    _check_against_oracle(case, output.cpu(), 3e-3, 3e-3, f"D={head_dim} page={block_size}")
