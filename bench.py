@@ -11,8 +11,10 @@ page pool (``--pools``), so every step streams its pages from HBM.
 Prints ONE JSON line.  ``value`` is algorithmic GB/s of the whole call
 (byte model of benchmark/attention_benchmark.py:148-161: q, K, V, tables,
 output of the active rows) over the timed steps; ``roofline`` reports the
-one kernel of the call, timed with HIP events recorded around each launch on
-the launch stream inside the same timed region.  ``cpu_baseline`` is
+one kernel of the call, timed with HIP events recorded around each of K
+eager launches on the launch stream.  The K timed steps themselves run as
+one HIP-graph replay (a ctypes call costs the host longer than the kernel
+takes, so eager steps would time the host).  ``cpu_baseline`` is
 the CPU oracle on a bounded sample of the same rows, on this host's cores.
 """
 
@@ -43,7 +45,8 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--pools", type=int, default=6, help="rotated K/V page pools")
-    parser.add_argument("--split-size", type=int, default=256)
+    parser.add_argument("--split-size", type=int, default=512,
+                        help="tokens per split-KV partition (multiple of 32)")
     parser.add_argument("--merge", choices=("fused", "kernel"), default="fused",
                         help="in-kernel merge (arrival counters) or a separate merge launch")
     parser.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -153,13 +156,12 @@ def main() -> int:
     output = torch.empty_like(gpu.query)
     dtype = _native.dtype_code(gpu.query.dtype)
     stream = torch.cuda.current_stream(device)
-    handle = stream.cuda_stream
     variant = lib.tf_paged_gqa_decode_variant(dtype, head_dim, query_heads // kv_heads, block_size, 0)
 
     counters = workspace.split_counters
     fused = args.merge == "fused"
 
-    def attention_call(pool: int) -> None:
+    def attention_call(pool: int, handle: int) -> None:
         # The product path, tf_paged_gqa_decode: with arrival counters one
         # launch whose last workgroup per (row, kv head) merges; without them
         # the split kernel is followed by the merge kernel.
@@ -173,7 +175,7 @@ def main() -> int:
             block_size, table_width, split_size, num_splits, case.scale, dtype, 0, handle),
             "attention")
 
-    def split_stage(pool: int) -> None:
+    def split_stage(pool: int, handle: int) -> None:
         key_cache, value_cache = pools[pool]
         _native.check(lib.tf_paged_gqa_decode_partials(
             gpu.query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
@@ -183,7 +185,7 @@ def main() -> int:
             query_heads, kv_heads, head_dim, num_blocks, block_size, table_width, split_size,
             num_splits, case.scale, dtype, 0, handle), "partials")
 
-    def merge_stage() -> None:
+    def merge_stage(handle: int) -> None:
         _native.check(lib.tf_paged_gqa_decode_merge(
             workspace.partial_max.data_ptr(), workspace.partial_sum.data_ptr(),
             workspace.partial_accumulator.data_ptr(), gpu.context_lengths.data_ptr(),
@@ -193,7 +195,8 @@ def main() -> int:
     # Gate before timing: the benchmarked raw call must equal the Python entry
     # point (the parity tests check that entry point) -- bit for bit on the
     # product path, up to rounding for the separate-merge alternative.
-    attention_call(0)
+    eager = stream.cuda_stream
+    attention_call(0, eager)
     torch.cuda.synchronize()
     from tensorforge_amd.kernels import paged_gqa_decode_attention
 
@@ -210,33 +213,57 @@ def main() -> int:
         print(json.dumps({"error": "raw C-ABI call and the Python entry point disagree"}))
         return 1
 
+    def one_step(step: int, handle: int) -> None:
+        if fused:
+            attention_call(step % args.pools, handle)
+        else:
+            split_stage(step % args.pools, handle)
+            merge_stage(handle)
+
     for step in range(args.warmup):
-        attention_call(step % args.pools)
+        one_step(step, eager)
     torch.cuda.synchronize()
 
-    # Timed region: one attention call per step.  With the separate merge the
-    # split kernel is bracketed by its own events so the dominant kernel can
-    # be reported alone.
+    # Whole-job throughput: the K steps are captured once in a HIP graph and
+    # replayed, so the host-side cost of a ctypes call (several microseconds,
+    # longer than the kernel) does not throttle the device.  One untimed
+    # replay precedes the timed one.
+    graph = torch.cuda.CUDAGraph()
+    capture_stream = torch.cuda.Stream(device)
+    capture_stream.wait_stream(stream)
+    with torch.cuda.graph(graph, stream=capture_stream):
+        for step in range(args.steps):
+            one_step(step, capture_stream.cuda_stream)
+    stream.wait_stream(capture_stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    replay_begin = torch.cuda.Event(enable_timing=True)
+    replay_end = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    replay_begin.record(stream)
+    graph.replay()
+    replay_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_per_step = replay_begin.elapsed_time(replay_end) / args.steps
+
+    # Kernel duration for the roofline: the same K steps launched eagerly on
+    # the launch stream, each split-stage launch bracketed by its own pair of
+    # HIP events (the device idles between launches, so every bracket holds
+    # one kernel and its start-up).
     begin = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     split_end = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    finish = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
     for step in range(args.steps):
         begin[step].record(stream)
         if fused:
-            attention_call(step % args.pools)
-        else:
-            split_stage(step % args.pools)
+            attention_call(step % args.pools, eager)
             split_end[step].record(stream)
-            merge_stage()
-        finish[step].record(stream)
+        else:
+            split_stage(step % args.pools, eager)
+            split_end[step].record(stream)
+            merge_stage(eager)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    total_ms = begin[0].elapsed_time(finish[-1])
-    ms_per_step = total_ms / args.steps
-    stop = finish if fused else split_end
-    split_ms = sum(begin[i].elapsed_time(stop[i]) for i in range(args.steps)) / args.steps
+    split_ms = sum(begin[i].elapsed_time(split_end[i]) for i in range(args.steps)) / args.steps
 
     lengths = case.lengths
     nbytes = decode_attention_bytes(lengths, query_heads, kv_heads, head_dim, block_size, 2)
@@ -286,8 +313,10 @@ def main() -> int:
             "traffic": traffic,
             "kernel": "paged_decode_mfma_kernel"
             + (" (split stage with in-kernel merge)" if fused else " (split stage)"),
+            "timing": "HIP events around each of K eager launches",
             "kernel_ms": round(split_ms, 6),
         },
+        "timing": "K steps captured in one HIP graph, one timed replay",
         "wall_s_timed_loop": round(wall, 4),
     }
     if not args.no_cpu_baseline:

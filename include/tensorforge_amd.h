@@ -55,14 +55,15 @@ enum tf_attention_variant {
                                split_size % 32 == 0 when num_splits > 1    */
 };
 
-/* tf_paged_gqa_decode* flags.  With split_counters and the MFMA family the
- * split stage is a balanced streaming kernel (equal contiguous token ranges
- * per wavefront); FORCE_GRID selects the one-workgroup-per-split kernel
- * instead.  Bits 8-15: streaming wavefronts per compute unit; bits 16-19:
- * chunks in flight per streaming wavefront (2, 3, 4, 6 or 8); 0 selects the
+/* tf_paged_gqa_decode* flags.  FORCE_GENERIC selects the generic family.
+ * STREAM (MFMA family, split_counters given, num_splits >= 2) replaces the
+ * one-workgroup-per-split grid by a balanced streaming kernel: equal
+ * contiguous ranges of 16-token tiles per wavefront whatever the length
+ * distribution.  Bits 8-15: streaming wavefronts per compute unit; bits
+ * 16-19: tiles in flight per streaming wavefront (2..4); 0 selects the
  * defaults. */
 #define TF_ATTENTION_FLAG_FORCE_GENERIC 1
-#define TF_ATTENTION_FLAG_FORCE_GRID 2
+#define TF_ATTENTION_FLAG_STREAM 4
 #define TF_ATTENTION_WAVES_PER_CU_SHIFT 8
 #define TF_ATTENTION_DEPTH_SHIFT 16
 

@@ -1360,8 +1360,8 @@ int32_t launch_split_stage(const AttnParams &p, int32_t dtype, int32_t flags, hi
   if (p.batch == 0) return TF_SUCCESS;
   {
     const int32_t variant = choose_variant(dtype, p.head_dim, p.group, p.block_size, flags);
-    if (variant == TF_ATTENTION_MFMA && p.num_splits >= 2 && p.split_counters != nullptr &&
-        !(flags & TF_ATTENTION_FLAG_FORCE_GRID) && p.batch <= kStreamMaxRows) {
+    if (variant == TF_ATTENTION_MFMA && (flags & TF_ATTENTION_FLAG_STREAM) && p.num_splits >= 2 &&
+        p.split_counters != nullptr && p.batch <= kStreamMaxRows) {
       int32_t per_cu = (flags >> 8) & 0xff;
       if (per_cu == 0) per_cu = kStreamWavesPerCu;
       const int32_t waves = device_compute_units() * per_cu;

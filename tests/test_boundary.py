@@ -1,0 +1,285 @@
+"""The drop-in boundary without a GPU: C-ABI exports and argument checks,
+the Python mirror's validation (order, exception types, messages), the
+workspace capacity contract and the byte models used by the benchmark.
+
+Nothing here launches a kernel: C-ABI calls are made only with arguments the
+library rejects before touching the device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+from tensorforge_amd import _native
+from tensorforge_amd.kernels import (
+    PagedAttentionWorkspace,
+    autotune_cache_size,
+    paged_gqa_decode_attention,
+    paged_kv_write_slots,
+    paged_kv_write_token,
+    residual_rms_norm,
+    rms_norm,
+    selected_autotune_config,
+    set_attention_split_size,
+    swiglu,
+)
+from tensorforge_amd.kernels.attention import attention_split_size
+from tensorforge_amd.workloads import (
+    decode_attention_bytes,
+    kv_append_bytes,
+    make_decode_attention_case,
+    rms_norm_bytes,
+    swiglu_bytes,
+    tinyllama_decode_case,
+    tinyllama_decode_lengths,
+)
+
+REPO_ROOT = Path(__file__).resolve().parents[1]
+HEADER = REPO_ROOT / "include" / "tensorforge_amd.h"
+
+
+@pytest.fixture(scope="module")
+def lib() -> ctypes.CDLL:
+    if not _native.LIBRARY_PATH.exists():
+        from tensorforge_amd import build
+
+        build.build()
+    return _native.library()
+
+
+def _declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return re.findall(r"\b(tf_[a-z0-9_]+)\s*\(", text)
+
+
+def test_library_exports_every_declared_symbol(lib) -> None:
+    declared = _declared_functions()
+    assert len(declared) == len(set(declared)) >= 10
+    for name in declared:
+        assert hasattr(lib, name), f"{name} is declared in the header but not exported"
+    assert set(declared) == set(_native.SIGNATURES), "ctypes signatures and header disagree"
+
+
+def test_header_constants_match_the_python_binding() -> None:
+    text = HEADER.read_text()
+    for name in ("TF_ATTENTION_FLAG_FORCE_GENERIC", "TF_ATTENTION_FLAG_STREAM",
+                 "TF_ATTENTION_WAVES_PER_CU_SHIFT", "TF_ATTENTION_DEPTH_SHIFT"):
+        match = re.search(rf"#define {name} (\d+)", text)
+        assert match and int(match.group(1)) == getattr(_native, name), name
+    for name in ("TF_DTYPE_FLOAT32", "TF_DTYPE_FLOAT16", "TF_DTYPE_BFLOAT16",
+                 "TF_ATTENTION_GENERIC", "TF_ATTENTION_MFMA"):
+        match = re.search(rf"{name} = (\d+)", text)
+        assert match and int(match.group(1)) == getattr(_native, name), name
+
+
+def test_abi_version_and_variant_selection(lib) -> None:
+    assert lib.tf_abi_version() == 4
+    variant = lib.tf_paged_gqa_decode_variant
+    bf16, f16, f32 = (_native.TF_DTYPE_BFLOAT16, _native.TF_DTYPE_FLOAT16,
+                      _native.TF_DTYPE_FLOAT32)
+    assert variant(bf16, 64, 8, 16, 0) == _native.TF_ATTENTION_MFMA
+    assert variant(f16, 128, 4, 32, 0) == _native.TF_ATTENTION_MFMA
+    assert variant(bf16, 32, 16, 16, 0) == _native.TF_ATTENTION_MFMA
+    assert variant(f32, 64, 8, 16, 0) == _native.TF_ATTENTION_GENERIC  # fp32: no MFMA path
+    assert variant(bf16, 80, 4, 16, 0) == _native.TF_ATTENTION_GENERIC  # head_dim 80
+    assert variant(bf16, 64, 32, 16, 0) == _native.TF_ATTENTION_GENERIC  # group > 16
+    assert variant(bf16, 64, 8, 4, 0) == _native.TF_ATTENTION_GENERIC  # page of 4 tokens
+    assert variant(bf16, 64, 8, 16, _native.TF_ATTENTION_FLAG_FORCE_GENERIC) == 0
+
+
+def _error(lib) -> str:
+    return lib.tf_last_error().decode()
+
+
+def test_c_abi_rejects_bad_arguments_before_launch(lib) -> None:
+    invalid = 1
+    stream = None
+    fake = 0x1000  # never dereferenced: every call below fails validation first
+    status = lib.tf_paged_gqa_decode(
+        fake, fake, fake, fake, fake, fake, None, None, None, None, 0, 64,
+        2, 8, 3, 64, 4, 16, 8, 256, 1, 0.125, _native.TF_DTYPE_BFLOAT16, 0, stream)
+    assert status == invalid and "multiple of kv heads" in _error(lib)
+    status = lib.tf_paged_gqa_decode(
+        fake, fake, fake, fake, fake, fake, None, None, None, None, 0, 64,
+        2, 8, 2, 64, 4, 16, 8, 256, 2, 0.125, _native.TF_DTYPE_BFLOAT16, 0, stream)
+    assert status == invalid and "partial buffers" in _error(lib)
+    status = lib.tf_paged_gqa_decode(
+        fake, fake, fake, fake, fake, fake, fake, fake, fake, None, 3, 64,
+        2, 8, 2, 64, 4, 16, 8, 256, 2, 0.125, _native.TF_DTYPE_BFLOAT16, 0, stream)
+    assert status == invalid and "too small" in _error(lib)
+    status = lib.tf_paged_gqa_decode(
+        None, fake, fake, fake, fake, fake, None, None, None, None, 0, 64,
+        2, 8, 2, 64, 4, 16, 8, 256, 1, 0.125, _native.TF_DTYPE_BFLOAT16, 0, stream)
+    assert status == invalid and "null" in _error(lib)
+    status = lib.tf_paged_gqa_decode(
+        fake, fake, fake, fake, fake, fake, None, None, None, None, 0, 64,
+        2, 8, 2, 64, 4, 16, 8, 256, 1, 0.125, 7, 0, stream)
+    assert status == invalid and "dtype" in _error(lib)
+    status = lib.tf_rms_norm(fake, fake, fake, 4, 20000, 1e-5, _native.TF_DTYPE_FLOAT16, stream)
+    assert status == invalid and "16384" in _error(lib)
+    status = lib.tf_rms_norm(fake, fake, fake, 4, 64, 0.0, _native.TF_DTYPE_FLOAT16, stream)
+    assert status == invalid and "eps" in _error(lib)
+    status = lib.tf_residual_rms_norm(fake, None, fake, fake, fake, 4, 64, 1e-5,
+                                      _native.TF_DTYPE_BFLOAT16, stream)
+    assert status == invalid and "null" in _error(lib)
+    assert lib.tf_swiglu(fake, fake, fake, -1, _native.TF_DTYPE_BFLOAT16, stream) == invalid
+    status = lib.tf_paged_kv_write_token(fake, fake, fake, fake, None, None, None, 3, 4, 64,
+                                         8, 16, _native.TF_DTYPE_BFLOAT16, stream)
+    assert status == invalid and "null" in _error(lib)
+    status = lib.tf_paged_kv_write_slots(fake, fake, fake, fake, None, 3, 4, 64, 8, 16,
+                                         _native.TF_DTYPE_BFLOAT16, stream)
+    assert status == invalid and "slot mapping" in _error(lib)
+    # The message is per call: a successful no-op clears it.
+    assert lib.tf_swiglu(fake, fake, fake, 0, _native.TF_DTYPE_BFLOAT16, stream) == 0
+    assert _error(lib) == ""
+
+
+def test_check_maps_status_to_runtime_error(lib) -> None:
+    lib.tf_swiglu(None, None, None, 5, 9, None)
+    with pytest.raises(RuntimeError, match="swiglu failed .status 1.: unsupported dtype code"):
+        _native.check(1, "swiglu")
+
+
+# ---------------------------------------------------------------------------
+# Python mirror: validation order, types and messages of the reference.
+# ---------------------------------------------------------------------------
+def _cpu_attention_inputs():
+    case = make_decode_attention_case([5, 9], query_heads=8, kv_heads=2, head_dim=64,
+                                      block_size=16, dtype=torch.float16, seed=0)
+    return case.query, case.key_cache, case.value_cache, case.block_tables, case.context_lengths
+
+
+def test_attention_rejects_cpu_tensors_like_the_reference(lib) -> None:
+    """triton_attention.py:341-343: "CUDA" in the message."""
+
+    with pytest.raises(ValueError, match="CUDA"):
+        paged_gqa_decode_attention(*_cpu_attention_inputs())
+
+
+def test_ops_reject_cpu_tensors_like_the_reference(lib) -> None:
+    """tests/test_triton_kernels.py:130-140 of the reference."""
+
+    x = torch.randn(2, 64)
+    w = torch.ones(64)
+    with pytest.raises(ValueError, match="CUDA"):
+        rms_norm(x, w)
+    with pytest.raises(ValueError, match="CUDA"):
+        residual_rms_norm(x, x, w)
+    with pytest.raises(ValueError, match="CUDA"):
+        swiglu(x, x)
+
+
+def test_kv_writes_reject_cpu_tensors(lib) -> None:
+    keys = torch.randn(2, 2, 8)
+    cache = torch.zeros(4, 4, 2, 8)
+    control = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="CUDA"):
+        paged_kv_write_token(keys, keys, cache, cache, control, control, control)
+    with pytest.raises(ValueError, match="CUDA"):
+        paged_kv_write_slots(keys, keys, cache, cache, torch.zeros(2, dtype=torch.int64))
+    with pytest.raises(ValueError, match=r"\[batch, kv_heads, head_dim\]"):
+        paged_kv_write_token(keys, keys[:1], cache, cache, control, control, control)
+
+
+def test_autotune_hooks_reject_unknown_operations() -> None:
+    """triton_ops.py:263-295: ValueError for an unknown op name."""
+
+    with pytest.raises(ValueError, match="unknown operation"):
+        selected_autotune_config("gelu")
+    with pytest.raises(ValueError, match="unknown operation"):
+        autotune_cache_size("gelu")
+    for operation in ("rms_norm", "residual_rms_norm", "swiglu"):
+        assert autotune_cache_size(operation) >= 0
+
+
+def test_split_size_setting_is_validated_and_restorable() -> None:
+    previous = set_attention_split_size(512)
+    try:
+        assert attention_split_size() == 512
+        for bad in (0, -32, 100):
+            with pytest.raises(ValueError, match="multiple of 32"):
+                set_attention_split_size(bad)
+        assert attention_split_size() == 512
+    finally:
+        assert set_attention_split_size(previous) == 512
+    assert attention_split_size() == previous
+
+
+def test_workspace_capacity_contract() -> None:
+    """triton_attention.py:25-57: programs = B * Hq * ceil(ctx / 256) fp32
+    rows, accumulator rows padded to next_pow2(head_dim)."""
+
+    workspace = PagedAttentionWorkspace.allocate(
+        batch_capacity=3, query_heads=8, head_dim=80, max_context_length=1000,
+        device=torch.device("cpu"),
+    )
+    programs = 3 * 8 * 4
+    assert workspace.partial_max.shape == (programs,)
+    assert workspace.partial_sum.shape == (programs,)
+    assert workspace.partial_accumulator.shape == (programs, 128)
+    assert workspace.partial_max.dtype == torch.float32
+    assert workspace.split_counters is not None
+    assert workspace.split_counters.dtype == torch.int32
+    assert not bool(workspace.split_counters.any())
+    with pytest.raises(ValueError, match="positive"):
+        PagedAttentionWorkspace.allocate(batch_capacity=0, query_heads=8, head_dim=64,
+                                         max_context_length=16, device=torch.device("cpu"))
+    # Frozen: the fields of a workspace captured in a graph cannot be rebound.
+    with pytest.raises(AttributeError):
+        workspace.partial_max = torch.empty(1)  # type: ignore[misc]
+    # The three reference fields alone still form a workspace.
+    bare = PagedAttentionWorkspace(workspace.partial_max, workspace.partial_sum,
+                                   workspace.partial_accumulator)
+    assert bare.split_counters is None
+
+
+# ---------------------------------------------------------------------------
+# Workloads and byte models.
+# ---------------------------------------------------------------------------
+def test_decode_attention_byte_model_matches_reference_formula() -> None:
+    """attention_benchmark.py:148-161 for a single-length batch:
+    (2 q + 2 kv) elements * e + B * (ceil(ctx / page) + 1) * 4."""
+
+    batch, hq, hkv, d, ctx, page, e = 4, 32, 8, 128, 1000, 16, 2
+    q_elements = batch * hq * d
+    kv_elements = batch * ctx * hkv * d
+    expected = (2 * q_elements + 2 * kv_elements) * e + batch * ((ctx + page - 1) // page + 1) * 4
+    assert decode_attention_bytes([ctx] * batch, hq, hkv, d, page, e) == expected
+    assert decode_attention_bytes([0, ctx], hq, hkv, d, page, e) == expected // batch
+
+
+def test_config2_workload_is_the_documented_one() -> None:
+    lengths = tinyllama_decode_lengths(0)
+    assert len(lengths) == 72 and lengths[64:] == [0] * 8
+    assert all(128 <= ctx <= 2048 for ctx in lengths[:64])
+    case = tinyllama_decode_case(0)
+    assert tuple(case.query.shape) == (72, 32, 64)
+    assert case.key_cache.shape[1:] == (16, 4, 64)
+    assert case.query.dtype == torch.bfloat16
+    assert sum(case.lengths) == 77431
+    assert decode_attention_bytes(case.lengths, 32, 4, 64, 16, 2) == 79833372
+
+
+def test_elementwise_byte_models() -> None:
+    assert rms_norm_bytes(8, 2048, 2, residual=False) == (2 * 8 + 1) * 2048 * 2
+    assert rms_norm_bytes(8, 2048, 2, residual=True) == (4 * 8 + 1) * 2048 * 2
+    assert swiglu_bytes(5632, 2) == 3 * 5632 * 2
+    assert kv_append_bytes(64, 4, 64, 2) > 0
+
+
+def test_bench_refuses_more_than_one_gpu() -> None:
+    result = subprocess.run(
+        [sys.executable, str(REPO_ROOT / "bench.py"), "--gpus", "2"],
+        capture_output=True, text=True, timeout=300,
+    )
+    assert result.returncode == 2
+    message = json.loads(result.stdout.strip().splitlines()[-1])
+    assert "one GPU" in message["error"] and message["n_gpus"] == 2

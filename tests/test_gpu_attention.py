@@ -235,8 +235,8 @@ def test_mfma_and_generic_kernels_agree_through_the_c_abi(device):
     outputs = {}
     for name, flags, counter_ptr in (
         ("mfma, merge kernel", 0, None),
-        ("mfma stream, in-kernel merge", 0, counters),
-        ("mfma grid, in-kernel merge", _native.TF_ATTENTION_FLAG_FORCE_GRID, counters),
+        ("mfma stream, in-kernel merge", _native.TF_ATTENTION_FLAG_STREAM, counters),
+        ("mfma grid, in-kernel merge", 0, counters),
         ("generic, merge kernel", _native.TF_ATTENTION_FLAG_FORCE_GENERIC, None),
         ("generic, in-kernel merge", _native.TF_ATTENTION_FLAG_FORCE_GENERIC, counters),
     ):
@@ -400,7 +400,7 @@ def test_stream_kernel_long_ranges_cross_page_windows(device, waves_per_cu):
         device=device,
     )
     out = torch.full_like(gpu.query, float("nan"))
-    flags = waves_per_cu << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT
+    flags = _native.TF_ATTENTION_FLAG_STREAM | (waves_per_cu << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
     _raw_decode(gpu, out, flags, 16384, 2, workspace, workspace.split_counters.data_ptr())
     torch.cuda.synchronize()
     assert int(workspace.split_counters.sum()) == 0
@@ -421,9 +421,9 @@ def test_stream_kernel_head_dims_and_pages(device, head_dim, block_size):
         batch_capacity=len(lengths), query_heads=16, head_dim=head_dim,
         max_context_length=1025, device=device,
     )
-    output = paged_gqa_decode_attention(
-        gpu.query, gpu.key_cache, gpu.value_cache, gpu.block_tables, gpu.context_lengths,
-        max_context_length=1025, workspace=workspace,
-    )
-    assert selected_attention_launch()["in_kernel_merge"] is True
+    output = torch.full_like(gpu.query, float("nan"))
+    _raw_decode(gpu, output, _native.TF_ATTENTION_FLAG_STREAM, 256, 5, workspace,
+                workspace.split_counters.data_ptr())
+    torch.cuda.synchronize()
+    assert int(workspace.split_counters.sum()) == 0
     _check_against_oracle(case, output.cpu(), 3e-3, 3e-3, f"D={head_dim} page={block_size}")
