@@ -19,12 +19,19 @@
 //    with zeros).  The online softmax runs on the accumulator layout, where
 //    a lane owns one head, so the running max/sum and the rescale of the
 //    output accumulator are lane-local.  P.V uses the same instruction with
-//    V^T as the A operand: V is staged in a per-wavefront LDS tile
-//    transposed to [head_dim][token] so each lane reads its 4+4 tokens of one
-//    dimension with two 8-byte LDS reads; P (converted to the storage type)
-//    is already in the B-operand layout.  K/V for the next chunk are loaded
+//    V^T as the A operand: the V rows are stored token-major into a
+//    per-wavefront LDS tile exactly as loaded, and ds_read_b64_tr_b16 reads
+//    them back transposed (lane = output dimension, 4 consecutive tokens),
+//    two reads per 16-dimension block; P (converted to the storage type) is
+//    already in the B-operand layout.  K/V for the next chunk are loaded
 //    before the current chunk is computed (two chunks in flight per wave).
 //    Wavefronts of a workgroup merge their (max, sum, acc) states in LDS.
+//    With arrival counters the last workgroup of a (row, kv head) to finish
+//    merges the split partials in the same launch.
+//
+//  * Streaming (opt-in, TF_ATTENTION_FLAG_STREAM): one wavefront per
+//    workgroup, equal contiguous ranges of 16-token tiles per wavefront
+//    over the whole batch, so ragged lengths cannot leave workgroups idle.
 //
 //  * Generic (any dtype, head_dim <= 256, group <= 64, any page size).  A
 //    straightforward LDS-tiled implementation kept for fp32 and unusual
@@ -293,9 +300,10 @@ paged_decode_mfma_kernel(AttnParams p) {
   constexpr int kRow = v_row_bytes<D>();
   __shared__ __attribute__((aligned(16))) unsigned char lds[mfma_lds_bytes<D, NW>()];
 
-  // blockIdx.x enumerates (row, kv head) so that consecutive workgroups --
-  // which the dispatcher deals round-robin to the 8 XCDs -- belong to
-  // different rows; the split index is the slow dimension.
+  // blockIdx.x enumerates (row, kv head) and the split index is the slow
+  // dimension: the first dispatches cover split 0 of every row (present in
+  // every non-empty row) before any later split, and the round-robin deal
+  // over the 8 XCDs gives each XCD an even mix of rows and splits.
   const int32_t b = blockIdx.x / p.kv_heads;
   const int32_t kvh = blockIdx.x - b * p.kv_heads;
   const int32_t split = blockIdx.y;
