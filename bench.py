@@ -3,20 +3,21 @@
 Workload: paged GQA decode attention at TinyLlama
 geometry -- 64 rows with context U[128, 2048] plus 8 zero-length rows,
 32 query / 4 KV heads, head_dim 64, 16-token pages on a seeded permutation,
-bf16, N(0,1) inputs, scale 1/8.  A step is one attention call (split stage +
-in-kernel log-sum-exp merge, one launch) over one batch.  To keep the 256 MB Infinity Cache from
-serving the K/V pages, steps rotate over several independent copies of the
-page pool (``--pools``), so every step streams its pages from HBM.
+bf16, N(0,1) inputs, scale 1/8.  A step is one attention call over one
+batch: the split stage (one wavefront per (row, kv head, split)) and the
+log-sum-exp merge launch, as the Python entry point issues them.  To keep
+the 256 MB Infinity Cache from serving the K/V pages, steps rotate over
+several independent copies of the page pool (``--pools``), so every step
+streams its pages from HBM.
 
 Prints ONE JSON line.  ``value`` is algorithmic GB/s of the whole call
 (byte model of benchmark/attention_benchmark.py:148-161: q, K, V, tables,
-output of the active rows) over the timed steps; ``roofline`` reports the
-one kernel of the call.  The K timed steps run as one HIP-graph replay
-bracketed by HIP events on the launch stream (a ctypes call costs the host
-longer than the kernel takes, so eager steps would time the host); with
-the in-kernel merge a step is one launch, so that time per step is the
-kernel's duration.  ``cpu_baseline`` is
-the CPU oracle on a bounded sample of the same rows, on this host's cores.
+output of the active rows) over the timed steps.  The K timed steps run as
+one HIP-graph replay bracketed by HIP events on the launch stream (a ctypes
+call costs the host longer than the kernel takes, so eager steps would
+time the host).  ``roofline`` reports the dominant kernel, the split stage,
+timed the same way from a graph of K split-stage launches alone.
+``cpu_baseline`` is the CPU oracle on the same rows, on this host's cores.
 """
 
 from __future__ import annotations
@@ -46,10 +47,12 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--pools", type=int, default=6, help="rotated K/V page pools")
-    parser.add_argument("--split-size", type=int, default=512,
-                        help="tokens per split-KV partition (multiple of 32)")
-    parser.add_argument("--merge", choices=("fused", "kernel"), default="fused",
-                        help="in-kernel merge (arrival counters) or a separate merge launch")
+    parser.add_argument("--split-size", type=int, default=0,
+                        help="tokens per split-KV partition (multiple of 32); 0: the "
+                             "per-call choice of the Python entry point")
+    parser.add_argument("--merge", choices=("fused", "kernel"), default="kernel",
+                        help="separate merge launch (the product path) or the in-kernel "
+                             "merge enabled by arrival counters")
     parser.add_argument("--cpu-seconds", type=float, default=10.0,
                         help="target CPU time of the oracle baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -127,11 +130,11 @@ def main() -> int:
 
     from tensorforge_amd import _native
     from tensorforge_amd.kernels import PagedAttentionWorkspace, set_attention_split_size
+    from tensorforge_amd.kernels.attention import attention_split_size_for
     from tensorforge_amd.workloads import decode_attention_bytes, tinyllama_decode_case
 
     device = torch.device("cuda", 0)
     lib = _native.library()
-    set_attention_split_size(args.split_size)
 
     case = tinyllama_decode_case(seed=0, dtype=torch.bfloat16)
     gpu = case.to(device)
@@ -142,7 +145,8 @@ def main() -> int:
     num_blocks, block_size, kv_heads, _ = gpu.key_cache.shape
     table_width = gpu.block_tables.shape[1]
     max_context = 2048
-    split_size = args.split_size
+    split_size = args.split_size or attention_split_size_for(max_context, batch, kv_heads)
+    set_attention_split_size(split_size)
     num_splits = math.ceil(max_context / split_size)
     workspace = PagedAttentionWorkspace.allocate(
         batch_capacity=batch, query_heads=query_heads, head_dim=head_dim,
@@ -159,9 +163,9 @@ def main() -> int:
     fused = args.merge == "fused"
 
     def attention_call(pool: int, handle: int) -> None:
-        # The product path, tf_paged_gqa_decode: with arrival counters one
-        # launch whose last workgroup per (row, kv head) merges; without them
-        # the split kernel is followed by the merge kernel.
+        # tf_paged_gqa_decode: without arrival counters (the product path)
+        # the split kernel is followed by the merge kernel; with them one
+        # launch whose last wavefront per (row, kv head) merges.
         key_cache, value_cache = pools[pool]
         _native.check(lib.tf_paged_gqa_decode(
             gpu.query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
@@ -191,7 +195,7 @@ def main() -> int:
 
     # Gate before timing: the benchmarked raw call must equal the Python entry
     # point (the parity tests check that entry point) -- bit for bit on the
-    # product path, up to rounding for the separate-merge alternative.
+    # product path, up to rounding for the in-kernel merge alternative.
     eager = stream.cuda_stream
     attention_call(0, eager)
     torch.cuda.synchronize()
@@ -202,9 +206,9 @@ def main() -> int:
         scale=case.scale, max_context_length=max_context, workspace=workspace,
     )
     torch.cuda.synchronize()
-    if fused:
+    if not fused:
         agree = torch.equal(check.view(torch.int16), output.view(torch.int16))
-    else:  # a different kernel sequence: equal up to rounding
+    else:  # a different merge order: equal up to rounding
         agree = float((check.float() - output.float()).abs().max()) < 2e-2
     if not agree:
         print(json.dumps({"error": "raw C-ABI call and the Python entry point disagree"}))
@@ -247,22 +251,28 @@ def main() -> int:
     # Kernel duration for the roofline.  With the in-kernel merge a step is
     # exactly one launch, so the graph replay's time per step is the
     # kernel's duration (plus the graph's inter-launch gap).  With the
-    # separate merge the split-stage launch of each of K eager steps is
-    # bracketed by its own pair of HIP events on the launch stream.
+    # separate merge, K split-stage launches alone are captured in a second
+    # graph and timed the same way.
     if fused:
         split_ms = ms_per_step
         kernel_timing = "HIP events around the timed graph replay; one launch per step"
     else:
-        begin = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-        split_end = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-        for step in range(args.steps):
-            begin[step].record(stream)
-            split_stage(step % args.pools, eager)
-            split_end[step].record(stream)
-            merge_stage(eager)
+        split_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(split_graph, stream=capture_stream):
+            for step in range(args.steps):
+                split_stage(step % args.pools, capture_stream.cuda_stream)
+        stream.wait_stream(capture_stream)
+        split_graph.replay()
         torch.cuda.synchronize()
-        split_ms = sum(begin[i].elapsed_time(split_end[i]) for i in range(args.steps)) / args.steps
-        kernel_timing = "HIP events around each of K eager split-stage launches"
+        split_begin = torch.cuda.Event(enable_timing=True)
+        split_end = torch.cuda.Event(enable_timing=True)
+        split_begin.record(stream)
+        split_graph.replay()
+        split_end.record(stream)
+        torch.cuda.synchronize()
+        split_ms = split_begin.elapsed_time(split_end) / args.steps
+        kernel_timing = ("HIP events around a graph replay of K split-stage launches "
+                         "(the merge launch excluded)")
 
     lengths = case.lengths
     nbytes = decode_attention_bytes(lengths, query_heads, kv_heads, head_dim, block_size, 2)
@@ -299,7 +309,7 @@ def main() -> int:
             "split_size": split_size,
             "num_splits": num_splits,
             "kv_pools_rotated": args.pools,
-            "merge": "in-kernel (arrival counters)" if fused else "separate merge kernel",
+            "merge": "in-kernel (arrival counters)" if fused else "separate merge launch",
             "algorithmic_bytes_per_call": nbytes,
         },
         "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
@@ -312,6 +322,7 @@ def main() -> int:
             "traffic": traffic,
             "kernel": "paged_decode_mfma_kernel"
             + (" (split stage with in-kernel merge)" if fused else " (split stage)"),
+            "merge_ms": None if fused else round(ms_per_step - split_ms, 6),
             "timing": kernel_timing,
             "kernel_ms": round(split_ms, 6),
         },

@@ -59,13 +59,16 @@ enum tf_attention_variant {
  * STREAM (MFMA family, split_counters given, num_splits >= 2) replaces the
  * one-workgroup-per-split grid by a balanced streaming kernel: equal
  * contiguous ranges of 16-token tiles per wavefront whatever the length
- * distribution.  Bits 8-15: streaming wavefronts per compute unit; bits
- * 16-19: tiles in flight per streaming wavefront (2..4); 0 selects the
- * defaults. */
+ * distribution.  Tuning fields (0 selects the defaults):
+ *   bits 8-15   grid kernel: wavefronts per kv head (heads x this <= 8);
+ *               streaming kernel: wavefronts per compute unit
+ *   bits 16-19  streaming kernel: tiles in flight per wavefront (2..4)
+ *   bits 20-23  grid kernel: kv heads per workgroup (must divide kv_heads) */
 #define TF_ATTENTION_FLAG_FORCE_GENERIC 1
 #define TF_ATTENTION_FLAG_STREAM 4
 #define TF_ATTENTION_WAVES_PER_CU_SHIFT 8
 #define TF_ATTENTION_DEPTH_SHIFT 16
+#define TF_ATTENTION_HEADS_PER_WG_SHIFT 20
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char *tf_last_error(void);

@@ -83,6 +83,9 @@ struct AttnParams {
   int32_t num_splits;
   int32_t partial_stride;
   int32_t max_tokens;  // min(num_splits * split_size, table_width * block_size)
+  int64_t partial_rows;    // rows the partial buffers hold
+  int32_t heads_per_wg;    // MFMA grid kernel: kv heads served by one workgroup
+  int32_t waves_per_head;  // MFMA grid kernel: wavefronts sharing one kv head
   float scale_log2;
 };
 
@@ -118,14 +121,13 @@ __device__ __forceinline__ bool writes_output(const AttnParams &p) {
 }
 
 // Rows of length zero produce zeros, written by their split-0 workgroup
-// whenever no merge launch follows.
+// whenever no merge launch follows: query heads [qh0, qh0 + nheads).
 template <typename T>
-__device__ void zero_rows(const AttnParams &p, int32_t b, int32_t kvh) {
+__device__ void zero_rows(const AttnParams &p, int32_t b, int32_t qh0, int32_t nheads) {
   if (!writes_output(p)) return;
   T *out = static_cast<T *>(p.output) +
-           (static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(kvh) * p.group) *
-               p.head_dim;
-  for (int i = threadIdx.x; i < p.group * p.head_dim; i += blockDim.x) out[i] = from_float<T>(0.f);
+           (static_cast<int64_t>(b) * p.query_heads + qh0) * p.head_dim;
+  for (int i = threadIdx.x; i < nheads * p.head_dim; i += blockDim.x) out[i] = from_float<T>(0.f);
 }
 
 template <typename T>
@@ -133,18 +135,19 @@ __device__ __forceinline__ T *output_row(const AttnParams &p, int32_t b, int32_t
   return static_cast<T *>(p.output) + (static_cast<int64_t>(b) * p.query_heads + qh) * p.head_dim;
 }
 
-// Epilogue shared by both kernel families.  Every thread of the workgroup
-// calls it; thread t owns items idx = t + k * blockDim.x (k < MAXK) of the
-// group x head_dim result, and value_of(k, idx, m, l, num) yields the
+// Epilogue shared by both kernel families.  A workgroup finishes the query
+// heads [qh0, qh0 + nheads) of row b for its split.  Every thread calls it;
+// thread t owns items idx = t + k * blockDim.x (k < MAXK) of the
+// nheads x head_dim result, and value_of(k, idx, m, l, num) yields the
 // workgroup's base-2 max, sum and unnormalised numerator for that item.
 //
 //  * one pass, or a row with a single non-empty split in counter mode:
 //    write num / l to the output directly;
 //  * otherwise store the partial; in counter mode the workgroup then counts
-//    itself in and the last of the row's ceil(ctx / split_size) workgroups
-//    merges all partials of its (row, kv head) by log-sum-exp and resets the
-//    counter to zero, leaving it ready for the next call (no memset, so the
-//    call is graph-replay safe).
+//    itself in at split_counters[counter] and the last of the row's
+//    ceil(ctx / split_size) workgroups merges all partials of its heads by
+//    log-sum-exp and resets the counter to zero, leaving it ready for the
+//    next call (no memset, so the call is graph-replay safe).
 //
 // Cross-workgroup visibility without cache maintenance: partials are written
 // with agent-scope atomic stores, which on gfx950 write through the per-XCD
@@ -154,22 +157,23 @@ __device__ __forceinline__ T *output_row(const AttnParams &p, int32_t b, int32_t
 // which bypass the non-coherent caches.  No agent-scope fence is issued: on a
 // multi-XCD part such a fence writes back and invalidates the whole L2.
 template <typename T, int MAXK, typename F>
-__device__ __forceinline__ void finish(const AttnParams &p, int32_t b, int32_t kvh,
-                                       int32_t split, int32_t ctx, F value_of) {
-  const int G = p.group;
+__device__ __forceinline__ void finish(const AttnParams &p, int32_t b, int32_t qh0,
+                                       int32_t nheads, int64_t counter, int32_t split,
+                                       int32_t ctx, F value_of) {
   const int D = p.head_dim;
+  const int items = nheads * D;
   const int32_t nvalid = (ctx + p.split_size - 1) / p.split_size;
   const bool counters = p.num_splits > 1 && p.split_counters != nullptr;
   const bool direct = p.num_splits == 1 || (counters && nvalid == 1);
 #pragma unroll
   for (int k = 0; k < MAXK; ++k) {
     const int idx = threadIdx.x + k * blockDim.x;
-    if (idx < G * D) {
+    if (idx < items) {
       float m, l, num;
       value_of(k, idx, m, l, num);
       const int g = idx / D;
       const int d = idx - g * D;
-      const int32_t qh = kvh * G + g;
+      const int32_t qh = qh0 + g;
       if (direct) {
         output_row<T>(p, b, qh)[d] = from_float<T>(l > 0.f ? num / l : 0.f);
       } else {
@@ -197,35 +201,184 @@ __device__ __forceinline__ void finish(const AttnParams &p, int32_t b, int32_t k
   __builtin_amdgcn_s_waitcnt(0);  // this lane's partial stores have completed
   __syncthreads();                // ... and so have every other lane's
   if (threadIdx.x == 0) {
-    int32_t *counter = p.split_counters + static_cast<int64_t>(b) * p.kv_heads + kvh;
+    int32_t *slot = p.split_counters + counter;
     const int32_t prev =
-        __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     is_last = prev == nvalid - 1;
-    if (is_last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (is_last) __hip_atomic_store(slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!is_last) return;
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
+  // Merge: all loads of an item (nvalid <= 8 at a time) are issued before
+  // any is used, so the merge costs one round trip per 8 splits.
+  constexpr int kBatch = 8;
+  for (int idx = threadIdx.x; idx < items; idx += blockDim.x) {
     const int g = idx / D;
     const int d = idx - g * D;
-    const int32_t qh = kvh * G + g;
+    const int32_t qh = qh0 + g;
     const int64_t base = (static_cast<int64_t>(b) * p.query_heads + qh) * p.num_splits;
-    float gmax = kNegInf;
-    for (int32_t s = 0; s < nvalid; ++s)
-      gmax = fmaxf(gmax, __hip_atomic_load(p.partial_max + base + s, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT));
-    float num = 0.f, den = 0.f;
-    if (gmax != kNegInf) {
-      for (int32_t s = 0; s < nvalid; ++s) {
-        const float e = exp2f(__hip_atomic_load(p.partial_max + base + s, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT) - gmax);
-        den += e * __hip_atomic_load(p.partial_sum + base + s, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-        num += e * __hip_atomic_load(p.partial_acc + (base + s) * p.partial_stride + d,
-                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float gmax = kNegInf, num = 0.f, den = 0.f;
+    for (int32_t s0 = 0; s0 < nvalid; s0 += kBatch) {
+      float ms[kBatch], ls[kBatch], as[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int32_t sj = min(s0 + j, nvalid - 1);
+        ms[j] = __hip_atomic_load(p.partial_max + base + sj, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        ls[j] = __hip_atomic_load(p.partial_sum + base + sj, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        as[j] = __hip_atomic_load(p.partial_acc + (base + sj) * p.partial_stride + d,
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        if (s0 + j >= nvalid || ms[j] == kNegInf) continue;
+        // Running log-sum-exp over the batches (base 2).
+        if (ms[j] > gmax) {
+          const float r = fast_exp2(gmax - ms[j]);
+          num *= r;
+          den *= r;
+          gmax = ms[j];
+        }
+        const float e = fast_exp2(ms[j] - gmax);
+        den += e * ls[j];
+        num += e * as[j];
       }
     }
     output_row<T>(p, b, qh)[d] = from_float<T>(den > 0.f ? num / den : 0.f);
+  }
+}
+
+// Log-sum-exp merge of the nvalid split partials of (row b, kv head kvh) by
+// one wavefront, for the G query heads of the head.  Pass 1 loads every
+// (head, split) max and sum at once and leaves the normalised weights
+// exp2(m_s - M) / den in `scratch` (wavefront-private LDS, `capacity`
+// floats).  Pass 2 accumulates the weighted partial rows, 4 items x 8
+// splits of loads in flight per lane.  Partials are read with agent-scope
+// atomic loads (coherent across XCDs).  When the weights do not fit the
+// scratch, each item is merged on its own (slower, same result).
+template <typename T, int D>
+__device__ __forceinline__ void merge_head_partials(const AttnParams &p, int32_t b, int32_t kvh,
+                                                 int32_t nvalid, float *scratch,
+                                                 int32_t capacity) {
+  const int lane = threadIdx.x & 63;
+  const int32_t G = p.group;
+  const int64_t head0 = (static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(kvh) * G) *
+                        p.num_splits;  // partial row of (head 0 of the group, split 0)
+  const int32_t pairs = G * nvalid;
+  const int items = G * D;
+  if (2 * pairs <= capacity) {
+    float *wm = scratch;          // [G][nvalid] maxima, then weights
+    float *wl = scratch + pairs;  // [G][nvalid] sums
+    constexpr int kItems = 8, kSplits = 8;
+    float v[kItems][kSplits];
+    // Accumulator loads of items [64 k0, 64 (k0 + kItems)) x splits
+    // [s0, s0 + kSplits) of this lane (independent of the weights).
+    auto load_acc = [&](int k0, int32_t s0) {
+#pragma unroll
+      for (int i = 0; i < kItems; ++i) {
+        const int idx = min(lane + 64 * (k0 + i), items - 1);
+        const int g = idx / D;
+        const int d = idx - g * D;
+#pragma unroll
+        for (int j = 0; j < kSplits; ++j) {
+          const int32_t sj = min(s0 + j, nvalid - 1);
+          v[i][j] = __hip_atomic_load(
+              p.partial_acc + (head0 + static_cast<int64_t>(g) * p.num_splits + sj) *
+                                  p.partial_stride + d,
+              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    };
+    // Pass 1: the (head, split) maxima and sums, issued first; the first
+    // accumulator batch follows at once, so for G * D <= 512 and
+    // nvalid <= 8 the whole merge waits for memory once.
+    for (int32_t q0 = 0; q0 < pairs; q0 += 4 * 64) {
+      float mv[4], lv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int32_t q = min(q0 + j * 64 + lane, pairs - 1);
+        const int32_t g = q / nvalid;
+        const int64_t at = head0 + static_cast<int64_t>(g) * p.num_splits + (q - g * nvalid);
+        mv[j] = __hip_atomic_load(p.partial_max + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lv[j] = __hip_atomic_load(p.partial_sum + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (q0 == 0) load_acc(0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int32_t q = q0 + j * 64 + lane;
+        if (q < pairs) {
+          wm[q] = mv[j];
+          wl[q] = lv[j];
+        }
+      }
+    }
+    __asm__ volatile("" ::: "memory");
+    if (lane < G) {
+      float mmax = kNegInf;
+      for (int32_t s = 0; s < nvalid; ++s) mmax = fmaxf(mmax, wm[lane * nvalid + s]);
+      float den = 0.f;
+      if (mmax != kNegInf)
+        for (int32_t s = 0; s < nvalid; ++s)
+          den += wl[lane * nvalid + s] * fast_exp2(wm[lane * nvalid + s] - mmax);
+      const float inv = den > 0.f ? 1.f / den : 0.f;
+      for (int32_t s = 0; s < nvalid; ++s) {
+        const float m = wm[lane * nvalid + s];
+        wm[lane * nvalid + s] = m == kNegInf ? 0.f : fast_exp2(m - mmax) * inv;
+      }
+    }
+    __asm__ volatile("" ::: "memory");
+    for (int k0 = 0; k0 * 64 < items; k0 += kItems) {
+      float num[kItems];
+#pragma unroll
+      for (int i = 0; i < kItems; ++i) num[i] = 0.f;
+      for (int32_t s0 = 0; s0 < nvalid; s0 += kSplits) {
+        if (k0 > 0 || s0 > 0) load_acc(k0, s0);
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+          const int idx = min(lane + 64 * (k0 + i), items - 1);
+          const int g = idx / D;
+#pragma unroll
+          for (int j = 0; j < kSplits; ++j)
+            if (s0 + j < nvalid) num[i] += wm[g * nvalid + s0 + j] * v[i][j];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kItems; ++i) {
+        const int idx = lane + 64 * (k0 + i);
+        if (idx < items) {
+          const int g = idx / D;
+          output_row<T>(p, b, kvh * G + g)[idx - g * D] = from_float<T>(num[i]);
+        }
+      }
+    }
+    return;
+  }
+  // Fallback: one item at a time, all splits of the item in flight.
+  for (int idx = lane; idx < items; idx += 64) {
+    const int g = idx / D;
+    const int d = idx - g * D;
+    const int64_t base = head0 + static_cast<int64_t>(g) * p.num_splits;
+    float gmax = kNegInf, num = 0.f, den = 0.f;
+    for (int32_t s = 0; s < nvalid; ++s) {
+      const float m = __hip_atomic_load(p.partial_max + base + s, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+      const float l = __hip_atomic_load(p.partial_sum + base + s, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+      const float a = __hip_atomic_load(p.partial_acc + (base + s) * p.partial_stride + d,
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (m == kNegInf) continue;
+      if (m > gmax) {
+        const float r = fast_exp2(gmax - m);
+        num *= r;
+        den *= r;
+        gmax = m;
+      }
+      const float e = fast_exp2(m - gmax);
+      den += e * l;
+      num += e * a;
+    }
+    output_row<T>(p, b, kvh * G + g)[d] = from_float<T>(den > 0.f ? num / den : 0.f);
   }
 }
 
@@ -262,12 +415,12 @@ constexpr int kChunk = 32;  // tokens per wavefront step (two 16-row tiles)
 template <int D>
 constexpr int v_row_bytes() { return D * 2 + 16; }
 
-template <int D, int NW>
-constexpr int mfma_lds_bytes() {
-  // max(per-wave V tiles, cross-wave merge buffers for 16 heads)
-  return (NW * kChunk * v_row_bytes<D>()) > (NW * (16 * D + 32) * 4)
-             ? (NW * kChunk * v_row_bytes<D>())
-             : (NW * (16 * D + 32) * 4);
+// LDS of the MFMA grid kernel for `waves` wavefronts: max(per-wave V tiles,
+// cross-wave merge buffers for 16 heads).
+__host__ __device__ constexpr int mfma_lds_bytes(int head_dim, int waves) {
+  return (waves * kChunk * (head_dim * 2 + 16)) > (waves * (16 * head_dim + 32) * 4)
+             ? (waves * kChunk * (head_dim * 2 + 16))
+             : (waves * (16 * head_dim + 32) * 4);
 }
 
 // Rescale threshold of the lazy online softmax (base-2 units): the running
@@ -298,17 +451,30 @@ paged_decode_mfma_kernel(AttnParams p) {
   constexpr int KS = D / 32;  // k-steps of the score product
   constexpr int NB = D / 16;  // 16-dim blocks of the output
   constexpr int kRow = v_row_bytes<D>();
-  __shared__ __attribute__((aligned(16))) unsigned char lds[mfma_lds_bytes<D, NW>()];
+  // Dynamic LDS sized for the launch's wavefronts (mfma_lds_bytes).
+  extern __shared__ __attribute__((aligned(16))) unsigned char mfma_smem[];
+  unsigned char *lds = mfma_smem;
 
-  // blockIdx.x enumerates (row, kv head) and the split index is the slow
-  // dimension: the first dispatches cover split 0 of every row (present in
-  // every non-empty row) before any later split, and the round-robin deal
-  // over the 8 XCDs gives each XCD an even mix of rows and splits.
-  const int32_t b = blockIdx.x / p.kv_heads;
-  const int32_t kvh = blockIdx.x - b * p.kv_heads;
+  // blockIdx.x enumerates (row, kv-head group) and the split index is the
+  // slow dimension: the first dispatches cover split 0 of every row (present
+  // in every non-empty row) before any later split, and the round-robin
+  // deal over the 8 XCDs gives each XCD an even mix of rows and splits.
+  // Wavefront w serves kv head (group * HPW + w % HPW) and takes every
+  // WPH-th chunk of the split starting at w / HPW, so the HPW wavefronts of
+  // one sub-index read the slices of the same token rows at the same time:
+  // the cache row [token, kv head, head_dim] is fetched as a whole, not one
+  // head slice at a time from different workgroups.
+  const int32_t HPW = p.heads_per_wg;
+  const int32_t WPH = p.waves_per_head;
+  const int32_t NG = p.kv_heads / HPW;
+  const int32_t b = blockIdx.x / NG;
+  const int32_t grp = blockIdx.x - b * NG;
   const int32_t split = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int32_t hl = wave % HPW;   // head within the group
+  const int32_t sub = wave / HPW;  // chunk phase within the head
+  const int32_t kvh = grp * HPW + hl;
   const int l16 = lane & 15;
   const int q4 = lane >> 4;
   const int32_t s0 = split * p.split_size;
@@ -339,7 +505,7 @@ paged_decode_mfma_kernel(AttnParams p) {
   int32_t page_win = load_window(0);
 
   if (s0 >= ctx) {
-    if (split == 0) zero_rows<T>(p, b, kvh);
+    if (split == 0) zero_rows<T>(p, b, grp * HPW * p.group, HPW * p.group);
     return;
   }
   const int32_t s1 = min(s0 + p.split_size, ctx);
@@ -470,9 +636,9 @@ paged_decode_mfma_kernel(AttnParams p) {
     if (seg_first_tile != 0) page_win = load_window(seg_first_tile);
     const int32_t seg_s1 = min(seg_s0 + 16 * kSegmentTiles, s1);
     const int32_t seg_chunks = (seg_s1 - seg_s0 + kChunk - 1) / kChunk;
-    const int32_t mine = seg_chunks > wave ? (seg_chunks - wave + NW - 1) / NW : 0;
+    const int32_t mine = seg_chunks > sub ? (seg_chunks - sub + WPH - 1) / WPH : 0;
     if (mine == 0) continue;
-    auto chunk = [&](int32_t i) { return i < mine ? wave + i * NW : seg_chunks; };
+    auto chunk = [&](int32_t i) { return i < mine ? sub + i * WPH : seg_chunks; };
     load_kv(seg_first_tile, seg_s0, seg_s1, chunk(0), ka, va, vala);
     for (int32_t i = 0; i < mine; i += 2) {
       load_kv(seg_first_tile, seg_s0, seg_s1, chunk(i + 1), kb, vb, valb);
@@ -487,41 +653,115 @@ paged_decode_mfma_kernel(AttnParams p) {
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
 
-  // Cross-wave merge through LDS (the V tiles are dead after the barrier).
-  __syncthreads();
-  float *red_ml = reinterpret_cast<float *>(lds);  // [NW][2][16]
-  float *red_acc = red_ml + NW * 32;               // [NW][16][D]
-  if (q4 == 0) {
-    red_ml[wave * 32 + l16] = m_run;
-    red_ml[wave * 32 + 16 + l16] = l_run;
+  // Several wavefronts per head: the ones with sub > 0 hand their state to
+  // the sub == 0 wavefront of their head through LDS (the V tiles are dead
+  // after the first barrier).  Each lane combines the elements it owns, so
+  // the reads are independent.  The second barrier frees LDS again.
+  if (WPH > 1) {  // workgroup-uniform
+    __syncthreads();
+    float *xm = reinterpret_cast<float *>(lds);  // [waves][32]: m of 16 heads, then l
+    float *xa = xm + HPW * WPH * 32;             // [waves][64 lanes][D / 4]
+    constexpr int kLaneFloats = D / 4;
+    if (sub > 0) {
+      if (q4 == 0) {
+        xm[wave * 32 + l16] = m_run;
+        xm[wave * 32 + 16 + l16] = l_run;
+      }
+#pragma unroll
+      for (int n = 0; n < NB; ++n)
+        *reinterpret_cast<f32x4 *>(xa + (wave * 64 + lane) * kLaneFloats + 4 * n) = acc[n];
+    }
+    __syncthreads();
+    if (sub == 0) {
+      for (int32_t s = 1; s < WPH; ++s) {
+        const int w = hl + s * HPW;
+        const float mo = xm[w * 32 + l16];
+        const float lo = xm[w * 32 + 16 + l16];
+        f32x4 ao[NB];
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+          ao[n] = *reinterpret_cast<const f32x4 *>(xa + (w * 64 + lane) * kLaneFloats + 4 * n);
+        const float mn = fmaxf(m_run, mo);
+        const float a = m_run == kNegInf ? 0.f : fast_exp2(m_run - mn);
+        const float c = mo == kNegInf ? 0.f : fast_exp2(mo - mn);
+        m_run = mn;
+        l_run = l_run * a + lo * c;
+#pragma unroll
+        for (int n = 0; n < NB; ++n) acc[n] = acc[n] * a + ao[n] * c;
+      }
+    }
+    __syncthreads();
+    if (sub > 0) return;
   }
-#pragma unroll
-  for (int n = 0; n < NB; ++n)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red_acc[(wave * 16 + l16) * D + 16 * n + 4 * q4 + r] = acc[n][r];
-  __syncthreads();
 
-  constexpr int kMaxItems = (16 * D + NW * 64 - 1) / (NW * 64);
-  finish<T, kMaxItems>(p, b, kvh, split, ctx,
-                       [&](int, int idx, float &m, float &l, float &num) {
-                         const int g = idx / D;
-                         const int d = idx - g * D;
-                         float mmax = kNegInf;
+  // ---- per-wavefront epilogue for kv head kvh ----------------------------
+  // Lane (l16, q4) owns head l16 (if < G), dims 16n + 4q4 + r.
+  const int32_t G = p.group;
+  const int32_t nvalid = (ctx + p.split_size - 1) / p.split_size;
+  const bool counters = p.num_splits > 1 && p.split_counters != nullptr;
+  const bool direct = p.num_splits == 1 || (counters && nvalid == 1);
+  const bool head_ok = l16 < G;
+  const int32_t qh = kvh * G + l16;
+  if (direct) {
+    if (head_ok) {
+      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+      T *out = output_row<T>(p, b, qh);
 #pragma unroll
-                         for (int w = 0; w < NW; ++w) mmax = fmaxf(mmax, red_ml[w * 32 + g]);
-                         float acc_num = 0.f, den = 0.f;
-                         if (mmax != kNegInf) {
+      for (int n = 0; n < NB; ++n) {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        const t4 v = {from_float<T>(acc[n][0] * inv), from_float<T>(acc[n][1] * inv),
+                      from_float<T>(acc[n][2] * inv), from_float<T>(acc[n][3] * inv)};
+        *reinterpret_cast<t4 *>(out + 16 * n + 4 * q4) = v;
+      }
+    }
+    return;
+  }
+  // Partials: the accumulator tile goes through this wavefront's LDS area
+  // ([G][D] floats, <= 64 * D bytes, within the V staging tile) so that
+  // each store instruction writes consecutive floats of one partial row.
+  {
+    float *tile = reinterpret_cast<float *>(vt);
+    if (head_ok) {
 #pragma unroll
-                           for (int w = 0; w < NW; ++w) {
-                             const float e = fast_exp2(red_ml[w * 32 + g] - mmax);
-                             den += red_ml[w * 32 + 16 + g] * e;
-                             acc_num += red_acc[(w * 16 + g) * D + d] * e;
-                           }
-                         }
-                         m = mmax;
-                         l = den;
-                         num = acc_num;
-                       });
+      for (int n = 0; n < NB; ++n)
+        *reinterpret_cast<f32x4 *>(tile + l16 * D + 16 * n + 4 * q4) = acc[n];
+    }
+    __asm__ volatile("" ::: "memory");
+    const int64_t row0 = (static_cast<int64_t>(b) * p.query_heads + kvh * G) * p.num_splits + split;
+    for (int idx = lane; idx < G * D; idx += 64) {
+      const int g = idx / D;
+      const int d = idx - g * D;
+      float *dst = p.partial_acc + (row0 + static_cast<int64_t>(g) * p.num_splits) * p.partial_stride + d;
+      if (counters)
+        __hip_atomic_store(dst, tile[idx], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        *dst = tile[idx];
+    }
+    if (head_ok && q4 == 0) {
+      const int64_t row = row0 + static_cast<int64_t>(l16) * p.num_splits;
+      if (counters) {
+        __hip_atomic_store(p.partial_max + row, m_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.partial_sum + row, l_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        p.partial_max[row] = m_run;
+        p.partial_sum[row] = l_run;
+      }
+    }
+    __asm__ volatile("" ::: "memory");
+  }
+  if (!counters) return;
+  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's partial stores have completed
+  int32_t last = 0;
+  if (lane == 0) {
+    int32_t *slot = p.split_counters + static_cast<int64_t>(b) * p.kv_heads + kvh;
+    const int32_t prev =
+        __hip_atomic_fetch_add(slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev == nvalid - 1;
+    if (last) __hip_atomic_store(slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (__builtin_amdgcn_readfirstlane(last) == 0) return;
+  merge_head_partials<T, D>(p, b, kvh, nvalid, reinterpret_cast<float *>(vt),
+                            kChunk * kRow / static_cast<int>(sizeof(float)));
 }
 
 // ===========================================================================
@@ -597,10 +837,27 @@ __host__ __device__ inline size_t stream_meta_bytes(int32_t rows) {
   return (static_cast<size_t>(2 * rows + 1) * 4 + 15) / 16 * 16;
 }
 
-size_t stream_lds_bytes(int head_dim, int32_t heads_per_group, int32_t rows) {
+// Query blocks staged per page window: a unit's query heads are one
+// contiguous block of HU * head_dim elements; a window holds at most
+// stream_q_slots units (>= 2) within kStreamQBytes of LDS.
+constexpr int32_t kStreamQBytes = 8192;
+
+__host__ __device__ inline int32_t stream_q_slots(int32_t unit_heads, int32_t head_dim) {
+  const int32_t per_unit = unit_heads * head_dim * 2;
+  const int32_t slots = kStreamQBytes / per_unit;
+  return slots < 2 ? 2 : slots;
+}
+
+size_t stream_lds_bytes(int head_dim, int32_t heads_per_group, int32_t group, int32_t rows) {
   const size_t vtiles = static_cast<size_t>(heads_per_group) * 16 * (head_dim * 2 + 16);
   const size_t weights = 16 * 64 * sizeof(float);
-  return stream_meta_bytes(rows) + (vtiles > weights ? vtiles : weights);
+  const size_t transpose = 16 * static_cast<size_t>(head_dim) * sizeof(float);
+  size_t region = vtiles > weights ? vtiles : weights;
+  if (transpose > region) region = transpose;
+  const int32_t unit_heads = heads_per_group * group;
+  const size_t qbytes = static_cast<size_t>(stream_q_slots(unit_heads, head_dim)) * unit_heads *
+                        head_dim * 2;
+  return stream_meta_bytes(rows) + qbytes + region;
 }
 
 template <typename T, int D, int HG, int DEPTH>
@@ -619,9 +876,12 @@ paged_decode_stream_kernel(AttnParams p) {
   const int32_t R = p.batch;
   const int32_t NG = p.kv_heads / HG;  // head groups per row
   const int32_t G = p.group;
+  const int32_t HU = HG * G;  // query heads of a unit
+  const int32_t QSLOTS = stream_q_slots(HU, D);
   int32_t *rstart = reinterpret_cast<int32_t *>(stream_smem);  // [R + 1] first tile of row / NG
   int32_t *rctx = rstart + R + 1;                               // [R] clamped row length
-  unsigned char *vt = stream_smem + stream_meta_bytes(R);
+  T *qs = reinterpret_cast<T *>(stream_smem + stream_meta_bytes(R));  // [QSLOTS][HU][D] queries
+  unsigned char *vt = stream_smem + stream_meta_bytes(R) + static_cast<size_t>(QSLOTS) * HU * D * 2;
   float *weights = reinterpret_cast<float *>(vt);               // merge weights (after streaming)
 
   // ---- row lengths (all loads in flight together) and their prefix sum ------
@@ -665,11 +925,13 @@ paged_decode_stream_kernel(AttnParams p) {
   if (total == 0) return;
 
   // ---- this wavefront's range ----------------------------------------------
-  // At most min(slots, 64) pieces per unit: the merge keeps one weight per
-  // (head, piece) in LDS.
-  const int32_t slots = min(p.num_splits, 64);
-  const int32_t min_tiles = max(kStreamMinTiles, (nmax + slots - 2) / (slots - 1));
-  int64_t nw64 = total / min_tiles;
+  // Each wavefront owns two partial slots of HU = HG * G rows (its first and
+  // its last unit), so the partial buffers bound the wavefront count.  The
+  // range length is kept >= ceil(nmax / 62) tiles so that no unit spans
+  // more than 63 pieces (the merge keeps one weight per (head, piece) in
+  // a 64-wide LDS row).
+  const int32_t min_tiles = max(kStreamMinTiles, (nmax + 61) / 62);
+  int64_t nw64 = min<int64_t>(total / min_tiles, p.partial_rows / (2 * HU));
   if (nw64 < 1) nw64 = 1;
   const int32_t nw = static_cast<int32_t>(min<int64_t>(nw64, gridDim.x));
   const int32_t w = blockIdx.x;
@@ -692,7 +954,10 @@ paged_decode_stream_kernel(AttnParams p) {
   int32_t w_page = -1;     // physical page
   int32_t w_inpage = 0;    // token offset of the tile inside its page
   int32_t w_ntok = 0;      // present tokens of the tile (0..16)
+  int32_t w_row = 0;       // row (sequence) of the tile's unit
+  int32_t w_hg = 0;        // kv-head group of the tile's unit
   int32_t cont_unit = -1;  // unit of the first tile after the window, if in range
+  int32_t win_u0 = 0;      // unit in query slot 0
   auto find_unit = [&](int64_t g) {  // u with unit_start(u) <= g < unit_start(u + 1)
     int32_t lo = 0, hi = R;  // row b with NG * rstart[b] <= g < NG * rstart[b + 1]
     while (hi - lo > 1) {
@@ -703,28 +968,51 @@ paged_decode_stream_kernel(AttnParams p) {
     const int64_t rel = g - static_cast<int64_t>(NG) * rstart[lo];
     return lo * NG + static_cast<int32_t>(n > 0 ? rel / n : 0);
   };
+  // A window is the next (up to) 64 tiles of the range whose units have a
+  // query slot: units win_u0 .. win_u0 + QSLOTS - 1, whose query blocks are
+  // staged into LDS here, so tiles carry no query loads of their own.
   auto load_window = [&](int32_t first) {
     win = first;
-    win_count = min(64, range - first);
+    const int32_t avail = min(64, range - first);
+    const bool avail_lane = lane < avail;
+    const int64_t g = t_begin + first + (avail_lane ? lane : 0);
+    const int32_t u = find_unit(g);  // non-decreasing over the lanes
+    const int32_t u0 = __builtin_amdgcn_readfirstlane(u);
+    const bool in_range = avail_lane && u - u0 < QSLOTS;
+    win_count = __builtin_popcountll(__ballot(in_range));
+    win_u0 = u0;
     next = 0;
-    cont_unit = first + 64 < range ? find_unit(t_begin + first + 64) : -1;
-    const bool in_range = lane < win_count;
-    const int64_t g = t_begin + first + lane;
-    const int32_t u = in_range ? find_unit(g) : 0;
+    cont_unit = first + win_count < range ? find_unit(t_begin + first + win_count) : -1;
     w_unit = in_range ? u : -1;
     w_page = -1;
     w_ntok = 0;
     w_inpage = 0;
+    w_row = u / NG;
+    w_hg = u - w_row * NG;
     if (in_range) {
       const int32_t tile = static_cast<int32_t>(g - unit_start(u));
       const int32_t tok = 16 * tile;
-      const int32_t bb = u / NG;
+      const int32_t bb = w_row;
       const int32_t logical = p.page_shift >= 0 ? (tok >> p.page_shift) : (tok / p.block_size);
       const int32_t page = p.block_tables[static_cast<int64_t>(bb) * p.table_width + logical];
       w_inpage = tok - logical * p.block_size;
       const bool ok = page >= 0 && page < p.num_blocks;
       w_page = ok ? page : -1;
       w_ntok = ok ? min(16, rctx[bb] - tok) : 0;
+    }
+    // Query blocks of the window's units (16 bytes per lane and step).
+    const int32_t nq = __builtin_amdgcn_readlane(u, win_count - 1) - u0 + 1;
+    const int32_t chunks = HU * D / 8;
+    for (int32_t c = lane; c < nq * chunks; c += 64) {
+      const int32_t j = c / chunks;
+      const int32_t off = c - j * chunks;
+      const int32_t uj = u0 + j;
+      const int32_t bj = uj / NG;
+      const T *src = static_cast<const T *>(p.query) +
+                     (static_cast<int64_t>(bj) * p.query_heads + static_cast<int64_t>(uj - bj * NG) * HU) * D +
+                     8 * off;
+      *reinterpret_cast<vec8 *>(qs + static_cast<int64_t>(j) * HU * D + 8 * off) =
+          *reinterpret_cast<const vec8 *>(src);
     }
     // Complete the window's loads here, where no tile is in flight: a load
     // still pending at the streaming loop's entry would make the compiler
@@ -735,7 +1023,7 @@ paged_decode_stream_kernel(AttnParams p) {
 
   // ---- per-tile register sets -----------------------------------------------
   struct Set {
-    vec8 k[HG][KS], v[HG][KS], q[HG][KS];
+    vec8 k[HG][KS], v[HG][KS];
     uint32_t valid;  // bit t: token t of the tile is present
     int32_t unit;    // -1: no tile
   };
@@ -744,17 +1032,22 @@ paged_decode_stream_kernel(AttnParams p) {
   // the same loads read a stand-in line (cache element 0), so the load
   // sequence never branches and the wait counts stay exact.
   auto issue = [&](Set &st) {
-    const bool have = next < win_count;  // uniform
-    const int f = have ? next : 0;
-    next += have ? 1 : 0;
-    const int32_t unit = have ? __builtin_amdgcn_readlane(w_unit, f) : -1;
-    const int32_t ntok = have ? __builtin_amdgcn_readlane(w_ntok, f) : 0;
+    // next and win_count are wave-uniform; readfirstlane makes that visible
+    // to the compiler, so the selects below stay scalar and branch-free.
+    const int32_t nx = __builtin_amdgcn_readfirstlane(next);
+    const bool have = nx < __builtin_amdgcn_readfirstlane(win_count);
+    const int f = have ? nx : 0;
+    next = nx + (have ? 1 : 0);
+    const int32_t unit_f = __builtin_amdgcn_readlane(w_unit, f);
+    const int32_t ntok_f = __builtin_amdgcn_readlane(w_ntok, f);
+    const int32_t unit = have ? unit_f : -1;
+    const int32_t ntok = have ? ntok_f : 0;
     const int32_t page = __builtin_amdgcn_readlane(w_page, f);
     const int32_t inpage = __builtin_amdgcn_readlane(w_inpage, f);
     st.unit = unit;
     st.valid = ntok >= 16 ? 0xffffu : ((1u << ntok) - 1u);
-    const int32_t bb = have ? unit / NG : 0;
-    const int32_t hg = have ? unit - bb * NG : 0;
+    const int32_t hg_f = __builtin_amdgcn_readlane(w_hg, f);
+    const int32_t hg = have ? hg_f : 0;
     const int64_t tile_off =
         ntok > 0 ? (static_cast<int64_t>(page) * p.block_size + inpage) * token_bytes +
                        static_cast<int64_t>(hg) * HG * D * sizeof(T)
@@ -768,18 +1061,6 @@ paged_decode_stream_kernel(AttnParams p) {
         st.k[h][ks] = *reinterpret_cast<const vec8 *>(kbytes + tile_off + o);
         st.v[h][ks] = *reinterpret_cast<const vec8 *>(vbytes + tile_off + o);
       }
-    // Columns l16 >= G of the score MFMA repeat query head 0 of the group;
-    // their results are never stored, so no select (which would wait on the
-    // load) is needed.
-#pragma unroll
-    for (int h = 0; h < HG; ++h) {
-      const T *qrow = static_cast<const T *>(p.query) +
-                      (static_cast<int64_t>(bb) * p.query_heads +
-                       static_cast<int64_t>(hg * HG + h) * G + (l16 < G ? l16 : 0)) * D;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        st.q[h][ks] = *reinterpret_cast<const vec8 *>(qrow + 32 * ks + 8 * q4);
-    }
   };
 
   f32x4 acc[HG][NB];
@@ -803,8 +1084,15 @@ paged_decode_stream_kernel(AttnParams p) {
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
       f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+      {
+        // Query operand from the window's LDS slot; columns l16 >= G repeat
+        // head 0 of the group and their results are never stored.
+        const T *qrow = qs + (static_cast<int64_t>(st.unit - win_u0) * HU + h * G +
+                              (l16 < G ? l16 : 0)) * D;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) s = M::mma(st.k[h][ks], st.q[h][ks], s);
+        for (int ks = 0; ks < KS; ++ks)
+          s = M::mma(st.k[h][ks], *reinterpret_cast<const vec8 *>(qrow + 32 * ks + 8 * q4), s);
+      }
       float sc[4] = {s[0], s[1], s[2], s[3]};  // token 4q4 + r, query head l16
       if (partial) {
 #pragma unroll
@@ -851,43 +1139,63 @@ paged_decode_stream_kernel(AttnParams p) {
     }
   };
 
-  // Finish the piece of `unit` held in (m_run, l_run, acc).
+  // Partial slot of (wavefront wv, unit starting at tile u_first): 2 wv for
+  // the unit holding the first tile of wv's range, 2 wv + 1 for the one
+  // holding its last tile (when different).
+  auto piece_slot = [&](int32_t wv, int64_t u_first) -> int64_t {
+    const int64_t tb = static_cast<int64_t>(wv) * total / nw;
+    return 2 * static_cast<int64_t>(wv) + (u_first > tb ? 1 : 0);
+  };
+
+  // Finish the piece of `unit` held in (m_run, l_run, acc): the output when
+  // the unit lies inside this range, else a partial in this wavefront's
+  // slot, transposed through LDS so each store writes consecutive floats.
   auto flush = [&](int32_t unit) {
     const int32_t bb = unit / NG;
     const int32_t hg = unit - bb * NG;
     const int64_t u_first = unit_start(unit);
     const int32_t w0 = wave_of_tile(u_first, nw, total);
     const int32_t w1 = wave_of_tile(u_first + (rstart[bb + 1] - rstart[bb]) - 1, nw, total);
+    const int64_t slot_row = piece_slot(w, u_first) * HU;
+    float *xt = reinterpret_cast<float *>(vt);
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
       float l = l_run[h];
       l += __shfl_xor(l, 16, 64);
       l += __shfl_xor(l, 32, 64);
-      if (l16 < G) {
-        const int32_t qh = (hg * HG + h) * G + l16;
-        if (w0 == w1) {
-          T *out = output_row<T>(p, bb, qh);
+      if (w0 == w1) {
+        if (l16 < G) {
+          T *out = output_row<T>(p, bb, (hg * HG + h) * G + l16);
           const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
-          for (int n = 0; n < NB; ++n)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) out[16 * n + 4 * q4 + r] = from_float<T>(acc[h][n][r] * inv);
-        } else {
-          const int64_t row =
-              (static_cast<int64_t>(bb) * p.query_heads + qh) * p.num_splits + (w - w0);
-          float *dst = p.partial_acc + row * p.partial_stride;
-#pragma unroll
-          for (int n = 0; n < NB; ++n)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              __hip_atomic_store(dst + 16 * n + 4 * q4 + r, acc[h][n][r], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-          if (q4 == 0) {
-            __hip_atomic_store(p.partial_max + row, m_run[h], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(p.partial_sum + row, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          for (int n = 0; n < NB; ++n) {
+            typedef T t4 __attribute__((ext_vector_type(4)));
+            const t4 v = {from_float<T>(acc[h][n][0] * inv), from_float<T>(acc[h][n][1] * inv),
+                          from_float<T>(acc[h][n][2] * inv), from_float<T>(acc[h][n][3] * inv)};
+            *reinterpret_cast<t4 *>(out + 16 * n + 4 * q4) = v;
           }
         }
+      } else {
+        __asm__ volatile("" ::: "memory");
+        if (l16 < G) {
+#pragma unroll
+          for (int n = 0; n < NB; ++n)
+            *reinterpret_cast<f32x4 *>(xt + l16 * D + 16 * n + 4 * q4) = acc[h][n];
+        }
+        __asm__ volatile("" ::: "memory");
+        const int64_t row0 = slot_row + h * G;
+        for (int idx = lane; idx < G * D; idx += 64) {
+          const int g = idx / D;
+          __hip_atomic_store(p.partial_acc + (row0 + g) * p.partial_stride + (idx - g * D),
+                             xt[idx], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (l16 < G && q4 == 0) {
+          __hip_atomic_store(p.partial_max + row0 + l16, m_run[h], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(p.partial_sum + row0 + l16, l, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __asm__ volatile("" ::: "memory");
       }
     }
     if (w0 != w1) {
@@ -899,34 +1207,58 @@ paged_decode_stream_kernel(AttnParams p) {
     reset();
   };
 
-  // Log-sum-exp merge of the `pieces` partials of unit (bb, hg) by the
-  // whole wavefront, 16 query heads at a time.  Pass 1: lanes (head, piece
-  // mod lph) load the partial maxima and sums (all in flight at once),
-  // reduce them per head and leave the weights exp2(m_s - M) / den in LDS.
-  // Pass 2: lanes over (head, dim) accumulate the weighted partial rows
-  // with independent loads.  Partials are read with agent-scope atomic
-  // loads (coherent across XCDs).
-  auto merge_unit = [&](int32_t bb, int32_t hg, int32_t pieces) {
-    const int32_t heads = HG * G;  // query heads of the unit
-    const int32_t qh0 = hg * HG * G;
-    for (int32_t hb = 0; hb < heads; hb += 16) {
-      const int32_t nh = min(16, heads - hb);
+  // Log-sum-exp merge of the pieces of unit (bb, hg), held by wavefronts
+  // w0..w1, by the whole wavefront, 16 query heads at a time.  Pass 1:
+  // lanes (head, piece mod lph) load the partial maxima and sums (all in
+  // flight at once), reduce them per head and leave the weights
+  // exp2(m_s - M) / den in LDS.  Pass 2: lanes over (head, dim) accumulate
+  // the weighted partial rows with SB pieces of loads in flight.  Partials
+  // are read with agent-scope atomic loads (coherent across XCDs).
+  auto merge_unit = [&](int32_t bb, int32_t hg, int32_t w0, int32_t w1, int64_t u_first) {
+    const int32_t pieces = w1 - w0 + 1;  // <= 63
+    const int32_t qh0 = hg * HU;
+    for (int32_t hb = 0; hb < HU; hb += 16) {
+      const int32_t nh = min(16, HU - hb);
       const int gp = nh <= 1 ? 1 : nh <= 2 ? 2 : nh <= 4 ? 4 : nh <= 8 ? 8 : 16;
       const int lph = 64 / gp;  // lanes per head
       const int g = lane / lph;
       const int j = lane - g * lph;
       const bool head_ok = g < nh;
-      const int64_t hbase =
-          (static_cast<int64_t>(bb) * p.query_heads + qh0 + hb + (head_ok ? g : 0)) * p.num_splits;
+      constexpr int kItems = (16 * D + 63) / 64;
+      constexpr int SB = kItems >= 64 ? 1 : 64 / kItems;  // pieces of loads in flight
+      // Loads of the accumulators of pieces [s0, s0 + SB) (independent of the
+      // weights, so the first batch is issued together with pass 1).
+      auto load_acc = [&](int32_t s0, float (&v)[SB][kItems]) {
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb) {
+          const int64_t base = piece_slot(w0 + min(s0 + sb, pieces - 1), u_first) * HU + hb;
+#pragma unroll
+          for (int k = 0; k < kItems; ++k) {
+            const int idx = lane + 64 * k;
+            const int gg = min(idx / D, nh - 1);
+            const int d = idx - (idx / D) * D;
+            v[sb][k] = __hip_atomic_load(p.partial_acc + (base + gg) * p.partial_stride + d,
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      };
+      float v[SB][kItems];
       float pm[16], ps[16];
+      const int pass1 = min(16, (pieces + lph - 1) / lph);  // uniform
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (k >= pass1) break;
+        const int32_t sidx = j + k * lph;
+        const bool ok = head_ok && sidx < pieces;
+        const int64_t at = piece_slot(w0 + (ok ? sidx : 0), u_first) * HU + hb + (head_ok ? g : 0);
+        pm[k] = __hip_atomic_load(p.partial_max + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ps[k] = __hip_atomic_load(p.partial_sum + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      load_acc(0, v);
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         const int32_t sidx = j + k * lph;
-        const bool ok = head_ok && sidx < pieces;
-        const int64_t at = hbase + (ok ? sidx : 0);
-        pm[k] = __hip_atomic_load(p.partial_max + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ps[k] = __hip_atomic_load(p.partial_sum + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (!ok) {
+        if (k >= pass1 || !(head_ok && sidx < pieces)) {
           pm[k] = kNegInf;
           ps[k] = 0.f;
         }
@@ -950,26 +1282,20 @@ paged_decode_stream_kernel(AttnParams p) {
           weights[g * 64 + sidx] = mloc != kNegInf ? fast_exp2(pm[k] - mloc) * inv : 0.f;
       }
       __asm__ volatile("" ::: "memory");
-      constexpr int kItems = (16 * D + 63) / 64;
       float num[kItems];
 #pragma unroll
       for (int k = 0; k < kItems; ++k) num[k] = 0.f;
-      for (int32_t sidx = 0; sidx < pieces; ++sidx) {
-        float v[kItems];
+      for (int32_t s0 = 0; s0 < pieces; s0 += SB) {
+        if (s0 > 0) load_acc(s0, v);
 #pragma unroll
-        for (int k = 0; k < kItems; ++k) {
-          const int idx = lane + 64 * k;
-          const int gg = min(idx / D, nh - 1);
-          const int d = idx - (idx / D) * D;
-          const int64_t row = (static_cast<int64_t>(bb) * p.query_heads + qh0 + hb + gg) * p.num_splits + sidx;
-          v[k] = __hip_atomic_load(p.partial_acc + row * p.partial_stride + d, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        }
+        for (int sb = 0; sb < SB; ++sb) {
+          if (s0 + sb >= pieces) break;
 #pragma unroll
-        for (int k = 0; k < kItems; ++k) {
-          const int idx = lane + 64 * k;
-          const int gg = min(idx / D, nh - 1);
-          num[k] += weights[gg * 64 + sidx] * v[k];
+          for (int k = 0; k < kItems; ++k) {
+            const int idx = lane + 64 * k;
+            const int gg = min(idx / D, nh - 1);
+            num[k] += weights[gg * 64 + s0 + sb] * v[sb][k];
+          }
         }
       }
 #pragma unroll
@@ -1016,32 +1342,42 @@ paged_decode_stream_kernel(AttnParams p) {
         if (step(st[3], st[0])) break;
       }
     }
-    if (win + 64 >= range) break;
-    load_window(win + 64);
+    if (win + win_count >= range) break;
+    load_window(win + win_count);
   }
 
   // ---- count the partial pieces in; the last arrival merges its unit ----------
+  // Lanes 0 and 1 count this wavefront in for its first and last pending
+  // unit with one atomic instruction; the wavefront then merges each unit
+  // for which it arrived last.
   if (pending_first < 0) return;
   __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wavefront has completed
-  for (int i = 0; i < 2; ++i) {
-    const int32_t unit = i == 0 ? pending_first : pending_last;
-    if (unit < 0) continue;
-    const int32_t bb = unit / NG;
-    const int32_t hg = unit - bb * NG;
-    const int64_t u_first = unit_start(unit);
-    const int32_t w0 = wave_of_tile(u_first, nw, total);
-    const int32_t w1 = wave_of_tile(u_first + (rstart[bb + 1] - rstart[bb]) - 1, nw, total);
-    const int32_t pieces = w1 - w0 + 1;  // <= 64
-    int32_t last = 0;
-    if (lane == 0) {
-      const int32_t prev =
-          __hip_atomic_fetch_add(p.split_counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = prev == pieces - 1;
-      if (last) __hip_atomic_store(p.split_counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  {
+    const int32_t my_unit = lane == 0 ? pending_first : (lane == 1 ? pending_last : -1);
+    int32_t arrived_last = 0;
+    if (my_unit >= 0) {
+      const int32_t bb = my_unit / NG;
+      const int64_t u_first = unit_start(my_unit);
+      const int32_t w0 = wave_of_tile(u_first, nw, total);
+      const int32_t w1 = wave_of_tile(u_first + (rstart[bb + 1] - rstart[bb]) - 1, nw, total);
+      const int32_t prev = __hip_atomic_fetch_add(p.split_counters + my_unit, 1, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+      arrived_last = prev == w1 - w0;
+      if (arrived_last)
+        __hip_atomic_store(p.split_counters + my_unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    last = __shfl(last, 0, 64);
-    if (!last) continue;
-    merge_unit(bb, hg, pieces);
+    const int32_t last0 = __builtin_amdgcn_readlane(arrived_last, 0);
+    const int32_t last1 = __builtin_amdgcn_readlane(arrived_last, 1);
+    for (int i = 0; i < 2; ++i) {
+      if ((i == 0 ? last0 : last1) == 0) continue;
+      const int32_t unit = i == 0 ? pending_first : pending_last;
+      const int32_t bb = unit / NG;
+      const int32_t hg = unit - bb * NG;
+      const int64_t u_first = unit_start(unit);
+      const int32_t w0 = wave_of_tile(u_first, nw, total);
+      const int32_t w1 = wave_of_tile(u_first + (rstart[bb + 1] - rstart[bb]) - 1, nw, total);
+      merge_unit(bb, hg, w0, w1, u_first);
+    }
   }
 }
 
@@ -1073,7 +1409,7 @@ paged_decode_generic_kernel(AttnParams p) {
   const int32_t ctx = clamp_context(p, b);
   const int32_t s0 = split * p.split_size;
   if (s0 >= ctx) {
-    if (split == 0) zero_rows<T>(p, b, kvh);
+    if (split == 0) zero_rows<T>(p, b, kvh * p.group, p.group);
     return;
   }
   const int32_t s1 = min(s0 + p.split_size, ctx);
@@ -1154,7 +1490,7 @@ paged_decode_generic_kernel(AttnParams p) {
     }
   }
   __syncthreads();
-  finish<T, kGenericMaxAcc>(p, b, kvh, split, ctx,
+  finish<T, kGenericMaxAcc>(p, b, kvh * G, G, static_cast<int64_t>(b) * p.kv_heads + kvh, split, ctx,
                             [&](int k, int idx, float &m, float &l, float &num) {
                               const int g = idx / D;
                               m = m_run[g];
@@ -1179,25 +1515,76 @@ merge_partials_kernel(const float *__restrict__ partial_max, const float *__rest
                       const int32_t *__restrict__ context_lengths, T *__restrict__ output,
                       int32_t query_heads, int32_t head_dim, int32_t split_size,
                       int32_t num_splits, int32_t partial_stride, int32_t max_tokens) {
+  // One wavefront per (row, query head).  Lane s holds the max and sum of
+  // split s (64 splits per pass); lanes over head_dim accumulate the
+  // weighted rows, kBatch splits of loads in flight.  The first batch is
+  // issued together with the max/sum loads (before the row length is
+  // known), so a row with <= kBatch splits costs one memory round trip;
+  // loads of splits past the row's last one are discarded by a select.
+  constexpr int kBatch = 16;
+  constexpr int kDims = 4;  // head_dim <= 256 = 4 x 64 lanes
+  const int lane = threadIdx.x;
   const int32_t qh = blockIdx.x;
   const int32_t b = blockIdx.y;
-  int32_t ctx = context_lengths[b];
-  if (ctx < 0) ctx = 0;
-  if (ctx > max_tokens) ctx = max_tokens;
-  const int32_t nvalid = (ctx + split_size - 1) / split_size;
   const int64_t base = (static_cast<int64_t>(b) * query_heads + qh) * num_splits;
   T *out = output + (static_cast<int64_t>(b) * query_heads + qh) * head_dim;
+  const int ndim = (head_dim + 63) / 64;
+  float v[kBatch][kDims];
+  auto load_batch = [&](int32_t s0) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int32_t sj = min(s0 + j, num_splits - 1);
+#pragma unroll
+      for (int k = 0; k < kDims; ++k) {
+        const int d = min(lane + 64 * k, head_dim - 1);
+        v[j][k] = k < ndim ? partial_acc[(base + sj) * partial_stride + d] : 0.f;
+      }
+    }
+  };
+  const int32_t first = min(lane, num_splits - 1);
+  float m = partial_max[base + first];
+  float l = partial_sum[base + first];
+  load_batch(0);
+  int32_t ctx = context_lengths[b];
+  ctx = ctx < 0 ? 0 : (ctx > max_tokens ? max_tokens : ctx);
+  const int32_t nvalid = (ctx + split_size - 1) / split_size;
+  // Max and sum over the valid splits (lanes beyond 64 splits in later passes).
   float gmax = kNegInf;
-  for (int32_t s = 0; s < nvalid; ++s) gmax = fmaxf(gmax, partial_max[base + s]);
+  for (int32_t s0 = 0; s0 < nvalid; s0 += 64) {
+    const float ms = s0 == 0 ? m : partial_max[base + min(s0 + lane, num_splits - 1)];
+    gmax = fmaxf(gmax, s0 + lane < nvalid ? ms : kNegInf);
+  }
+  gmax = wave_max(gmax);
   float den = 0.f;
-  if (gmax != kNegInf)
-    for (int32_t s = 0; s < nvalid; ++s) den += partial_sum[base + s] * exp2f(partial_max[base + s] - gmax);
-  for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
-    float num = 0.f;
-    if (gmax != kNegInf)
-      for (int32_t s = 0; s < nvalid; ++s)
-        num += partial_acc[(base + s) * partial_stride + d] * exp2f(partial_max[base + s] - gmax);
-    out[d] = from_float<T>(den > 0.f ? num / den : 0.f);
+  if (gmax != kNegInf) {
+    for (int32_t s0 = 0; s0 < nvalid; s0 += 64) {
+      const int32_t sl = min(s0 + lane, num_splits - 1);
+      const float ms = s0 == 0 ? m : partial_max[base + sl];
+      const float ls = s0 == 0 ? l : partial_sum[base + sl];
+      if (s0 + lane < nvalid && ms != kNegInf) den += ls * fast_exp2(ms - gmax);
+    }
+  }
+  den = wave_sum(den);
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  float num[kDims] = {0.f, 0.f, 0.f, 0.f};
+  for (int32_t s0 = 0; s0 < nvalid; s0 += kBatch) {
+    if (s0 > 0) load_batch(s0);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int32_t sj = s0 + j;
+      if (sj >= nvalid) break;
+      // Weight of split sj: its max comes from lane sj % 64 of the pass
+      // holding it (the first pass's values are in registers).
+      const float msj = sj < 64 ? __shfl(m, sj, 64) : partial_max[base + sj];
+      const float w = msj == kNegInf ? 0.f : fast_exp2(msj - gmax) * inv;
+#pragma unroll
+      for (int k = 0; k < kDims; ++k) num[k] += w * v[j][k];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kDims; ++k) {
+    const int d = lane + 64 * k;
+    if (k < ndim && d < head_dim) out[d] = from_float<T>(num[k]);
   }
 }
 
@@ -1214,11 +1601,33 @@ int32_t choose_variant(int32_t dtype, int32_t head_dim, int32_t group, int32_t b
   return TF_ATTENTION_MFMA;
 }
 
-constexpr int kMfmaWaves = 4;
+// Wavefronts per MFMA grid workgroup (upper bound; the launch uses
+// heads_per_wg * waves_per_head of them).
+constexpr int kMfmaWaves = 8;
+
+// Work split of the MFMA grid kernel: a workgroup serves HPW kv heads (the
+// largest divisor of kv_heads that is <= 8) with WPH = 8 / HPW wavefronts
+// per head.
+// Default: one wavefront per (row, kv head, split) -- measured fastest at
+// batch 64 x 2k (each wavefront finishes its own partial with no workgroup
+// barrier).  Flag bits 20-23 / 8-15 override HPW / WPH (tuning; HPW must
+// divide kv_heads and HPW * WPH <= 8).
+void mfma_geometry(AttnParams &p, int32_t flags) {
+  int32_t hpw = 1;
+  const int32_t want_hpw = (flags >> TF_ATTENTION_HEADS_PER_WG_SHIFT) & 0xf;
+  if (want_hpw > 0 && want_hpw <= kMfmaWaves && p.kv_heads % want_hpw == 0) hpw = want_hpw;
+  int32_t wph = 1;
+  const int32_t want_wph = (flags >> TF_ATTENTION_WAVES_PER_CU_SHIFT) & 0xff;
+  if (want_wph > 0 && want_wph * hpw <= kMfmaWaves) wph = want_wph;
+  p.heads_per_wg = hpw;
+  p.waves_per_head = wph;
+}
 
 template <typename T, int D>
 void launch_mfma(const AttnParams &p, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves>), grid, dim3(kMfmaWaves * 64), 0,
+  const int waves = p.heads_per_wg * p.waves_per_head;
+  const size_t lds = static_cast<size_t>(mfma_lds_bytes(D, waves));
+  hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves>), grid, dim3(waves * 64), lds,
                      stream, p);
 }
 
@@ -1300,6 +1709,9 @@ int32_t make_params(AttnParams &p, const void *query, const void *key_cache,
   int64_t max_tokens = split_tokens < table_tokens ? split_tokens : table_tokens;
   if (max_tokens > 0x7fffffff) max_tokens = 0x7fffffff;
   p.max_tokens = static_cast<int32_t>(max_tokens);
+  p.partial_rows = partial_capacity;
+  p.heads_per_wg = 1;
+  p.waves_per_head = 1;
   p.scale_log2 = scale * kLog2e;
   return TF_SUCCESS;
 }
@@ -1318,20 +1730,20 @@ int32_t device_compute_units() {
   return count;
 }
 
-// Heads per group: the largest power-of-two divisor of kv_heads whose
-// contiguous run of head_dim elements is at most 512 bytes... at least one
-// head; register sets then hold HG * head_dim elements per tile and lane.
-int32_t stream_heads_per_group(int32_t kv_heads, int32_t head_dim) {
-  int32_t hg = 1;
-  while (hg * 2 <= 4 && kv_heads % (hg * 2) == 0 && hg * 2 * head_dim * 2 <= 512) hg *= 2;
-  return hg;
+// Kv heads per streaming unit: 1 by default (measured as fast as grouping
+// and the lightest in registers); flag bits 20-23 may ask for 2 or 4 when
+// that divides kv_heads and HG * head_dim <= 256.
+int32_t stream_heads_per_group(int32_t kv_heads, int32_t head_dim, int32_t flags) {
+  const int32_t want = (flags >> TF_ATTENTION_HEADS_PER_WG_SHIFT) & 0xf;
+  if ((want == 2 || want == 4) && kv_heads % want == 0 && want * head_dim <= 256) return want;
+  return 1;
 }
 
 template <typename T, int D, int HG>
 void launch_stream_hg(const AttnParams &p, int32_t waves, int32_t depth, size_t lds,
                       hipStream_t stream) {
   // Deeper pipelines for the smaller register footprints.
-  constexpr int kMaxDepth = (D * HG <= 128) ? 4 : 3;
+  constexpr int kMaxDepth = (D * HG <= 128) ? 4 : 2;
   if (depth <= 2)
     hipLaunchKernelGGL((paged_decode_stream_kernel<T, D, HG, 2>), dim3(waves), dim3(64), lds, stream, p);
   else if (depth == 3 || kMaxDepth == 3)
@@ -1341,44 +1753,51 @@ void launch_stream_hg(const AttnParams &p, int32_t waves, int32_t depth, size_t 
 }
 
 template <typename T, int D>
-void launch_stream_dim(const AttnParams &p, int32_t waves, int32_t depth, hipStream_t stream) {
-  const int32_t hg = stream_heads_per_group(p.kv_heads, D);
-  const size_t lds = stream_lds_bytes(D, hg, p.batch);
+void launch_stream_dim(const AttnParams &p, int32_t hg, int32_t waves, int32_t depth,
+                       hipStream_t stream) {
+  const size_t lds = stream_lds_bytes(D, hg, p.group, p.batch);
   if (hg == 1) {
     launch_stream_hg<T, D, 1>(p, waves, depth, lds, stream);
-  } else if (hg == 2 || D == 128) {  // 128-dim heads group at most 2 (512 bytes)
+  } else if (hg == 2 || D == 128) {
     launch_stream_hg<T, D, 2>(p, waves, depth, lds, stream);
   } else if constexpr (D < 128) {
     launch_stream_hg<T, D, 4>(p, waves, depth, lds, stream);
   }
 }
 
-int32_t default_stream_depth(int32_t) { return 3; }
+int32_t default_stream_depth(int32_t head_dim, int32_t hg) { return head_dim * hg <= 128 ? 4 : 2; }
 
 template <typename T>
-void launch_stream(const AttnParams &p, int32_t waves, int32_t depth, hipStream_t stream) {
+void launch_stream(const AttnParams &p, int32_t hg, int32_t waves, int32_t depth,
+                   hipStream_t stream) {
   switch (p.head_dim) {
-    case 32: launch_stream_dim<T, 32>(p, waves, depth, stream); break;
-    case 64: launch_stream_dim<T, 64>(p, waves, depth, stream); break;
-    default: launch_stream_dim<T, 128>(p, waves, depth, stream); break;
+    case 32: launch_stream_dim<T, 32>(p, hg, waves, depth, stream); break;
+    case 64: launch_stream_dim<T, 64>(p, hg, waves, depth, stream); break;
+    default: launch_stream_dim<T, 128>(p, hg, waves, depth, stream); break;
   }
 }
+
+// Fewest wavefronts the streaming kernel is used with: below this the
+// partial buffers are too small for it and the grid kernel runs instead.
+constexpr int64_t kStreamMinWaves = 64;
 
 int32_t launch_split_stage(const AttnParams &p, int32_t dtype, int32_t flags, hipStream_t stream) {
   if (p.batch == 0) return TF_SUCCESS;
   {
     const int32_t variant = choose_variant(dtype, p.head_dim, p.group, p.block_size, flags);
+    const int32_t hg = stream_heads_per_group(p.kv_heads, p.head_dim, flags);
     if (variant == TF_ATTENTION_MFMA && (flags & TF_ATTENTION_FLAG_STREAM) && p.num_splits >= 2 &&
-        p.split_counters != nullptr && p.batch <= kStreamMaxRows) {
-      int32_t per_cu = (flags >> 8) & 0xff;
+        p.split_counters != nullptr && p.batch <= kStreamMaxRows &&
+        p.partial_rows / (2 * static_cast<int64_t>(hg) * p.group) >= kStreamMinWaves) {
+      int32_t per_cu = (flags >> TF_ATTENTION_WAVES_PER_CU_SHIFT) & 0xff;
       if (per_cu == 0) per_cu = kStreamWavesPerCu;
       const int32_t waves = device_compute_units() * per_cu;
-      int32_t depth = (flags >> 16) & 0xf;
-      if (depth == 0) depth = default_stream_depth(p.head_dim);
+      int32_t depth = (flags >> TF_ATTENTION_DEPTH_SHIFT) & 0xf;
+      if (depth == 0) depth = default_stream_depth(p.head_dim, hg);
       if (dtype == TF_DTYPE_BFLOAT16)
-        launch_stream<__bf16>(p, waves, depth, stream);
+        launch_stream<__bf16>(p, hg, waves, depth, stream);
       else
-        launch_stream<_Float16>(p, waves, depth, stream);
+        launch_stream<_Float16>(p, hg, waves, depth, stream);
       return check_launch("paged_gqa_decode (stream)");
     }
   }
@@ -1388,10 +1807,14 @@ int32_t launch_split_stage(const AttnParams &p, int32_t dtype, int32_t flags, hi
   // The MFMA kernel's tiles start at multiples of 16 tokens of a split.
   if (p.num_splits > 1 && p.split_size % 32 != 0) variant = TF_ATTENTION_GENERIC;
   if (variant == TF_ATTENTION_MFMA) {
+    AttnParams q = p;
+    mfma_geometry(q, flags);
+    const dim3 mgrid(static_cast<unsigned>(p.batch) * static_cast<unsigned>(p.kv_heads / q.heads_per_wg),
+                     static_cast<unsigned>(p.num_splits));
     if (dtype == TF_DTYPE_BFLOAT16)
-      launch_mfma_dim<__bf16>(p, grid, stream);
+      launch_mfma_dim<__bf16>(q, mgrid, stream);
     else
-      launch_mfma_dim<_Float16>(p, grid, stream);
+      launch_mfma_dim<_Float16>(q, mgrid, stream);
     return check_launch("paged_gqa_decode (mfma)");
   }
   if (p.group > 64 || p.group * p.head_dim > kGenericThreads * kGenericMaxAcc)

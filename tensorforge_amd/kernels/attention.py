@@ -20,12 +20,14 @@ from torch import Tensor
 
 from tensorforge_amd import _native
 
-# Tokens per split-KV partition (reference: triton_attention.py:46,406).  The
-# workspace capacity contract is sized for this value, so a smaller split
-# needs a workspace allocated for it.
+# Tokens per split-KV partition of the reference (triton_attention.py:46,406).
+# The workspace capacity contract is sized for this value, so a smaller split
+# needs a workspace allocated for it; larger ones fit any reference-sized
+# workspace.
 REFERENCE_SPLIT_SIZE = 256
 
-_SPLIT_SIZE = REFERENCE_SPLIT_SIZE
+# None: choose the partition size per call (attention_split_size_for).
+_SPLIT_SIZE: int | None = None
 _LAST_ATTENTION_CONFIG: dict[str, Any] | None = None
 _LAST_ATTENTION_LAUNCH: dict[str, Any] | None = None
 
@@ -88,23 +90,48 @@ def is_hip_attention_available() -> bool:
     return _native.is_available()
 
 
-def set_attention_split_size(split_size: int) -> int:
-    """Set the split-KV partition size (tokens) and return the previous one.
+def set_attention_split_size(split_size: int | None) -> int | None:
+    """Fix the split-KV partition size (tokens) and return the previous one.
 
-    Must be a positive multiple of 32.  Sizes below 256 need a workspace
+    A positive multiple of 32, or None for the per-call choice of
+    :func:`attention_split_size_for`.  Sizes below 256 need a workspace
     allocated with at least ``ceil(context / split_size)`` partials per head.
     """
 
     global _SPLIT_SIZE
-    if split_size <= 0 or split_size % 32 != 0:
+    if split_size is not None and (split_size <= 0 or split_size % 32 != 0):
         raise ValueError("split_size must be a positive multiple of 32")
     previous = _SPLIT_SIZE
     _SPLIT_SIZE = split_size
     return previous
 
 
-def attention_split_size() -> int:
+def attention_split_size() -> int | None:
+    """The fixed partition size, or None when it is chosen per call."""
+
     return _SPLIT_SIZE
+
+
+def attention_split_size_for(max_context_length: int, batch: int, kv_heads: int) -> int:
+    """Partition size chosen from host-known sizes only (no device sync).
+
+    One wavefront streams one (row, kv head, split) and the merge reads every
+    split's partial, so the size balances three things: enough wavefronts to
+    cover the GPU, few enough that their loads do not congest HBM (measured
+    best near 500-1300 wavefronts in flight on MI355X), and at most 16 splits
+    per row.  ``max(256, ceil64(L * B * Hkv / 1024), ceil64(L / 16))``: 576
+    for 72 rows x 4 kv heads at 2k, 2048 for 4 x 8 at 32k, and the
+    reference's 256 for short batches.
+    """
+
+    def ceil64(value: int) -> int:
+        return (value + 63) // 64 * 64
+
+    return max(
+        REFERENCE_SPLIT_SIZE,
+        ceil64(max_context_length * max(batch, 1) * kv_heads // 1024),
+        ceil64((max_context_length + 15) // 16),
+    )
 
 
 def paged_gqa_decode_attention(
@@ -188,7 +215,11 @@ def paged_gqa_decode_attention(
         raise ValueError("output must be contiguous and share query shape, dtype, and device")
     attention_scale = head_dim**-0.5 if scale is None else scale
 
-    split_size = _SPLIT_SIZE
+    split_size = (
+        _SPLIT_SIZE
+        if _SPLIT_SIZE is not None
+        else attention_split_size_for(launch_context, batch, kv_heads)
+    )
     use_split_kv = attention_path == "split_kv" or (
         attention_path == "auto" and launch_context > split_size
     )
@@ -231,16 +262,10 @@ def paged_gqa_decode_attention(
             workspace.partial_sum.numel(),
             workspace.partial_accumulator.shape[0],
         )
-        counters = workspace.split_counters
+        # The partials are merged by a second launch: measured faster on
+        # MI355X than the in-kernel merge that the workspace's arrival
+        # counters enable (the C ABI keeps both).
         counters_ptr = None
-        if (
-            counters is not None
-            and counters.device == device
-            and counters.dtype == torch.int32
-            and counters.is_contiguous()
-            and counters.numel() >= batch * kv_heads
-        ):
-            counters_ptr = counters.data_ptr()
         _native.check(
             _native.library().tf_paged_gqa_decode(
                 query.data_ptr(),

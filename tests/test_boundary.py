@@ -31,7 +31,7 @@ from tensorforge_amd.kernels import (
     set_attention_split_size,
     swiglu,
 )
-from tensorforge_amd.kernels.attention import attention_split_size
+from tensorforge_amd.kernels.attention import attention_split_size, attention_split_size_for
 from tensorforge_amd.workloads import (
     decode_attention_bytes,
     kv_append_bytes,
@@ -71,7 +71,8 @@ def test_library_exports_every_declared_symbol(lib) -> None:
 def test_header_constants_match_the_python_binding() -> None:
     text = HEADER.read_text()
     for name in ("TF_ATTENTION_FLAG_FORCE_GENERIC", "TF_ATTENTION_FLAG_STREAM",
-                 "TF_ATTENTION_WAVES_PER_CU_SHIFT", "TF_ATTENTION_DEPTH_SHIFT"):
+                 "TF_ATTENTION_WAVES_PER_CU_SHIFT", "TF_ATTENTION_DEPTH_SHIFT",
+                 "TF_ATTENTION_HEADS_PER_WG_SHIFT"):
         match = re.search(rf"#define {name} (\d+)", text)
         assert match and int(match.group(1)) == getattr(_native, name), name
     for name in ("TF_DTYPE_FLOAT32", "TF_DTYPE_FLOAT16", "TF_DTYPE_BFLOAT16",
@@ -208,9 +209,27 @@ def test_split_size_setting_is_validated_and_restorable() -> None:
             with pytest.raises(ValueError, match="multiple of 32"):
                 set_attention_split_size(bad)
         assert attention_split_size() == 512
+        assert set_attention_split_size(None) == 512
+        assert attention_split_size() is None
     finally:
-        assert set_attention_split_size(previous) == 512
+        set_attention_split_size(previous)
     assert attention_split_size() == previous
+
+
+def test_automatic_split_size() -> None:
+    """The per-call choice: the reference's 256 for its own split-KV test
+    case (1 x 8 heads at 2k, tests/test_decode_attention.py:158-162), 576
+    for 72 rows x 4 kv heads at 2k, 2048 for 4 x 8 kv heads at 32k; always
+    a multiple of 32 and >= 256."""
+
+    assert attention_split_size_for(2048, 1, 4) == 256
+    assert attention_split_size_for(2048, 72, 4) == 576
+    assert attention_split_size_for(32768, 4, 8) == 2048
+    for context in (1, 17, 300, 4096, 100000):
+        for batch in (1, 7, 64, 300):
+            size = attention_split_size_for(context, batch, 8)
+            assert size >= 256 and size % 32 == 0
+            assert -(-context // size) <= max(16, -(-context // 256))
 
 
 def test_workspace_capacity_contract() -> None:

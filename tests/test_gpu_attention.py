@@ -203,12 +203,13 @@ def test_group_and_head_dim_variants(device, query_heads, kv_heads, head_dim):
     _check_against_oracle(case, output.cpu(), 3e-3, 3e-3, f"G={query_heads // kv_heads} D={head_dim}")
 
 
-def _raw_decode(gpu, out, flags, split_size, num_splits, workspace, counters=None):
+def _raw_decode(gpu, out, flags, split_size, num_splits, workspace, counters=None, query=None):
+    query = gpu.query if query is None else query
     head_bucket = workspace.partial_accumulator.shape[1]
-    batch, query_heads, head_dim = gpu.query.shape
+    batch, query_heads, head_dim = query.shape
     num_blocks, block_size, kv_heads, _ = gpu.key_cache.shape
     status = _native.library().tf_paged_gqa_decode(
-        gpu.query.data_ptr(), gpu.key_cache.data_ptr(), gpu.value_cache.data_ptr(),
+        query.data_ptr(), gpu.key_cache.data_ptr(), gpu.value_cache.data_ptr(),
         gpu.block_tables.data_ptr(), gpu.context_lengths.data_ptr(), out.data_ptr(),
         workspace.partial_max.data_ptr(), workspace.partial_sum.data_ptr(),
         workspace.partial_accumulator.data_ptr(), counters, workspace.partial_max.numel(),
@@ -368,10 +369,8 @@ def test_in_kernel_merge_is_fresh_on_every_call(device):
                for _ in range(6)]
     fused_out = [torch.empty_like(gpu.query) for _ in queries]
     for q, out in zip(queries, fused_out):
-        paged_gqa_decode_attention(q, gpu.key_cache, gpu.value_cache, gpu.block_tables,
-                                   gpu.context_lengths, max_context_length=2048, output=out,
-                                   workspace=workspace)
-    assert selected_attention_launch()["in_kernel_merge"] is True
+        # The C ABI's in-kernel merge: arrival counters given.
+        _raw_decode(gpu, out, 0, 256, 8, workspace, workspace.split_counters.data_ptr(), query=q)
     for index, (q, out) in enumerate(zip(queries, fused_out)):
         separate = paged_gqa_decode_attention(q, gpu.key_cache, gpu.value_cache,
                                               gpu.block_tables, gpu.context_lengths,
