@@ -17,8 +17,10 @@
  *                            :268-316 log-sum-exp reduce)
  *   tf_paged_kv_write_token  tensorforge/kernels/triton_cache.py:68-133
  *                            (kernel :23-63)
- *   tf_paged_kv_write_slots  tensorforge/cache/paged.py:191-236
- *                            (PagedKVCache.write_layer multi-token scatter)
+ *   tf_paged_kv_write_slots  tensorforge/cache/paged.py:221-235
+ *                            (slot-mapping form of the multi-token scatter)
+ *   tf_paged_kv_write_range  tensorforge/cache/paged.py:191-236
+ *                            (PagedKVCache.write_layer through a table row)
  *   tf_rms_norm              tensorforge/kernels/triton_ops.py:179-205
  *   tf_residual_rms_norm     tensorforge/kernels/triton_ops.py:208-243
  *   tf_swiglu                tensorforge/kernels/triton_ops.py:246-260
@@ -172,6 +174,23 @@ int32_t tf_paged_kv_write_slots(
     const int64_t *slot_mapping, int32_t tokens, int32_t kv_heads,
     int32_t head_dim, int32_t num_blocks, int32_t block_size, int32_t dtype,
     void *stream);
+
+/*
+ * Append of `tokens` rows for one sequence at logical positions
+ * start_position .. start_position + tokens - 1 through the sequence's
+ * block-table row (table_width int32 entries):
+ *   cache token row (block_table[p / block_size], p % block_size) = row p - start
+ * keys/values [tokens, kv_heads, head_dim]; positions whose table entry is
+ * missing or outside the cache are skipped.  A bit-exact copy, one launch
+ * with no host-side index construction.  Replaces
+ * PagedKVCache.write_layer, cache/paged.py:212-235 (single-token copy_ and
+ * multi-token index_put).
+ */
+int32_t tf_paged_kv_write_range(
+    const void *keys, const void *values, void *key_cache, void *value_cache,
+    const int32_t *block_table, int32_t table_width, int32_t start_position,
+    int32_t tokens, int32_t kv_heads, int32_t head_dim, int32_t num_blocks,
+    int32_t block_size, int32_t dtype, void *stream);
 
 /*
  * Row-wise RMSNorm over [rows, columns]: y = x * rsqrt(mean(x^2) + eps) * w,

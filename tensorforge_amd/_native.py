@@ -70,6 +70,10 @@ SIGNATURES: dict[str, tuple[Any, ...]] = {
         _p, _p, _p, _p, _p,
         _i32, _i32, _i32, _i32, _i32, _i32, _p,
     ),
+    "tf_paged_kv_write_range": (
+        _p, _p, _p, _p, _p,
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p,
+    ),
     "tf_rms_norm": (_p, _p, _p, _i64, _i32, _f32, _i32, _p),
     "tf_residual_rms_norm": (_p, _p, _p, _p, _p, _i64, _i32, _f32, _i32, _p),
     "tf_swiglu": (_p, _p, _p, _i64, _i32, _p),

@@ -10,8 +10,8 @@
 // Reference semantics:
 //   single-token writer  tensorforge/kernels/triton_cache.py:23-63 (kernel),
 //                        :68-133 (host contract: masked lanes store nothing)
-//   multi-token append   tensorforge/cache/paged.py:221-235 (index_put of
-//                        T rows at positions start..start+T-1)
+//   multi-token append   tensorforge/cache/paged.py:212-235 (copy / index_put
+//                        of T rows at positions start..start+T-1)
 #include "tf_common.hpp"
 
 namespace tf {
@@ -34,6 +34,25 @@ struct TokenSlots {  // physical_blocks / block_offsets / active_mask (int32)
 struct MappedSlots {  // int64 slot mapping, negative = padded lane
   const int64_t *slots;
   __device__ __forceinline__ int64_t operator()(int64_t r) const { return slots[r]; }
+};
+
+// Rows start..start+T-1 of one sequence through its block-table row:
+// position p -> page table[p / block_size], offset p % block_size.  Entries
+// outside the table or the cache are skipped.
+struct RangeSlots {
+  const int32_t *table;
+  int32_t table_width;
+  int32_t start;
+  int32_t block_size;
+  int32_t num_blocks;
+  __device__ __forceinline__ int64_t operator()(int64_t r) const {
+    const int64_t pos = start + r;
+    const int64_t logical = pos / block_size;
+    if (logical >= table_width) return -1;
+    const int32_t page = table[logical];
+    if (page < 0 || page >= num_blocks) return -1;
+    return static_cast<int64_t>(page) * block_size + (pos - logical * block_size);
+  }
 };
 
 // grid.x covers the 2 * row_units units of one row (K then V), grid.y rows.
@@ -140,4 +159,25 @@ extern "C" int32_t tf_paged_kv_write_slots(
   return launch_scatter(keys, values, key_cache, value_cache, slots, tokens, row_bytes,
                         static_cast<int64_t>(num_blocks) * block_size,
                         static_cast<hipStream_t>(stream), "paged_kv_write_slots");
+}
+
+extern "C" int32_t tf_paged_kv_write_range(
+    const void *keys, const void *values, void *key_cache, void *value_cache,
+    const int32_t *block_table, int32_t table_width, int32_t start_position, int32_t tokens,
+    int32_t kv_heads, int32_t head_dim, int32_t num_blocks, int32_t block_size, int32_t dtype,
+    void *stream) {
+  using namespace tf;
+  clear_error();
+  if (int32_t s = check_geometry(keys, values, key_cache, value_cache, kv_heads, head_dim,
+                                 num_blocks, block_size, dtype))
+    return s;
+  if (tokens < 0 || start_position < 0 || table_width <= 0)
+    return fail(TF_ERROR_INVALID_ARGUMENT,
+                "tokens and start_position must be non-negative, table_width positive");
+  if (tokens > 0 && !block_table) return fail(TF_ERROR_INVALID_ARGUMENT, "null block table");
+  const int64_t row_bytes = static_cast<int64_t>(kv_heads) * head_dim * dtype_size(dtype);
+  RangeSlots slots{block_table, table_width, start_position, block_size, num_blocks};
+  return launch_scatter(keys, values, key_cache, value_cache, slots, tokens, row_bytes,
+                        static_cast<int64_t>(num_blocks) * block_size,
+                        static_cast<hipStream_t>(stream), "paged_kv_write_range");
 }

@@ -1,0 +1,157 @@
+"""Per-kernel timing of the decode hot path on one GPU.
+
+``python -m tensorforge_amd.kernel_bench`` prints one JSON line per case:
+
+* config 4 -- residual+RMSNorm and RMSNorm at T in {1, 8, 64, 256} tokens x
+  H in {2048, 4096} (eps 1e-5, weight N(1, 0.1)), SwiGLU at T x F in
+  {5632, 14336}, and the paged KV append of T tokens x 4 kv heads x 64
+  through ``PagedKVCache.write_layer`` starting mid-page, all bf16;
+* config 3 -- paged GQA decode attention at Llama-3-8B geometry (4 rows of
+  8k/16k/24k/32k, 32/8 heads, head_dim 128), split size chosen per call.
+
+Each case is captured as ``--calls`` launches in one HIP graph and timed by
+HIP events around one replay (a ctypes call costs the host longer than these
+kernels take).  Rates use the algorithmic byte models of
+``tensorforge_amd.workloads`` (the reference's models,
+benchmark/kernel_benchmark.py:144-158 and attention_benchmark.py:148-161).
+At decode token counts the fused ops are launch-bound: their time is
+dominated by the launch and the kernel's fixed start-up, not by HBM.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+from typing import Callable
+
+import torch
+
+from tensorforge_amd import workloads
+from tensorforge_amd.cache import PagedKVCache, PagedKVCacheConfig
+from tensorforge_amd.kernels import (
+    PagedAttentionWorkspace,
+    paged_gqa_decode_attention,
+    residual_rms_norm,
+    rms_norm,
+    selected_attention_autotune_config,
+    swiglu,
+)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def graph_time_us(run: Callable[[int], None], calls: int, device: torch.device) -> float:
+    """Average time per call of `calls` captured calls, replayed once."""
+
+    stream = torch.cuda.Stream(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream):
+        for i in range(3):
+            run(i)
+    torch.cuda.current_stream(device).wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(calls):
+            run(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    begin = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    begin.record()
+    graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return begin.elapsed_time(end) * 1e3 / calls
+
+
+def report(case: str, us: float, nbytes: int, **extra) -> None:
+    gbs = nbytes / (us * 1e-6) / 1e9
+    print(json.dumps({"case": case, "us_per_call": round(us, 3), "algorithmic_bytes": nbytes,
+                      "GB/s": round(gbs, 1), "hbm_fraction": round(gbs / HBM_PEAK_GBS, 4),
+                      **extra}), flush=True)
+
+
+def config4(device: torch.device, calls: int) -> None:
+    generator = torch.Generator().manual_seed(0)
+    dtype = torch.bfloat16
+
+    def randn(*shape, mean=0.0, std=1.0):
+        return (torch.randn(*shape, generator=generator) * std + mean).to(dtype).to(device)
+
+    for hidden in (2048, 4096):
+        weight = randn(hidden, mean=1.0, std=0.1)
+        for tokens in (1, 8, 64, 256):
+            x, r = randn(tokens, hidden), randn(tokens, hidden)
+            res_out, norm_out = torch.empty_like(x), torch.empty_like(x)
+            us = graph_time_us(lambda i: residual_rms_norm(
+                x, r, weight, 1e-5, residual_output=res_out, norm_output=norm_out), calls, device)
+            report(f"residual_rms_norm T={tokens} H={hidden}", us,
+                   workloads.rms_norm_bytes(tokens, hidden, 2, residual=True))
+            out = torch.empty_like(x)
+            us = graph_time_us(lambda i: rms_norm(x, weight, 1e-5, output=out), calls, device)
+            report(f"rms_norm T={tokens} H={hidden}", us,
+                   workloads.rms_norm_bytes(tokens, hidden, 2, residual=False))
+    for ffn in (5632, 14336):
+        for tokens in (1, 8, 64, 256):
+            gate, up = randn(tokens, ffn), randn(tokens, ffn)
+            out = torch.empty_like(gate)
+            us = graph_time_us(lambda i: swiglu(gate, up, output=out), calls, device)
+            report(f"swiglu T={tokens} F={ffn}", us, workloads.swiglu_bytes(tokens * ffn, 2))
+    for tokens in (1, 8, 64, 256):
+        config = PagedKVCacheConfig(num_layers=1, num_blocks=64, block_size=16, num_kv_heads=4,
+                                    head_dim=64, max_sequences=1, max_sequence_length=1024,
+                                    dtype=dtype, device=device)
+        cache = PagedKVCache(config)
+        cache.create_sequence("s")
+        head = cache.begin_append("s", 5)  # the timed append starts mid-page
+        cache.record_layer_write(head, 0)
+        cache.commit(head)
+        reservation = cache.begin_append("s", tokens)
+        keys, values = randn(tokens, 4, 64), randn(tokens, 4, 64)
+        us = graph_time_us(lambda i: cache.write_layer(reservation, 0, keys, values), calls,
+                           device)
+        report(f"kv_append T={tokens} (4 x 64, 16-token pages, straddling)", us,
+               workloads.kv_append_bytes(tokens, 4, 64, 2))
+
+
+def config3(device: torch.device, calls: int) -> None:
+    case = workloads.llama3_long_context_case(seed=0)
+    pools = [case.to(device) for _ in range(2)]  # 2 x 671 MB: the MALL cannot hold them
+    batch, query_heads, head_dim = case.query.shape
+    workspace = PagedAttentionWorkspace.allocate(
+        batch_capacity=batch, query_heads=query_heads, head_dim=head_dim,
+        max_context_length=32768, device=device)
+    output = torch.empty_like(pools[0].query)
+
+    def run(i: int) -> None:
+        gpu = pools[i % 2]
+        paged_gqa_decode_attention(gpu.query, gpu.key_cache, gpu.value_cache, gpu.block_tables,
+                                   gpu.context_lengths, scale=case.scale,
+                                   max_context_length=32768, output=output, workspace=workspace)
+
+    us = graph_time_us(run, calls, device)
+    nbytes = workloads.decode_attention_bytes(case.lengths, query_heads, 8, head_dim, 16, 2)
+    report("paged_gqa_decode cfg3 (4 x 8k..32k, 32/8 heads, D128, bf16)", us, nbytes,
+           record=selected_attention_autotune_config())
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--calls", type=int, default=100)
+    parser.add_argument("--only", choices=("cfg3", "cfg4"), default=None)
+    args = parser.parse_args()
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 1
+    device = torch.device("cuda", 0)
+    if args.only in (None, "cfg4"):
+        config4(device, args.calls)
+    if args.only in (None, "cfg3"):
+        config3(device, max(10, args.calls // 4))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
