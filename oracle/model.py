@@ -1,0 +1,76 @@
+"""CPU oracle of the Llama-style decoder the decode path serves.  TEST
+INFRASTRUCTURE ONLY (same import rule as oracle/reference.py).
+
+A full-prefix fp32 forward restating tensorforge/model/layers.py and
+model/llama.py: embedding, pre-norm blocks (RMSNorm :14-30, grouped-query
+causal attention with RoPE :33-143, SwiGLU MLP :146-158, residuals
+:161-171), final RMSNorm and the LM head.  Weights come from the same
+container the GPU path uses (tensorforge_amd.decode.DecoderWeights), read on
+the CPU in fp32.
+
+Pinning (tests/test_oracle_model.py): RoPE against its closed forms
+(identity at position 0, norm preservation, dot products depending only on
+the position difference, a hand-rotated pair); the last position's
+attention against paged_gqa_decode_reference over the same keys and values;
+the whole block against a pure-Python brute-force block on a tiny model.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from oracle.reference import rms_norm_reference
+
+
+def rope_tables(head_dim: int, theta: float, positions: Tensor) -> tuple[Tensor, Tensor]:
+    """cos/sin [len, head_dim] in fp32: angle(p, i) = p * theta^(-2i/D), the
+    half-dimension table repeated twice (layers.py:33-46)."""
+
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim))
+    angles = positions.double()[:, None] * inv_freq[None, :]
+    angles = torch.cat((angles, angles), dim=-1)
+    return angles.cos().float(), angles.sin().float()
+
+
+def rotate_half(x: Tensor) -> Tensor:
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+def apply_rope(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
+    """x [..., seq, D] with cos/sin [seq, D] (layers.py:49-60)."""
+
+    return x * cos + rotate_half(x) * sin
+
+
+def decoder_forward(weights, tokens: Tensor) -> Tensor:
+    """Logits [seq, vocab] (fp32) of a full causal forward over `tokens` [seq]."""
+
+    config = weights.config
+    f32 = lambda t: t.detach().cpu().float()  # noqa: E731
+    hq, hkv, d = config.num_attention_heads, config.num_key_value_heads, config.head_dim
+    group = hq // hkv
+    seq = tokens.shape[0]
+    x = f32(weights.embedding)[tokens.cpu()]
+    cos, sin = rope_tables(d, config.rope_theta, torch.arange(seq))
+    causal = torch.ones(seq, seq, dtype=torch.bool).triu(1)
+    for layer in weights.layers:
+        h = rms_norm_reference(x, f32(layer.input_norm), config.rms_norm_eps)
+        qkv = h @ f32(layer.qkv).T
+        q = qkv[:, : hq * d].view(seq, hq, d).transpose(0, 1)
+        k = qkv[:, hq * d: (hq + hkv) * d].view(seq, hkv, d).transpose(0, 1)
+        v = qkv[:, (hq + hkv) * d:].view(seq, hkv, d).transpose(0, 1)
+        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+        k = k.repeat_interleave(group, dim=0)
+        v = v.repeat_interleave(group, dim=0)
+        scores = (q @ k.transpose(-1, -2)) * d**-0.5
+        scores = scores.masked_fill(causal, float("-inf"))
+        context = torch.softmax(scores, dim=-1) @ v  # [hq, seq, d]
+        x = x + context.transpose(0, 1).reshape(seq, hq * d) @ f32(layer.o_proj).T
+        h = rms_norm_reference(x, f32(layer.post_norm), config.rms_norm_eps)
+        gate = h @ f32(layer.gate).T
+        up = h @ f32(layer.up).T
+        x = x + (torch.nn.functional.silu(gate) * up) @ f32(layer.down).T
+    h = rms_norm_reference(x, f32(weights.final_norm), config.rms_norm_eps)
+    return h @ f32(weights.lm_head).T

@@ -10,8 +10,13 @@ differs is the device work:
   count: the kernel resolves each position through the sequence's
   block-table row, where the reference builds index tensors with three
   launches plus an ``index_put`` per cache (cache/paged.py:212-235);
-* a block-table row is updated with one host-to-device copy instead of one
-  device write per entry (cache/paged.py:174-175, 253-255);
+* block tables and sequence lengths live on the host (the allocator's
+  authority) and reach the device with one copy per table, made only when a
+  device reader asks (``write_layer``, ``layer_view``, the ``block_tables``
+  and ``sequence_lengths`` attributes), where the reference issues one device
+  write per table entry and per length update (cache/paged.py:174-175,
+  253-258, 268-269, 290-291); a decode step that stages its own tables therefore
+  costs the cache no device work at all;
 * ``materialize`` gathers with one indexing operation.
 
 Page writes need the cache on a CUDA (HIP) device -- there is no CPU write
@@ -110,9 +115,11 @@ class SequenceLayout:
 @dataclass(slots=True)
 class _Sequence:
     slot: int
+    serial: int
     length: int = 0
     pages: list[int] = field(default_factory=list)
     pending: int | None = None  # id of the open reservation
+    truncations: int = 0  # bumped whenever pages are removed from the end
 
 
 @dataclass(slots=True)
@@ -126,22 +133,65 @@ class PagedKVCache:
     """Physical KV pages with per-request transactional appends
     (cache/paged.py:109-402)."""
 
-    def __init__(self, config: PagedKVCacheConfig) -> None:
+    def __init__(self, config: PagedKVCacheConfig, page_order: list[int] | None = None) -> None:
+        """``page_order`` (no reference counterpart): the order in which free
+        pages are handed out, e.g. a seeded permutation to exercise
+        non-contiguous tables; by default the lowest free page first, as in
+        the reference."""
+
         self.config = config
         shape = (config.num_layers, config.num_blocks, config.block_size, config.num_kv_heads,
                  config.head_dim)
         self.key_cache = torch.empty(shape, dtype=config.dtype, device=config.device)
         self.value_cache = torch.empty_like(self.key_cache)
-        self.block_tables = torch.full((config.max_sequences, config.max_blocks_per_sequence), -1,
-                                       dtype=torch.int32, device=config.device)
-        self.sequence_lengths = torch.zeros(config.max_sequences, dtype=torch.int32,
-                                            device=config.device)
-        self._free_pages = list(range(config.num_blocks))  # a heap: lowest page first
+        self._host_tables = torch.full((config.max_sequences, config.max_blocks_per_sequence), -1,
+                                       dtype=torch.int32)
+        self._host_lengths = torch.zeros(config.max_sequences, dtype=torch.int32)
+        self._tables_np = self._host_tables.numpy()
+        self._lengths_np = self._host_lengths.numpy()
+        if config.device.type == "cpu":
+            self._device_tables, self._device_lengths = self._host_tables, self._host_lengths
+        else:
+            self._device_tables = self._host_tables.to(config.device)
+            self._device_lengths = self._host_lengths.to(config.device)
+        self._stale = False
+        order = list(range(config.num_blocks)) if page_order is None else list(page_order)
+        if sorted(order) != list(range(config.num_blocks)):
+            raise ValueError("page_order must be a permutation of the page ids")
+        self._rank = {page: rank for rank, page in enumerate(order)}
+        self._page_of_rank = order
+        self._free_pages = list(range(config.num_blocks))  # heap of ranks: next page first
         self._free_slots = list(range(config.max_sequences))
         self._owner: list[str | None] = [None] * config.num_blocks
         self._sequences: dict[str, _Sequence] = {}
         self._pending: dict[int, _Pending] = {}
         self._next_id = 0
+        self._next_serial = 0
+
+    # -- device copies of the control state ---------------------------------
+    @property
+    def block_tables(self) -> Tensor:
+        """[max_sequences, max_blocks_per_sequence] int32 on the cache device
+        (-1 = unmapped), current as of this call."""
+
+        self._stage()
+        return self._device_tables
+
+    @property
+    def sequence_lengths(self) -> Tensor:
+        """[max_sequences] int32 committed lengths on the cache device."""
+
+        self._stage()
+        return self._device_lengths
+
+    def _stage(self) -> None:
+        # Pageable source: the copy completes before it returns, so later host
+        # edits cannot race it, and it is ordered after earlier device readers
+        # on the current stream.
+        if self._stale:
+            self._device_tables.copy_(self._host_tables)
+            self._device_lengths.copy_(self._host_lengths)
+            self._stale = False
 
     # -- allocation -------------------------------------------------------
     def create_sequence(self, request_id: str) -> None:
@@ -151,7 +201,9 @@ class PagedKVCache:
             raise ValueError(f"sequence already exists: {request_id}")
         if not self._free_slots:
             raise CacheExhaustedError("no free sequence slots")
-        self._sequences[request_id] = _Sequence(slot=heapq.heappop(self._free_slots))
+        self._sequences[request_id] = _Sequence(slot=heapq.heappop(self._free_slots),
+                                                serial=self._next_serial)
+        self._next_serial += 1
 
     def begin_append(self, request_id: str, token_count: int) -> AppendReservation:
         sequence = self._sequence(request_id)
@@ -167,7 +219,8 @@ class PagedKVCache:
             raise CacheExhaustedError(
                 f"KV cache needs {needed} blocks but only {len(self._free_pages)} are free"
             )
-        new_pages = [heapq.heappop(self._free_pages) for _ in range(max(needed, 0))]
+        new_pages = [self._page_of_rank[heapq.heappop(self._free_pages)]
+                     for _ in range(max(needed, 0))]
         for page in new_pages:
             if self._owner[page] is not None:
                 raise RuntimeError("allocator ownership corruption detected")
@@ -226,6 +279,12 @@ class PagedKVCache:
             raise IndexError("layer_index is out of range")
         pending.layers.add(layer_index)
 
+    def record_all_layers_written(self, reservation: AppendReservation) -> None:
+        """Mark every layer written at once (no reference counterpart: a
+        whole-model decode step writes all layers of its tokens together)."""
+
+        self._reservation(reservation).layers.update(range(self.config.num_layers))
+
     # -- transactions ---------------------------------------------------------
     def commit(self, reservation: AppendReservation, accepted_tokens: int | None = None) -> None:
         pending = self._reservation(reservation)
@@ -239,12 +298,14 @@ class PagedKVCache:
         keep = -(-sequence.length // self.config.block_size)
         dropped = sequence.pages[keep:]
         if dropped:
-            self.block_tables[sequence.slot, keep:keep + len(dropped)] = -1
+            self._tables_np[sequence.slot, keep:keep + len(dropped)] = -1
+            sequence.truncations += 1
             for page in dropped:
                 self._owner[page] = None
-                heapq.heappush(self._free_pages, page)
+                heapq.heappush(self._free_pages, self._rank[page])
             del sequence.pages[keep:]
-        self.sequence_lengths[sequence.slot] = sequence.length
+        self._lengths_np[sequence.slot] = sequence.length
+        self._stale = True
         sequence.pending = None
         del self._pending[reservation.reservation_id]
 
@@ -255,11 +316,13 @@ class PagedKVCache:
         sequence = self._sequence(reservation.request_id)
         first = len(sequence.pages) - len(pending.new_pages)
         if pending.new_pages:
-            self.block_tables[sequence.slot, first:len(sequence.pages)] = -1
+            self._tables_np[sequence.slot, first:len(sequence.pages)] = -1
+            self._stale = True
+            sequence.truncations += 1
             del sequence.pages[first:]
             for page in pending.new_pages:
                 self._owner[page] = None
-                heapq.heappush(self._free_pages, page)
+                heapq.heappush(self._free_pages, self._rank[page])
         sequence.pending = None
         del self._pending[reservation.reservation_id]
 
@@ -273,9 +336,10 @@ class PagedKVCache:
             if self._owner[page] != request_id:
                 raise RuntimeError("allocator ownership corruption detected")
             self._owner[page] = None
-            heapq.heappush(self._free_pages, page)
-        self.block_tables[sequence.slot].fill_(-1)
-        self.sequence_lengths[sequence.slot] = 0
+            heapq.heappush(self._free_pages, self._rank[page])
+        self._tables_np[sequence.slot] = -1
+        self._lengths_np[sequence.slot] = 0
+        self._stale = True
         heapq.heappush(self._free_slots, sequence.slot)
         del self._sequences[request_id]
 
@@ -290,6 +354,16 @@ class PagedKVCache:
         sequence = self._sequence(request_id)
         length = self._visible_length(request_id, sequence, reservation)
         return SequenceLayout(tuple(sequence.pages), length)
+
+    def page_list(self, request_id: str) -> tuple[list[int], tuple[int, int]]:
+        """The sequence's physical pages in logical order -- the live list,
+        which callers must not modify -- and a version key that changes when
+        the sequence is recreated or loses pages, so a caller mirroring the
+        row can append only the pages added since it last looked (no
+        reference counterpart: the decode executor's table staging)."""
+
+        sequence = self._sequence(request_id)
+        return sequence.pages, (sequence.serial, sequence.truncations)
 
     def append_location(self, reservation: AppendReservation,
                         token_offset: int = 0) -> CacheAppendLocation:
@@ -334,8 +408,8 @@ class PagedKVCache:
 
     # -- internals --------------------------------------------------------------
     def _write_table(self, slot: int, first: int, pages: list[int]) -> None:
-        row = torch.tensor(pages, dtype=torch.int32)
-        self.block_tables[slot, first:first + len(pages)].copy_(row)
+        self._tables_np[slot, first:first + len(pages)] = pages
+        self._stale = True
 
     def _visible_length(self, request_id: str, sequence: _Sequence,
                         reservation: AppendReservation | None) -> int:

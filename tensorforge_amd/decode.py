@@ -1,0 +1,598 @@
+"""Bucketed, HIP-graph-captured batched decode over the paged cache.
+
+The caller of the hot path (reference: runtime/decode_bucket.py:175-666).
+One decode step of a Llama-style decoder for up to ``batch_capacity``
+sequences runs as ONE captured HIP graph.  Per layer:
+
+* ``rms_norm`` (first layer) or the fused ``residual_rms_norm``;
+* a single fused QKV projection, then RoPE;
+* ``paged_kv_write_token`` for the new token;
+* ``paged_gqa_decode_attention`` (split stage + merge);
+* the output projection;
+* ``residual_rms_norm`` of (attention output, residual);
+* the gate and up projections, ``swiglu``, and the down projection.
+
+The gfx950 kernels of this package do the norm, cache and attention work;
+the GEMMs are library GEMMs (torch -> hipBLASLt).  Every per-step input
+lives in one device "control" slab, filled from one pinned host slab with
+one asynchronous copy per step.  So the graph's addresses never change,
+and a step needs no host synchronisation beyond reading back the sampled
+tokens.
+
+Lanes past the live batch are padded: context length 0, masked cache
+write.  Their attention output is zero and their sampled token is ignored.
+The model math follows tensorforge/model/layers.py (RMSNorm, RoPE with the
+half-split rotation, grouped-query attention, SwiGLU MLP, pre-norm
+residuals); weights are random (N(0, 0.02), norms 1), as in the reference's
+initialize_weights (layers.py:174-176).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+from torch import Tensor
+from torch.nn import functional as F
+
+from tensorforge_amd.cache import AppendReservation, PagedKVCache
+from tensorforge_amd.kernels import (
+    PagedAttentionWorkspace,
+    paged_gqa_decode_attention,
+    paged_kv_write_token,
+    residual_rms_norm,
+    rms_norm,
+    swiglu,
+)
+from tensorforge_amd.kernels.attention import attention_split_size_for, set_attention_split_size
+
+
+@dataclass(frozen=True, slots=True)
+class DecoderConfig:
+    vocab_size: int
+    hidden_size: int
+    intermediate_size: int
+    num_hidden_layers: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+    max_position_embeddings: int = 4096
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+
+def tinyllama_config() -> DecoderConfig:
+    """TinyLlama-1.1B geometry."""
+
+    return DecoderConfig(vocab_size=32000, hidden_size=2048, intermediate_size=5632,
+                         num_hidden_layers=22, num_attention_heads=32, num_key_value_heads=4)
+
+
+def small_config() -> DecoderConfig:
+    """4 layers, d_model 256, 8/2 heads (head_dim 32), FFN 768,
+    vocab 1024."""
+
+    return DecoderConfig(vocab_size=1024, hidden_size=256, intermediate_size=768,
+                         num_hidden_layers=4, num_attention_heads=8, num_key_value_heads=2,
+                         max_position_embeddings=512)
+
+
+@dataclass(slots=True)
+class LayerWeights:
+    input_norm: Tensor  # [H]
+    qkv: Tensor         # [(Hq + 2 Hkv) D, H]: q, k, v projections stacked
+    o_proj: Tensor      # [H, Hq D]
+    post_norm: Tensor   # [H]
+    gate: Tensor        # [F, H]
+    up: Tensor          # [F, H]
+    down: Tensor        # [H, F]
+
+
+@dataclass(slots=True)
+class DecoderWeights:
+    config: DecoderConfig
+    embedding: Tensor   # [V, H]
+    layers: list[LayerWeights]
+    final_norm: Tensor  # [H]
+    lm_head: Tensor     # [V, H]
+    rope_cos: Tensor    # [max_position, D] in the model dtype
+    rope_sin: Tensor
+
+    @classmethod
+    def random(cls, config: DecoderConfig, *, seed: int = 0, dtype: torch.dtype = torch.bfloat16,
+               device: torch.device | str = "cuda") -> DecoderWeights:
+        device = torch.device(device)
+        generator = torch.Generator(device=device).manual_seed(seed)
+
+        def normal(*shape: int) -> Tensor:
+            return (torch.randn(*shape, generator=generator, device=device,
+                                dtype=torch.float32) * 0.02).to(dtype)
+
+        def ones(size: int) -> Tensor:
+            return torch.ones(size, device=device, dtype=dtype)
+
+        h, f, d = config.hidden_size, config.intermediate_size, config.head_dim
+        hq, hkv = config.num_attention_heads, config.num_key_value_heads
+        layers = [
+            LayerWeights(input_norm=ones(h), qkv=normal((hq + 2 * hkv) * d, h),
+                         o_proj=normal(h, hq * d), post_norm=ones(h), gate=normal(f, h),
+                         up=normal(f, h), down=normal(h, f))
+            for _ in range(config.num_hidden_layers)
+        ]
+        # RoPE tables: angles in fp64, cos/sin rounded once to the model dtype
+        # (the reference computes them in fp32 and casts, layers.py:43-46).
+        inv_freq = 1.0 / (config.rope_theta ** (
+            torch.arange(0, d, 2, dtype=torch.float64) / d))
+        angles = torch.arange(config.max_position_embeddings, dtype=torch.float64)[:, None] * inv_freq
+        angles = torch.cat((angles, angles), dim=-1)
+        return cls(config=config, embedding=normal(config.vocab_size, h), layers=layers,
+                   final_norm=ones(h), lm_head=normal(config.vocab_size, h),
+                   rope_cos=angles.cos().to(dtype).to(device),
+                   rope_sin=angles.sin().to(dtype).to(device))
+
+
+def _rope(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
+    """x [B, heads, D]; cos/sin [B, D]: x cos + rotate_half(x) sin."""
+
+    half = x.shape[-1] // 2
+    rotated = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+    return x * cos[:, None, :] + rotated * sin[:, None, :]
+
+
+class DecodeGraphBucket:
+    """Static buffers and one captured HIP graph for a decode step of up to
+    ``batch_capacity`` sequences whose contexts stay within
+    ``context_capacity`` tokens (reference: _DecodeBucket,
+    decode_bucket.py:175-528).
+
+    Control state per lane: the input token (taken either from the host or,
+    on the device, from ``token_state[source_lane]`` -- the token the previous
+    step sampled in that lane, so a running request never round-trips its
+    token through the host), the position, the block-table row, the context
+    length, the append page/offset and the active flag.  The host keeps a
+    master copy and rewrites only what changed: a lane that decodes the same
+    request as last time gets just its newly appended pages.  Each step
+    copies the master into one of two pinned slabs and from there, with one
+    asynchronous copy per slab, to the device; a slab is reused only after
+    its previous copy has completed.
+    """
+
+    def __init__(self, weights: DecoderWeights, cache: PagedKVCache, *, batch_capacity: int,
+                 context_capacity: int, token_state: Tensor | None = None) -> None:
+        config = weights.config
+        self.weights = weights
+        self.cache = cache
+        self.batch_capacity = batch_capacity
+        self.context_capacity = context_capacity
+        device = cache.config.device
+        dtype = cache.config.dtype
+        width = cache.config.max_blocks_per_sequence
+        b = batch_capacity
+        self.device = device
+        # Long rows: host token, position, source lane.  Int32 segments: block
+        # tables [b, width], context lengths, append pages, page offsets,
+        # active flags.
+        self._ctl_long = np.zeros((3, b), dtype=np.int64)
+        self._ctl_int = np.zeros(b * (width + 4), dtype=np.int32)
+        self._ctl_int[:b * width] = -1
+        cuts = [b * width, b * (width + 1), b * (width + 2), b * (width + 3)]
+        self._host_views = (self._ctl_int[:cuts[0]].reshape(b, width), self._ctl_int[cuts[0]:cuts[1]],
+                            self._ctl_int[cuts[1]:cuts[2]], self._ctl_int[cuts[2]:cuts[3]],
+                            self._ctl_int[cuts[3]:])
+        self._pinned = [(torch.zeros((3, b), dtype=torch.long, pin_memory=True),
+                         torch.zeros(self._ctl_int.size, dtype=torch.int32, pin_memory=True))
+                        for _ in range(2)]
+        self._copied = [torch.cuda.Event(), torch.cuda.Event()]
+        self._copy_recorded = [False, False]
+        self._flip = 0
+        self._long = torch.zeros((3, b), dtype=torch.long, device=device)
+        self._int = torch.zeros(self._ctl_int.size, dtype=torch.int32, device=device)
+        self.host_tokens = self._long[0]
+        self.positions = self._long[1]
+        self.source_lanes = self._long[2]
+        self.block_tables = self._int[:cuts[0]].view(b, width)
+        self.context_lengths = self._int[cuts[0]:cuts[1]]
+        self.physical_blocks = self._int[cuts[1]:cuts[2]]
+        self.block_offsets = self._int[cuts[2]:cuts[3]]
+        self.active_mask = self._int[cuts[3]:]
+        self._lane_rows: list[tuple[tuple[int, int], int] | None] = [None] * b
+        if token_state is None:
+            token_state = torch.zeros(b, dtype=torch.long, device=device)
+        if token_state.numel() < b or token_state.dtype != torch.long:
+            raise ValueError("token_state must be an int64 tensor of at least batch_capacity")
+        self.token_state = token_state
+        hq, hkv, d = config.num_attention_heads, config.num_key_value_heads, config.head_dim
+        self.workspace = PagedAttentionWorkspace.allocate(
+            batch_capacity=b, query_heads=hq, head_dim=d, max_context_length=context_capacity,
+            device=device)
+        self.split_size = attention_split_size_for(context_capacity, b, hkv)
+        self.attention_output = torch.empty((b, hq, d), dtype=dtype, device=device)
+        self.norm_output = torch.empty((b, config.hidden_size), dtype=dtype, device=device)
+        self.swiglu_output = torch.empty((b, config.intermediate_size), dtype=dtype,
+                                         device=device)
+        self.logits = torch.empty((b, config.vocab_size), dtype=dtype, device=device)
+        self.next_tokens = self.token_state[:b]
+        self._graph: torch.cuda.CUDAGraph | None = None
+
+    def addresses(self) -> dict[str, int]:
+        """Device addresses the captured graph depends on (decode_bucket.py:330-369)."""
+
+        return {name: getattr(self, name).data_ptr() for name in (
+            "host_tokens", "positions", "source_lanes", "block_tables", "context_lengths",
+            "physical_blocks", "block_offsets", "active_mask", "attention_output",
+            "norm_output", "swiglu_output", "logits", "next_tokens")}
+
+    def prepare(self, request_ids: list[str], reservations: dict[str, AppendReservation], *,
+                tokens: dict[str, int] | None = None,
+                source_lanes: dict[str, int] | None = None) -> None:
+        """Stage one step: lane i decodes request_ids[i] at its one-token
+        reservation, with input token ``tokens[rid]`` if given, else the
+        token the previous step sampled in lane ``source_lanes[rid]``."""
+
+        b = self.batch_capacity
+        if len(request_ids) > b:
+            raise ValueError("more requests than the bucket's batch capacity")
+        tokens = tokens or {}
+        source_lanes = source_lanes or {}
+        block_size = self.cache.config.block_size
+        tables, lengths, pages, offsets, active = self._host_views
+        host_tokens, positions, sources = self._ctl_long
+        for lane, request_id in enumerate(request_ids):
+            reservation = reservations[request_id]
+            if reservation.request_id != request_id or reservation.token_count != 1:
+                raise ValueError("each lane needs a one-token reservation of its own request")
+            page_list, version = self.cache.page_list(request_id)
+            start = reservation.start_position
+            if start + 1 > self.context_capacity:
+                raise ValueError("context exceeds the bucket's context capacity")
+            logical, offset = divmod(start, block_size)
+            if logical >= len(page_list):
+                raise RuntimeError("reservation is not backed by a page")
+            row = self._lane_rows[lane]
+            count = len(page_list)
+            if row is None or row[0] != version or row[1] > count:
+                tables[lane, :count] = page_list
+                tables[lane, count:] = -1
+            elif row[1] < count:
+                tables[lane, row[1]:count] = page_list[row[1]:]
+            self._lane_rows[lane] = (version, count)
+            lengths[lane] = start + 1
+            pages[lane] = page_list[logical]
+            offsets[lane] = offset
+            active[lane] = 1
+            positions[lane] = start
+            if request_id in tokens:
+                host_tokens[lane] = tokens[request_id]
+                sources[lane] = -1
+            else:
+                host_tokens[lane] = 0
+                sources[lane] = source_lanes[request_id]
+        live = len(request_ids)
+        lengths[live:] = 0
+        pages[live:] = 0
+        offsets[live:] = 0
+        active[live:] = 0
+        positions[live:] = 0
+        host_tokens[live:] = 0
+        sources[live:] = -1
+        self._stage()
+
+    def _stage(self) -> None:
+        k = self._flip
+        self._flip ^= 1
+        if self._copy_recorded[k]:
+            self._copied[k].synchronize()  # the slab's previous copy has landed
+        pinned_long, pinned_int = self._pinned[k]
+        np.copyto(pinned_long.numpy(), self._ctl_long)
+        np.copyto(pinned_int.numpy(), self._ctl_int)
+        self._long.copy_(pinned_long, non_blocking=True)
+        self._int.copy_(pinned_int, non_blocking=True)
+        self._copied[k].record()
+        self._copy_recorded[k] = True
+
+    def execute(self) -> Tensor:
+        """Run the step (capturing the graph on first use); returns the
+        device tensor of greedy next tokens, one per lane."""
+
+        if self._graph is None:
+            stream = torch.cuda.current_stream(self.device)
+            # The eager warm-up (library handles and plans) samples into
+            # token_state; restore it so the replay reads the previous step's
+            # tokens.  Its cache writes equal the replay's.
+            saved = self.token_state.clone()
+            side = torch.cuda.Stream(self.device)
+            side.wait_stream(stream)
+            with torch.cuda.stream(side):
+                self._forward()
+            stream.wait_stream(side)
+            self.token_state.copy_(saved)
+            torch.cuda.synchronize(self.device)
+            self._graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self._graph):
+                self._forward()
+        self._graph.replay()
+        return self.next_tokens
+
+    def _forward(self) -> None:
+        config = self.weights.config
+        hq, hkv, d = config.num_attention_heads, config.num_key_value_heads, config.head_dim
+        b = self.batch_capacity
+        eps = config.rms_norm_eps
+        previous = set_attention_split_size(self.split_size)
+        try:
+            fed = self.token_state.index_select(0, self.source_lanes.clamp(min=0))
+            input_ids = torch.where(self.source_lanes >= 0, fed, self.host_tokens)
+            x = F.embedding(input_ids, self.weights.embedding)
+            cos = self.weights.rope_cos.index_select(0, self.positions)
+            sin = self.weights.rope_sin.index_select(0, self.positions)
+            residual = x
+            h = rms_norm(x, self.weights.layers[0].input_norm, eps, output=self.norm_output)
+            for index, layer in enumerate(self.weights.layers):
+                qkv = F.linear(h, layer.qkv)
+                q = _rope(qkv[:, :hq * d].view(b, hq, d), cos, sin).contiguous()
+                k = _rope(qkv[:, hq * d:(hq + hkv) * d].view(b, hkv, d), cos, sin).contiguous()
+                v = qkv[:, (hq + hkv) * d:].reshape(b, hkv, d).contiguous()
+                key_cache = self.cache.key_cache[index]
+                value_cache = self.cache.value_cache[index]
+                paged_kv_write_token(k, v, key_cache, value_cache, self.physical_blocks,
+                                     self.block_offsets, self.active_mask)
+                paged_gqa_decode_attention(
+                    q, key_cache, value_cache, self.block_tables, self.context_lengths,
+                    scale=d ** -0.5, max_context_length=self.context_capacity,
+                    output=self.attention_output, workspace=self.workspace)
+                attn = F.linear(self.attention_output.view(b, hq * d), layer.o_proj)
+                residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps,
+                                                residual_output=torch.empty_like(attn),
+                                                norm_output=self.norm_output)
+                act = swiglu(F.linear(h, layer.gate), F.linear(h, layer.up),
+                             output=self.swiglu_output)
+                mlp = F.linear(act, layer.down)
+                next_norm = (self.weights.layers[index + 1].input_norm
+                             if index + 1 < len(self.weights.layers) else self.weights.final_norm)
+                residual, h = residual_rms_norm(mlp, residual, next_norm, eps,
+                                                residual_output=torch.empty_like(mlp),
+                                                norm_output=self.norm_output)
+            torch.matmul(h, self.weights.lm_head.t(), out=self.logits)
+            torch.argmax(self.logits, dim=-1, out=self.next_tokens)
+        finally:
+            set_attention_split_size(previous)
+
+
+def prefill(weights: DecoderWeights, cache: PagedKVCache, request_id: str,
+            prompt: list[int]) -> tuple[int, Tensor]:
+    """Write the prompt's K/V into the cache and return (greedy next token,
+    last-position logits).  Full-prefix forward in fp32 on the device (the
+    reference's prefill path, runtime/prefill.py:36-149): projections in the
+    model dtype, causal attention in fp32 with contiguous operands."""
+
+    config = weights.config
+    hq, hkv, d = config.num_attention_heads, config.num_key_value_heads, config.head_dim
+    device = cache.config.device
+    seq = len(prompt)
+    reservation = cache.begin_append(request_id, seq)
+    tokens = torch.tensor(prompt, dtype=torch.long, device=device)
+    positions = torch.arange(reservation.start_position, reservation.end_position, device=device)
+    cos = weights.rope_cos.index_select(0, positions)
+    sin = weights.rope_sin.index_select(0, positions)
+    eps = config.rms_norm_eps
+    residual = F.embedding(tokens, weights.embedding)
+    h = rms_norm(residual, weights.layers[0].input_norm, eps)
+    causal = torch.ones(seq, seq, dtype=torch.bool, device=device).triu(1)
+    for index, layer in enumerate(weights.layers):
+        qkv = F.linear(h, layer.qkv)
+        q = _rope(qkv[:, :hq * d].view(seq, hq, d), cos, sin)
+        k = _rope(qkv[:, hq * d:(hq + hkv) * d].view(seq, hkv, d), cos, sin).contiguous()
+        v = qkv[:, (hq + hkv) * d:].reshape(seq, hkv, d).contiguous()
+        cache.write_layer(reservation, index, k, v)
+        qf = q.float().transpose(0, 1).contiguous()                       # [hq, seq, d]
+        kf = k.float().repeat_interleave(hq // hkv, dim=1).transpose(0, 1).contiguous()
+        vf = v.float().repeat_interleave(hq // hkv, dim=1).transpose(0, 1).contiguous()
+        scores = torch.matmul(qf, kf.transpose(1, 2).contiguous()) * d ** -0.5
+        scores = scores.masked_fill(causal, float("-inf"))
+        context = torch.matmul(torch.softmax(scores, dim=-1), vf)          # [hq, seq, d]
+        context = context.transpose(0, 1).reshape(seq, hq * d).to(q.dtype)
+        attn = F.linear(context, layer.o_proj)
+        residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps)
+        act = swiglu(F.linear(h, layer.gate), F.linear(h, layer.up))
+        next_norm = (weights.layers[index + 1].input_norm
+                     if index + 1 < len(weights.layers) else weights.final_norm)
+        residual, h = residual_rms_norm(F.linear(act, layer.down), residual, next_norm, eps)
+    logits = F.linear(h[-1:], weights.lm_head)[0]
+    cache.commit(reservation)
+    return int(torch.argmax(logits)), logits
+
+
+DEFAULT_BATCH_BUCKETS = (1, 2, 4, 8, 16, 32, 64)
+DEFAULT_CONTEXT_BUCKETS = (512, 1024, 2048, 4096)
+
+
+@dataclass(slots=True)
+class DecodeTicket:
+    """One launched decode step whose sampled tokens have not been read yet."""
+
+    request_ids: tuple[str, ...]
+    bucket: tuple[int, int]
+    slot: int
+
+
+@dataclass(frozen=True, slots=True)
+class DecodeStepRecord:
+    bucket: tuple[int, int]
+    lanes: int
+    device_ms: float
+
+
+class BucketedDecodeExecutor:
+    """Decode executor over graph buckets (reference:
+    BucketedPagedDecodeExecutor, decode_bucket.py:532-666).
+
+    ``launch`` stages and replays one step and returns at once; ``collect``
+    returns that step's sampled tokens.  A request that ran in the previously
+    launched step needs no host token: its lane's sample is fed back on the
+    device.  So a serving loop can launch step n+1 before reading step n's
+    tokens and keep the GPU one step ahead of the host.  ``append_tokens``
+    is the reference's synchronous form (host tokens in, logits out).
+    """
+
+    _RING = 4
+
+    def __init__(self, weights: DecoderWeights, cache: PagedKVCache, *,
+                 batch_buckets: tuple[int, ...] = DEFAULT_BATCH_BUCKETS,
+                 context_buckets: tuple[int, ...] = DEFAULT_CONTEXT_BUCKETS) -> None:
+        if not batch_buckets or any(value <= 0 for value in batch_buckets):
+            raise ValueError("batch_buckets must contain positive capacities")
+        if not context_buckets or any(value <= 0 for value in context_buckets):
+            raise ValueError("context_buckets must contain positive capacities")
+        self.weights = weights
+        self.cache = cache
+        self.batch_buckets = tuple(sorted(set(batch_buckets)))
+        self.context_buckets = tuple(sorted(set(context_buckets)))
+        if self.batch_buckets[-1] > cache.config.max_sequences:
+            raise ValueError("batch bucket exceeds cache sequence capacity")
+        if self.context_buckets[-1] > cache.config.max_sequence_length:
+            raise ValueError("context bucket exceeds cache sequence capacity")
+        device = cache.config.device
+        lanes = self.batch_buckets[-1]
+        self.token_state = torch.zeros(lanes, dtype=torch.long, device=device)
+        self._buckets: dict[tuple[int, int], DecodeGraphBucket] = {}
+        self._last_lanes: dict[str, int] = {}
+        self._readback = [torch.zeros(lanes, dtype=torch.long, pin_memory=True)
+                          for _ in range(self._RING)]
+        self._events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+                         torch.cuda.Event()) for _ in range(self._RING)]
+        self._busy = [False] * self._RING
+        self._next_slot = 0
+        self.step_records: list[DecodeStepRecord] = []
+
+    @property
+    def vocab_size(self) -> int:
+        return self.weights.config.vocab_size
+
+    def create_request(self, request_id: str) -> None:
+        self.cache.create_sequence(request_id)
+
+    def release_request(self, request_id: str) -> None:
+        self._last_lanes.pop(request_id, None)
+        self.cache.release(request_id)
+
+    def prefill_prompts(self, prompts: dict[str, list[int]]) -> dict[str, int]:
+        """Prefill each prompt; returns its greedy first token."""
+
+        return {rid: prefill(self.weights, self.cache, rid, prompt)[0]
+                for rid, prompt in prompts.items()}
+
+    def buffer_addresses(self) -> dict[str, dict[str, int]]:
+        return {f"b{batch}-c{context}": bucket.addresses()
+                for (batch, context), bucket in self._buckets.items()}
+
+    def bucket(self, batch: int, context: int) -> DecodeGraphBucket:
+        batch_capacity = next((v for v in self.batch_buckets if v >= batch), None)
+        context_capacity = next((v for v in self.context_buckets if v >= context), None)
+        if batch_capacity is None or context_capacity is None:
+            raise ValueError(f"no decode bucket holds batch {batch} at context {context}")
+        key = (batch_capacity, context_capacity)
+        if key not in self._buckets:
+            self._buckets[key] = DecodeGraphBucket(
+                self.weights, self.cache, batch_capacity=batch_capacity,
+                context_capacity=context_capacity, token_state=self.token_state)
+        return self._buckets[key]
+
+    def launch(self, request_ids: list[str], tokens: dict[str, int] | None = None) -> DecodeTicket:
+        """Append one token to each request and enqueue the step.  Requests in
+        ``tokens`` take that input token; the others must have run in the
+        previously launched step, whose sample they continue from."""
+
+        tokens = tokens or {}
+        if not request_ids:
+            raise ValueError("launch requires at least one request")
+        for request_id in request_ids:
+            if request_id not in tokens and request_id not in self._last_lanes:
+                raise ValueError(f"{request_id}: no input token (not in the previous step)")
+            if request_id in tokens and not 0 <= tokens[request_id] < self.vocab_size:
+                raise ValueError(f"{request_id}: token_id is outside the model vocabulary")
+        slot = self._next_slot
+        if self._busy[slot]:
+            raise RuntimeError("too many decode steps launched without collect()")
+        reservations: dict[str, AppendReservation] = {}
+        try:
+            for request_id in request_ids:
+                reservations[request_id] = self.cache.begin_append(request_id, 1)
+            context = max(r.end_position for r in reservations.values())
+            bucket = self.bucket(len(request_ids), context)
+            bucket.prepare(list(request_ids), reservations, tokens=tokens,
+                           source_lanes=self._last_lanes)
+        except Exception:
+            for reservation in reservations.values():
+                self.cache.rollback(reservation)
+            raise
+        begin, end, copied = self._events[slot]
+        begin.record()
+        bucket.execute()
+        end.record()
+        lanes = len(request_ids)
+        self._readback[slot][:lanes].copy_(self.token_state[:lanes], non_blocking=True)
+        copied.record()
+        # Host bookkeeping only: the step's device work is ordered before any
+        # later reader of these pages on this stream.
+        for reservation in reservations.values():
+            self.cache.record_all_layers_written(reservation)
+            self.cache.commit(reservation)
+        self._last_lanes = {request_id: lane for lane, request_id in enumerate(request_ids)}
+        self._busy[slot] = True
+        self._next_slot = (slot + 1) % self._RING
+        return DecodeTicket(tuple(request_ids), (bucket.batch_capacity, bucket.context_capacity),
+                            slot)
+
+    def collect(self, ticket: DecodeTicket) -> list[int]:
+        """Wait for a launched step; its sampled token per request, in order."""
+
+        if not self._busy[ticket.slot]:
+            raise RuntimeError("decode ticket was already collected")
+        begin, end, copied = self._events[ticket.slot]
+        copied.synchronize()
+        lanes = len(ticket.request_ids)
+        sampled = self._readback[ticket.slot][:lanes].tolist()
+        self.step_records.append(DecodeStepRecord(ticket.bucket, lanes, begin.elapsed_time(end)))
+        self._busy[ticket.slot] = False
+        return sampled
+
+    def append_tokens(self, tokens: dict[str, int]) -> dict[str, Tensor]:
+        """The reference's synchronous step: logits per request
+        (decode_bucket.py:582-666); views into the bucket's logits buffer,
+        valid until the next step."""
+
+        ticket = self.launch(list(tokens), tokens)
+        self.collect(ticket)
+        bucket = self._buckets[ticket.bucket]
+        return {request_id: bucket.logits[lane] for lane, request_id in enumerate(tokens)}
+
+
+def greedy_decode(executor: BucketedDecodeExecutor, prompts: dict[str, list[int]],
+                  steps: int) -> dict[str, list[int]]:
+    """Prefill each prompt, then decode ``steps - 1`` more greedy tokens for
+    all of them together, keeping one step in flight: step n+1 is launched
+    (its inputs fed back on the device) before step n's tokens are read."""
+
+    outputs: dict[str, list[int]] = {}
+    for request_id, prompt in prompts.items():
+        executor.create_request(request_id)
+    first = executor.prefill_prompts(prompts)
+    for request_id in prompts:
+        outputs[request_id] = [first[request_id]]
+    order = list(prompts)
+    pending: DecodeTicket | None = None
+    for step in range(steps - 1):
+        ticket = executor.launch(order, first if step == 0 else None)
+        if pending is not None:
+            for request_id, token in zip(order, executor.collect(pending)):
+                outputs[request_id].append(token)
+        pending = ticket
+    if pending is not None:
+        for request_id, token in zip(order, executor.collect(pending)):
+            outputs[request_id].append(token)
+    return outputs
+

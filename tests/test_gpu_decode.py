@@ -1,0 +1,172 @@
+"""The bucketed, graph-captured decode executor against the decoder oracle
+(4 layers, d_model 256, 8/2 heads, FFN 768, vocab 1024,
+fp16 on the GPU, 4 prompts of {17, 64, 100, 255} tokens, 32 greedy steps,
+16-token pages on a seeded permutation of a 128-page pool).
+
+Greedy tokens are checked the way the reference checks them
+(tests/test_decode_bucket.py:61-68, tests/test_triton_model.py:38-43): each
+sampled token must be the oracle's argmax over the same prefix unless the
+oracle's own top-two margin is within the fp16 error.
+"""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+
+from oracle.model import decoder_forward
+from tensorforge_amd.cache import PagedKVCache, PagedKVCacheConfig
+from tensorforge_amd.decode import (
+    BucketedDecodeExecutor,
+    DecoderWeights,
+    greedy_decode,
+    prefill,
+    small_config,
+)
+
+pytestmark = pytest.mark.gpu
+
+MARGIN = 2e-3  # fraction of the row's largest |logit| an fp16 flip may need
+
+
+def _cache(config, device, pages=128, sequences=4):
+    order = list(range(pages))
+    random.Random(0).shuffle(order)
+    return PagedKVCache(
+        PagedKVCacheConfig(num_layers=config.num_hidden_layers, num_blocks=pages, block_size=16,
+                           num_kv_heads=config.num_key_value_heads, head_dim=config.head_dim,
+                           max_sequences=sequences, max_sequence_length=512,
+                           dtype=torch.float16, device=device),
+        page_order=order,
+    )
+
+
+def _prompts():
+    rng = random.Random(0)
+    return {f"req{i}": [rng.randrange(1024) for _ in range(n)]
+            for i, n in enumerate((17, 64, 100, 255))}
+
+
+def _greedy_mismatches(weights, prompt: list[int], generated: list[int]) -> list[tuple]:
+    logits = decoder_forward(weights, torch.tensor(prompt + generated[:-1]))
+    mismatches = []
+    for step, token in enumerate(generated):
+        row = logits[len(prompt) - 1 + step]
+        best = int(torch.argmax(row))
+        if token != best:
+            margin = float(row[best] - row[token])
+            assert margin <= MARGIN * float(row.abs().max()), (step, token, best, margin)
+            mismatches.append((step, margin))
+    return mismatches
+
+
+def test_prefill_logits_match_the_oracle(device):
+    config = small_config()
+    weights = DecoderWeights.random(config, seed=0, dtype=torch.float16, device=device)
+    cache = _cache(config, device)
+    for rid, prompt in _prompts().items():
+        cache.create_sequence(rid)
+        token, logits = prefill(weights, cache, rid, prompt)
+        expected = decoder_forward(weights, torch.tensor(prompt))[-1]
+        scale = float(expected.abs().max())
+        err = float((logits.float().cpu() - expected).abs().max())
+        assert err <= 2e-2 * scale, f"{rid}: max |dlogits| {err:.3e} vs scale {scale:.3e}"
+        assert token == int(torch.argmax(expected)) or \
+            float(expected.max() - expected[token]) <= 4 * err
+
+
+def test_greedy_decode_matches_the_oracle(device):
+    """32 greedy tokens per request, one step always in flight; the 255-token
+    prompt crosses from the 256- into the 512-token context bucket."""
+
+    config = small_config()
+    weights = DecoderWeights.random(config, seed=0, dtype=torch.float16, device=device)
+    cache = _cache(config, device)
+    prompts = _prompts()
+    executor = BucketedDecodeExecutor(weights, cache, batch_buckets=(1, 2, 4),
+                                      context_buckets=(256, 512))
+    outputs = greedy_decode(executor, prompts, steps=32)
+    mismatches = {}
+    for rid, prompt in prompts.items():
+        assert len(outputs[rid]) == 32
+        if found := _greedy_mismatches(weights, prompt, outputs[rid]):
+            mismatches[rid] = found
+    assert sum(map(len, mismatches.values())) <= 1, mismatches
+    assert {key for key in executor.buffer_addresses()} == {"b4-c256", "b4-c512"}
+
+
+def test_changing_batches_feed_tokens_back_by_lane(device):
+    """Requests leave, join and move between lanes and buckets while each
+    step's tokens stay on the device: a request that ran in the previous step
+    continues from its old lane's sample, a newly prefilled one from its host
+    token."""
+
+    config = small_config()
+    weights = DecoderWeights.random(config, seed=2, dtype=torch.float16, device=device)
+    cache = _cache(config, device)
+    prompts = _prompts()
+    executor = BucketedDecodeExecutor(weights, cache, batch_buckets=(1, 2, 4),
+                                      context_buckets=(256, 512))
+    outputs: dict[str, list[int]] = {}
+
+    def admit(rids):
+        for rid in rids:
+            executor.create_request(rid)
+        first = executor.prefill_prompts({rid: prompts[rid] for rid in rids})
+        for rid in rids:
+            outputs[rid] = [first[rid]]
+        return first
+
+    def run(order, host_tokens, steps):
+        pending = None
+        for step in range(steps):
+            ticket = executor.launch(order, host_tokens if step == 0 else None)
+            if pending is not None:
+                for rid, token in zip(pending.request_ids, executor.collect(pending)):
+                    outputs[rid].append(token)
+            pending = ticket
+        for rid, token in zip(pending.request_ids, executor.collect(pending)):
+            outputs[rid].append(token)
+
+    run(["req0", "req1", "req2"], admit(["req0", "req1", "req2"]), 3)   # bucket 4
+    executor.release_request("req0")
+    run(["req1", "req2"], None, 2)                                      # bucket 2, lanes move
+    run(["req2", "req1", "req3"], admit(["req3"]), 4)                   # bucket 4, swapped + new
+    run(["req3"], None, 2)                                              # bucket 1
+    assert [len(outputs[r]) for r in ("req0", "req1", "req2", "req3")] == [4, 10, 10, 7]
+    total = 0
+    for rid, generated in outputs.items():
+        total += len(_greedy_mismatches(weights, prompts[rid], generated))
+    assert total <= 1
+
+
+def test_padded_lanes_write_nothing_and_addresses_are_stable(device):
+    """Two requests in a 4-lane bucket: only pages the live requests own
+    change, the graph's buffers keep their addresses across steps, and the
+    reference's synchronous append_tokens returns the oracle's logits."""
+
+    config = small_config()
+    weights = DecoderWeights.random(config, seed=1, dtype=torch.float16, device=device)
+    cache = _cache(config, device)
+    prompts = dict(list(_prompts().items())[:2])
+    executor = BucketedDecodeExecutor(weights, cache, batch_buckets=(4,), context_buckets=(512,))
+    bits = lambda t: t.view(torch.int16)  # noqa: E731  (bitwise: the pool starts uninitialised)
+    before = (bits(cache.key_cache).clone(), bits(cache.value_cache).clone())
+    outputs = greedy_decode(executor, prompts, steps=4)
+    addresses = executor.buffer_addresses()
+    tokens = {rid: generated[-1] for rid, generated in outputs.items()}
+    logits = executor.append_tokens(tokens)
+    assert executor.buffer_addresses() == addresses
+    owned = {page for page, owner in enumerate(cache.block_owners()) if owner is not None}
+    changed = set()
+    for now, then in zip((bits(cache.key_cache), bits(cache.value_cache)), before):
+        per_page = (now != then).transpose(0, 1).flatten(1).any(1)  # [layer, page, ...]
+        changed |= {int(p) for p in torch.nonzero(per_page).flatten()}
+    assert changed and changed <= owned
+    for rid, prompt in prompts.items():
+        expected = decoder_forward(weights, torch.tensor(prompt + outputs[rid]))[-1]
+        err = float((logits[rid].float().cpu() - expected).abs().max())
+        assert err <= 2e-2 * float(expected.abs().max()), (rid, err)
+        assert cache.sequence_layout(rid).context_length == len(prompt) + len(outputs[rid])
