@@ -27,8 +27,14 @@ Pinning (tests/test_oracle.py):
   paged_kv_write_*_reference   the arange known answer of
                                tests/test_paged_cache.py:11-37, dense
                                recomputation by materialisation order
+  rope_kv_append_reference     (tests/test_oracle_model.py) position-0
+                               identity, unit vectors turning into
+                               (cos p, sin p) / (-sin p, cos p), per-pair norm
+                               preservation, masked lanes and untouched rows
+                               bit-identical, values copied bit for bit
 Mutation tests plant a wrong GQA map, a dropped scale and a reversed page
-order in these functions and check that the pins above reject them.
+order in these functions (and a negated sine, an off-by-one position and an
+unrotated key in the RoPE append) and check that the pins above reject them.
 """
 
 from __future__ import annotations
@@ -317,3 +323,49 @@ def paged_kv_write_slots_reference(
             vb[slot] = vs[t]
     return k_out, v_out
 
+
+
+def rope_kv_append_reference(
+    qkv: Tensor,
+    positions: Tensor,
+    cos_table: Tensor,
+    sin_table: Tensor,
+    key_cache: Tensor,
+    value_cache: Tensor,
+    physical_blocks: Tensor,
+    block_offsets: Tensor,
+    active_mask: Tensor,
+    query_heads: int,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """(rotated query [B, Hq, D] in fp32, key cache, value cache) after the
+    fused decode-step RoPE and append.
+
+    RoPE with the half-split rotation (model/layers.py:46-69), evaluated in
+    fp32 from the storage-dtype cos/sin rows of each lane's position; the
+    rotated key is rounded once to the cache dtype and, with the value
+    (copied bit for bit), written by the masked one-token write
+    (paged_kv_write_token_reference).
+    """
+
+    num_blocks, block_size, kv_heads, head_dim = key_cache.shape
+    half = head_dim // 2
+    rows = qkv.detach().cpu().float()
+    pos = positions.detach().cpu().long()
+    cos = cos_table.detach().cpu().float()[pos][:, None, :]
+    sin = sin_table.detach().cpu().float()[pos][:, None, :]
+
+    def rotate(x: Tensor) -> Tensor:
+        rotated = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+        return x * cos + rotated * sin
+
+    batch = rows.shape[0]
+    q = rotate(rows[:, : query_heads * head_dim].reshape(batch, query_heads, head_dim))
+    k = rotate(rows[:, query_heads * head_dim:(query_heads + kv_heads) * head_dim]
+               .reshape(batch, kv_heads, head_dim))
+    v = qkv.detach().cpu()[:, (query_heads + kv_heads) * head_dim:
+                           (query_heads + 2 * kv_heads) * head_dim]
+    keys = k.to(key_cache.dtype)
+    values = v.reshape(batch, kv_heads, head_dim).contiguous()
+    key_out, value_out = paged_kv_write_token_reference(
+        keys, values, key_cache, value_cache, physical_blocks, block_offsets, active_mask)
+    return q, key_out, value_out

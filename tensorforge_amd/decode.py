@@ -40,9 +40,9 @@ from tensorforge_amd.cache import AppendReservation, PagedKVCache
 from tensorforge_amd.kernels import (
     PagedAttentionWorkspace,
     paged_gqa_decode_attention,
-    paged_kv_write_token,
     residual_rms_norm,
     rms_norm,
+    rope_paged_kv_append,
     swiglu,
 )
 from tensorforge_amd.kernels.attention import attention_split_size_for, set_attention_split_size
@@ -200,6 +200,7 @@ class DecodeGraphBucket:
         self.block_offsets = self._int[cuts[2]:cuts[3]]
         self.active_mask = self._int[cuts[3]:]
         self._lane_rows: list[tuple[tuple[int, int], int] | None] = [None] * b
+        self._max_position = weights.rope_cos.shape[0]
         if token_state is None:
             token_state = torch.zeros(b, dtype=torch.long, device=device)
         if token_state.numel() < b or token_state.dtype != torch.long:
@@ -210,6 +211,7 @@ class DecodeGraphBucket:
             batch_capacity=b, query_heads=hq, head_dim=d, max_context_length=context_capacity,
             device=device)
         self.split_size = attention_split_size_for(context_capacity, b, hkv)
+        self.query = torch.empty((b, hq, d), dtype=dtype, device=device)
         self.attention_output = torch.empty((b, hq, d), dtype=dtype, device=device)
         self.norm_output = torch.empty((b, config.hidden_size), dtype=dtype, device=device)
         self.swiglu_output = torch.empty((b, config.intermediate_size), dtype=dtype,
@@ -249,6 +251,8 @@ class DecodeGraphBucket:
             start = reservation.start_position
             if start + 1 > self.context_capacity:
                 raise ValueError("context exceeds the bucket's context capacity")
+            if start >= self._max_position:
+                raise ValueError("position exceeds the model's RoPE table")
             logical, offset = divmod(start, block_size)
             if logical >= len(page_list):
                 raise RuntimeError("reservation is not backed by a page")
@@ -327,19 +331,18 @@ class DecodeGraphBucket:
             fed = self.token_state.index_select(0, self.source_lanes.clamp(min=0))
             input_ids = torch.where(self.source_lanes >= 0, fed, self.host_tokens)
             x = F.embedding(input_ids, self.weights.embedding)
-            cos = self.weights.rope_cos.index_select(0, self.positions)
-            sin = self.weights.rope_sin.index_select(0, self.positions)
             residual = x
             h = rms_norm(x, self.weights.layers[0].input_norm, eps, output=self.norm_output)
             for index, layer in enumerate(self.weights.layers):
                 qkv = F.linear(h, layer.qkv)
-                q = _rope(qkv[:, :hq * d].view(b, hq, d), cos, sin).contiguous()
-                k = _rope(qkv[:, hq * d:(hq + hkv) * d].view(b, hkv, d), cos, sin).contiguous()
-                v = qkv[:, (hq + hkv) * d:].reshape(b, hkv, d).contiguous()
                 key_cache = self.cache.key_cache[index]
                 value_cache = self.cache.value_cache[index]
-                paged_kv_write_token(k, v, key_cache, value_cache, self.physical_blocks,
-                                     self.block_offsets, self.active_mask)
+                # RoPE on q and k, k and v into their pages: one launch.
+                q = rope_paged_kv_append(qkv, self.positions, self.weights.rope_cos,
+                                         self.weights.rope_sin, key_cache, value_cache,
+                                         self.physical_blocks, self.block_offsets,
+                                         self.active_mask, query_heads=hq,
+                                         query_output=self.query)
                 paged_gqa_decode_attention(
                     q, key_cache, value_cache, self.block_tables, self.context_lengths,
                     scale=d ** -0.5, max_context_length=self.context_capacity,
@@ -500,6 +503,21 @@ class BucketedDecodeExecutor:
                 self.weights, self.cache, batch_capacity=batch_capacity,
                 context_capacity=context_capacity, token_state=self.token_state)
         return self._buckets[key]
+
+    def capture_all(self) -> None:
+        """Capture every (batch, context) bucket now, with all lanes padded,
+        so no capture lands inside a timed run.  Only between requests: it
+        overwrites the sampled-token state."""
+
+        if any(self._busy):
+            raise RuntimeError("capture_all with decode steps in flight")
+        for batch in self.batch_buckets:
+            for context in self.context_buckets:
+                bucket = self.bucket(batch, context)
+                bucket.prepare([], {})
+                bucket.execute()
+        self._last_lanes = {}
+        torch.cuda.synchronize(self.cache.config.device)
 
     def launch(self, request_ids: list[str], tokens: dict[str, int] | None = None) -> DecodeTicket:
         """Append one token to each request and enqueue the step.  Requests in

@@ -7,7 +7,13 @@
   {5632, 14336}, and the paged KV append of T tokens x 4 kv heads x 64
   through ``PagedKVCache.write_layer`` starting mid-page, all bf16;
 * config 3 -- paged GQA decode attention at Llama-3-8B geometry (4 rows of
-  8k/16k/24k/32k, 32/8 heads, head_dim 128), split size chosen per call.
+  8k/16k/24k/32k, 32/8 heads, head_dim 128), split size chosen per call;
+* decode steps -- one whole graph-captured decode step of the config-1
+  model (4 layers, d_model 256, fp16) at batch {1, 4, 8} x context
+  {32, 128, 512, 2048}, the grid of the reference's decode-step report
+  (results/reference/phase7a-rtx3080ti-wsl/execution.md); device time per
+  step from HIP events, and host-inclusive time per step of the pipelined
+  launch/collect loop.
 
 Each case is captured as ``--calls`` launches in one HIP graph and timed by
 HIP events around one replay (a ctypes call costs the host longer than these
@@ -29,6 +35,12 @@ import torch
 
 from tensorforge_amd import workloads
 from tensorforge_amd.cache import PagedKVCache, PagedKVCacheConfig
+from tensorforge_amd.decode import (
+    BucketedDecodeExecutor,
+    DecoderWeights,
+    small_config,
+    tinyllama_config,
+)
 from tensorforge_amd.kernels import (
     PagedAttentionWorkspace,
     paged_gqa_decode_attention,
@@ -137,10 +149,64 @@ def config3(device: torch.device, calls: int) -> None:
            record=selected_attention_autotune_config())
 
 
+def decode_steps(device: torch.device, model: str = "cfg1", steps: int = 64) -> None:
+    import dataclasses
+    import time
+
+    if model == "cfg1":
+        config = dataclasses.replace(small_config(), max_position_embeddings=4096)
+        dtype, grid = torch.float16, [(c, b) for c in (32, 128, 512, 2048) for b in (1, 4, 8)]
+    else:
+        config = tinyllama_config()
+        dtype, grid = torch.bfloat16, [(1024, b) for b in (1, 8, 64)]
+    weights = DecoderWeights.random(config, seed=0, dtype=dtype, device=device)
+    generator = torch.Generator().manual_seed(0)
+    for context, batch in grid:
+        prompt_length = context - steps // 2 - 8 if context > steps else context // 2
+        cache = PagedKVCache(PagedKVCacheConfig(
+            num_layers=config.num_hidden_layers, num_blocks=batch * (context // 16 + 2),
+            block_size=16, num_kv_heads=config.num_key_value_heads,
+            head_dim=config.head_dim, max_sequences=batch, max_sequence_length=context,
+            dtype=dtype, device=device))
+        executor = BucketedDecodeExecutor(weights, cache, batch_buckets=(batch,),
+                                          context_buckets=(context,))
+        rids = [f"s{i}" for i in range(batch)]
+        for rid in rids:
+            executor.create_request(rid)
+        prompts = {rid: torch.randint(0, config.vocab_size, (prompt_length,),
+                                      generator=generator).tolist() for rid in rids}
+        tokens = executor.prefill_prompts(prompts)
+        budget = context - prompt_length
+        warm = min(4, budget // 4)
+        timed = min(steps, budget - warm - 1)
+        pending = executor.launch(rids, tokens)
+        for _ in range(warm - 1):
+            ticket = executor.launch(rids)
+            executor.collect(pending)
+            pending = ticket
+        executor.step_records.clear()
+        begin = time.perf_counter()
+        for _ in range(timed):
+            ticket = executor.launch(rids)
+            executor.collect(pending)
+            pending = ticket
+        executor.collect(pending)
+        host_ms = (time.perf_counter() - begin) * 1e3 / timed
+        times = sorted(r.device_ms for r in executor.step_records[1:])
+        p50 = times[len(times) // 2]
+        print(json.dumps({
+            "case": f"decode_step {model}-model b{batch}-c{context}", "steps": timed,
+            "device_ms_p50": round(p50, 4),
+            "device_ms_p95": round(times[int(0.95 * (len(times) - 1))], 4),
+            "host_inclusive_ms_per_step": round(host_ms, 4),
+            "tokens_per_second": round(batch / (max(host_ms, p50) / 1e3), 1),
+        }), flush=True)
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--calls", type=int, default=100)
-    parser.add_argument("--only", choices=("cfg3", "cfg4"), default=None)
+    parser.add_argument("--only", choices=("cfg3", "cfg4", "decode", "decode22"), default=None)
     args = parser.parse_args()
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -150,6 +216,10 @@ def main() -> int:
         config4(device, args.calls)
     if args.only in (None, "cfg3"):
         config3(device, max(10, args.calls // 4))
+    if args.only in (None, "decode"):
+        decode_steps(device, "cfg1")
+    if args.only in (None, "decode22"):
+        decode_steps(device, "tinyllama")
     return 0
 
 

@@ -22,6 +22,7 @@ from tensorforge_amd.kernels.ops import (
     selected_autotune_config,
     swiglu,
 )
+from tensorforge_amd.kernels.rope import rope_paged_kv_append
 
 __all__ = [
     "PagedAttentionWorkspace",
@@ -33,6 +34,7 @@ __all__ = [
     "paged_kv_write_token",
     "residual_rms_norm",
     "rms_norm",
+    "rope_paged_kv_append",
     "selected_attention_autotune_config",
     "selected_attention_launch",
     "selected_autotune_config",

@@ -4,10 +4,15 @@ from __future__ import annotations
 
 import math
 
+import pytest
 import torch
 
 from oracle.model import apply_rope, decoder_forward, rope_tables, rotate_half
-from oracle.reference import paged_gqa_decode_reference, rms_norm_reference
+from oracle.reference import (
+    paged_gqa_decode_reference,
+    rms_norm_reference,
+    rope_kv_append_reference,
+)
 from tensorforge_amd.decode import DecoderConfig, DecoderWeights
 
 
@@ -120,3 +125,67 @@ def test_last_position_attention_is_the_decode_oracle() -> None:
                                          torch.tensor([pages], dtype=torch.int32),
                                          torch.tensor([seq], dtype=torch.int32))
     torch.testing.assert_close(decoded[0], last[:, 0], rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# The fused decode RoPE + append oracle (rope_kv_append_reference).
+# ---------------------------------------------------------------------------
+def pin_rope_kv_append(fn) -> None:
+    """Closed forms: position 0 is the identity; a unit vector e_0 at
+    position p turns into (cos p, sin p) on the pair (0, D/2) and e_{D/2}
+    into (-sin p, cos p); every pair keeps its norm; masked lanes leave the
+    cache untouched; values are copied bit for bit."""
+
+    hq, hkv, d, half = 4, 2, 8, 4
+    generator = torch.Generator().manual_seed(11)
+    cos, sin = rope_tables(d, 10000.0, torch.arange(16))
+    qkv = torch.randn(3, (hq + 2 * hkv) * d, generator=generator)
+    qkv[2, :d] = 0.0
+    qkv[2, 0] = 1.0                                  # q head 0 of lane 2 = e_0
+    qkv[2, d:2 * d] = 0.0
+    qkv[2, d + half] = 1.0                           # q head 1 of lane 2 = e_{D/2}
+    qkv[2, hq * d:(hq + 1) * d] = 0.0
+    qkv[2, hq * d] = 1.0                             # k head 0 of lane 2 = e_0
+    positions = torch.tensor([0, 5, 11])
+    key_cache = torch.randn(5, 4, hkv, d, generator=generator)
+    value_cache = torch.randn(5, 4, hkv, d, generator=generator)
+    pages = torch.tensor([3, 0, 4], dtype=torch.int32)
+    offsets = torch.tensor([1, 3, 0], dtype=torch.int32)
+    active = torch.tensor([1, 0, 1], dtype=torch.int32)
+    q, keys, values = fn(qkv, positions, cos, sin, key_cache, value_cache, pages, offsets, active,
+                         hq)
+    rows = qkv.view(3, hq + 2 * hkv, d)
+    assert torch.equal(q[0], rows[0, :hq]), "position 0 is not the identity on q"
+    assert torch.equal(keys[3, 1], rows[0, hq:hq + hkv]), "position 0 is not the identity on k"
+    for got, want in ((q[2, 0, 0], math.cos(11)), (q[2, 0, half], math.sin(11)),
+                      (q[2, 1, 0], -math.sin(11)), (q[2, 1, half], math.cos(11)),
+                      (keys[4, 0, 0, 0], math.cos(11)), (keys[4, 0, 0, half], math.sin(11))):
+        assert math.isclose(float(got), want, abs_tol=1e-6), (float(got), want)
+    pair_in = rows[:, :hq].reshape(3, hq, 2, half).pow(2).sum(2)
+    pair_out = q.reshape(3, hq, 2, half).pow(2).sum(2)
+    assert torch.allclose(pair_in, pair_out, atol=1e-5), "rotation changed a pair's norm"
+    assert torch.equal(keys[0, 3], key_cache[0, 3]) and torch.equal(values[0, 3], value_cache[0, 3])
+    for lane, (page, offset) in ((0, (3, 1)), (2, (4, 0))):
+        assert torch.equal(values[page, offset], rows[lane, hq + hkv:])
+    untouched = torch.ones(5, 4, dtype=torch.bool)
+    untouched[3, 1] = untouched[4, 0] = False
+    assert torch.equal(keys[untouched], key_cache[untouched])
+
+
+def test_rope_kv_append_oracle_pins() -> None:
+    pin_rope_kv_append(rope_kv_append_reference)
+
+
+def test_rope_kv_append_pins_reject_planted_mistakes() -> None:
+    def negated_sin(qkv, pos, cos, sin, *rest):
+        return rope_kv_append_reference(qkv, pos, cos, -sin, *rest)
+
+    def position_off_by_one(qkv, pos, cos, sin, *rest):
+        return rope_kv_append_reference(qkv, pos + 1, cos, sin, *rest)
+
+    def key_not_rotated(qkv, pos, cos, sin, *rest):
+        return rope_kv_append_reference(qkv, torch.zeros_like(pos), cos, sin, *rest)
+
+    for mutant in (negated_sin, position_off_by_one, key_not_rotated):
+        with pytest.raises(AssertionError):
+            pin_rope_kv_append(mutant)
