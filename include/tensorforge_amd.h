@@ -244,6 +244,18 @@ int32_t tf_residual_rms_norm(const void *inputs, const void *residual,
 int32_t tf_swiglu(const void *gate, const void *up, void *output,
                   int64_t numel, int32_t dtype, void *stream);
 
+/*
+ * SwiGLU over a fused gate|up projection: row r of gate_up (row stride
+ * gate_up_row_stride elements) holds gate[0..columns) then up[0..columns);
+ * output[r, c] = g * sigmoid(g) * u with the arithmetic of tf_swiglu.  No
+ * reference counterpart: it lets the decode step run the gate and up
+ * projections (tensorforge/model/layers.py:146-158, two GEMMs there) as one
+ * GEMM over stacked weights.
+ */
+int32_t tf_swiglu_rows(const void *gate_up, int64_t gate_up_row_stride,
+                       void *output, int64_t output_row_stride, int64_t rows,
+                       int32_t columns, int32_t dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

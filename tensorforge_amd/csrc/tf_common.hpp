@@ -55,6 +55,17 @@ __device__ __forceinline__ T from_float(float v) {
   return static_cast<T>(v);
 }
 
+// fp32 -> fp16 goes through a rounded fp32 value.  Without the empty asm the
+// compiler may fold a final fp32 multiply into the convert
+// (v_fma_mixlo_f16: the exact product rounded once to fp16), which differs
+// from rounding the fp32 product now and then and would make the scalar and
+// vector forms of a kernel disagree.
+template <>
+__device__ __forceinline__ _Float16 from_float<_Float16>(float v) {
+  asm("" : "+v"(v));
+  return static_cast<_Float16>(v);
+}
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------

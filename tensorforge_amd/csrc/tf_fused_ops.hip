@@ -13,6 +13,9 @@
 //                      stored rounded, the norm uses the fp32 sum
 //   swiglu             triton_ops.py:106-122, :246-260 -- g*sigmoid(g)*u in
 //                      fp32, one rounding
+//   swiglu_rows        the same activation read from one fused gate|up
+//                      projection row (no reference counterpart: the
+//                      reference runs gate and up as two GEMMs)
 #include "tf_common.hpp"
 
 namespace tf {
@@ -97,6 +100,18 @@ rms_norm_kernel(const T *__restrict__ inputs, const T *__restrict__ residual,
 }
 
 template <typename T, int VEC>
+__device__ __forceinline__ Vec<T, VEC> swiglu_vec(const Vec<T, VEC> &gv, const Vec<T, VEC> &uv) {
+  Vec<T, VEC> out;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    const float x = to_float(gv.v[e]);
+    const float silu = x / (1.0f + expf(-x));
+    out.v[e] = from_float<T>(silu * to_float(uv.v[e]));
+  }
+  return out;
+}
+
+template <typename T, int VEC>
 __global__ void __launch_bounds__(256)
 swiglu_kernel(const T *__restrict__ gate, const T *__restrict__ up, T *__restrict__ output,
               int64_t nvec) {
@@ -105,17 +120,25 @@ swiglu_kernel(const T *__restrict__ gate, const T *__restrict__ up, T *__restric
   const V *u = reinterpret_cast<const V *>(up);
   V *o = reinterpret_cast<V *>(output);
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec; i += stride) {
-    V gv = g[i];
-    V uv = u[i];
-    V out;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float x = to_float(gv.v[e]);
-      const float silu = x / (1.0f + expf(-x));
-      out.v[e] = from_float<T>(silu * to_float(uv.v[e]));
-    }
-    o[i] = out;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < nvec; i += stride)
+    o[i] = swiglu_vec<T, VEC>(g[i], u[i]);
+}
+
+// Row r of `gate_up` holds gate[0..columns) then up[0..columns); strides in
+// elements.  cvec = columns / VEC vectors per row.
+template <typename T, int VEC>
+__global__ void __launch_bounds__(256)
+swiglu_rows_kernel(const T *__restrict__ gate_up, int64_t in_stride, T *__restrict__ output,
+                   int64_t out_stride, int64_t rows, int32_t cvec) {
+  using V = Vec<T, VEC>;
+  const int64_t total = rows * cvec;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += stride) {
+    const int64_t r = i / cvec;
+    const int64_t c = i - r * cvec;
+    const V *g = reinterpret_cast<const V *>(gate_up + r * in_stride);
+    reinterpret_cast<V *>(output + r * out_stride)[c] = swiglu_vec<T, VEC>(g[c], g[cvec + c]);
   }
 }
 
@@ -211,6 +234,32 @@ int32_t swiglu_dispatch(const void *gate, const void *up, void *output, int64_t 
   return check_launch("swiglu");
 }
 
+template <typename T>
+int32_t swiglu_rows_dispatch(const void *gate_up, int64_t in_stride, void *output,
+                             int64_t out_stride, int64_t rows, int32_t columns,
+                             hipStream_t stream) {
+  constexpr int kVec = 16 / sizeof(T);
+  const uintptr_t align = reinterpret_cast<uintptr_t>(gate_up) |
+                          reinterpret_cast<uintptr_t>(output) |
+                          static_cast<uintptr_t>(in_stride * sizeof(T)) |
+                          static_cast<uintptr_t>(out_stride * sizeof(T)) |
+                          static_cast<uintptr_t>(columns * sizeof(T));
+  const int threads = 256;
+  const bool vec = align % 16 == 0;
+  const int32_t cvec = vec ? columns / kVec : columns;
+  int64_t blocks = (rows * cvec + threads - 1) / threads;
+  if (blocks > 8192) blocks = 8192;
+  if (vec)
+    hipLaunchKernelGGL((swiglu_rows_kernel<T, kVec>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(threads), 0, stream, static_cast<const T *>(gate_up), in_stride,
+                       static_cast<T *>(output), out_stride, rows, cvec);
+  else
+    hipLaunchKernelGGL((swiglu_rows_kernel<T, 1>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(threads), 0, stream, static_cast<const T *>(gate_up), in_stride,
+                       static_cast<T *>(output), out_stride, rows, cvec);
+  return check_launch("swiglu_rows");
+}
+
 }  // namespace
 }  // namespace tf
 
@@ -245,5 +294,30 @@ extern "C" int32_t tf_swiglu(const void *gate, const void *up, void *output, int
       return swiglu_dispatch<_Float16>(gate, up, output, numel, s);
     default:
       return swiglu_dispatch<__bf16>(gate, up, output, numel, s);
+  }
+}
+
+extern "C" int32_t tf_swiglu_rows(const void *gate_up, int64_t gate_up_row_stride, void *output,
+                                  int64_t output_row_stride, int64_t rows, int32_t columns,
+                                  int32_t dtype, void *stream) {
+  using namespace tf;
+  clear_error();
+  if (!valid_dtype(dtype)) return fail(TF_ERROR_INVALID_ARGUMENT, "unsupported dtype code");
+  if (rows < 0 || columns < 0) return fail(TF_ERROR_INVALID_ARGUMENT, "sizes must be non-negative");
+  if (gate_up_row_stride < 2 * static_cast<int64_t>(columns) || output_row_stride < columns)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "row strides are shorter than the rows");
+  if (rows == 0 || columns == 0) return TF_SUCCESS;
+  if (!gate_up || !output) return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TF_DTYPE_FLOAT32:
+      return swiglu_rows_dispatch<float>(gate_up, gate_up_row_stride, output, output_row_stride,
+                                         rows, columns, s);
+    case TF_DTYPE_FLOAT16:
+      return swiglu_rows_dispatch<_Float16>(gate_up, gate_up_row_stride, output,
+                                            output_row_stride, rows, columns, s);
+    default:
+      return swiglu_rows_dispatch<__bf16>(gate_up, gate_up_row_stride, output,
+                                          output_row_stride, rows, columns, s);
   }
 }

@@ -5,12 +5,12 @@ One decode step of a Llama-style decoder for up to ``batch_capacity``
 sequences runs as ONE captured HIP graph.  Per layer:
 
 * ``rms_norm`` (first layer) or the fused ``residual_rms_norm``;
-* a single fused QKV projection, then RoPE;
-* ``paged_kv_write_token`` for the new token;
+* one fused QKV projection;
+* ``rope_paged_kv_append``: RoPE on q and k, and k, v into their pages;
 * ``paged_gqa_decode_attention`` (split stage + merge);
 * the output projection;
 * ``residual_rms_norm`` of (attention output, residual);
-* the gate and up projections, ``swiglu``, and the down projection.
+* one fused gate|up projection, ``swiglu_gate_up``, the down projection.
 
 The gfx950 kernels of this package do the norm, cache and attention work;
 the GEMMs are library GEMMs (torch -> hipBLASLt).  Every per-step input
@@ -43,7 +43,7 @@ from tensorforge_amd.kernels import (
     residual_rms_norm,
     rms_norm,
     rope_paged_kv_append,
-    swiglu,
+    swiglu_gate_up,
 )
 from tensorforge_amd.kernels.attention import attention_split_size_for, set_attention_split_size
 
@@ -87,9 +87,16 @@ class LayerWeights:
     qkv: Tensor         # [(Hq + 2 Hkv) D, H]: q, k, v projections stacked
     o_proj: Tensor      # [H, Hq D]
     post_norm: Tensor   # [H]
-    gate: Tensor        # [F, H]
-    up: Tensor          # [F, H]
+    gate_up: Tensor     # [2F, H]: gate and up projections stacked (one GEMM)
     down: Tensor        # [H, F]
+
+    @property
+    def gate(self) -> Tensor:
+        return self.gate_up[: self.gate_up.shape[0] // 2]
+
+    @property
+    def up(self) -> Tensor:
+        return self.gate_up[self.gate_up.shape[0] // 2:]
 
 
 @dataclass(slots=True)
@@ -119,8 +126,8 @@ class DecoderWeights:
         hq, hkv = config.num_attention_heads, config.num_key_value_heads
         layers = [
             LayerWeights(input_norm=ones(h), qkv=normal((hq + 2 * hkv) * d, h),
-                         o_proj=normal(h, hq * d), post_norm=ones(h), gate=normal(f, h),
-                         up=normal(f, h), down=normal(h, f))
+                         o_proj=normal(h, hq * d), post_norm=ones(h), gate_up=normal(2 * f, h),
+                         down=normal(h, f))
             for _ in range(config.num_hidden_layers)
         ]
         # RoPE tables: angles in fp64, cos/sin rounded once to the model dtype
@@ -351,8 +358,7 @@ class DecodeGraphBucket:
                 residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps,
                                                 residual_output=torch.empty_like(attn),
                                                 norm_output=self.norm_output)
-                act = swiglu(F.linear(h, layer.gate), F.linear(h, layer.up),
-                             output=self.swiglu_output)
+                act = swiglu_gate_up(F.linear(h, layer.gate_up), output=self.swiglu_output)
                 mlp = F.linear(act, layer.down)
                 next_norm = (self.weights.layers[index + 1].input_norm
                              if index + 1 < len(self.weights.layers) else self.weights.final_norm)
@@ -400,7 +406,7 @@ def prefill(weights: DecoderWeights, cache: PagedKVCache, request_id: str,
         context = context.transpose(0, 1).reshape(seq, hq * d).to(q.dtype)
         attn = F.linear(context, layer.o_proj)
         residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps)
-        act = swiglu(F.linear(h, layer.gate), F.linear(h, layer.up))
+        act = swiglu_gate_up(F.linear(h, layer.gate_up))
         next_norm = (weights.layers[index + 1].input_norm
                      if index + 1 < len(weights.layers) else weights.final_norm)
         residual, h = residual_rms_norm(F.linear(act, layer.down), residual, next_norm, eps)

@@ -21,6 +21,7 @@ from tensorforge_amd.kernels.ops import (
     rms_norm,
     selected_autotune_config,
     swiglu,
+    swiglu_gate_up,
 )
 from tensorforge_amd.kernels.rope import rope_paged_kv_append
 
@@ -40,4 +41,5 @@ __all__ = [
     "selected_autotune_config",
     "set_attention_split_size",
     "swiglu",
+    "swiglu_gate_up",
 ]

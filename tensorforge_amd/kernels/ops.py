@@ -220,6 +220,39 @@ def swiglu(gate: Tensor, up: Tensor, *, output: Tensor | None = None) -> Tensor:
     return output
 
 
+def swiglu_gate_up(gate_up: Tensor, *, output: Tensor | None = None) -> Tensor:
+    """SwiGLU over a fused gate|up projection ``[rows, >= 2F]`` (rows may be
+    strided): ``output[r] = silu(gate_up[r, :F]) * gate_up[r, F:2F]`` with
+    ``F = output.shape[-1]`` (or half the row length).  The arithmetic of
+    :func:`swiglu`; no reference counterpart (the reference projects gate and
+    up separately, model/layers.py:146-158)."""
+
+    _require_library()
+    if gate_up.ndim != 2 or gate_up.stride(1) != 1:
+        raise ValueError("gate_up must be [rows, features] with contiguous rows")
+    if not gate_up.is_cuda:
+        raise ValueError("swiglu_gate_up requires CUDA tensors")
+    if gate_up.dtype not in _native.DTYPE_CODES:
+        raise TypeError(f"unsupported dtype: {gate_up.dtype}")
+    rows = gate_up.shape[0]
+    columns = output.shape[-1] if output is not None else gate_up.shape[1] // 2
+    if 2 * columns > gate_up.shape[1]:
+        raise ValueError("gate_up rows are shorter than twice the output width")
+    if output is None:
+        output = torch.empty((rows, columns), dtype=gate_up.dtype, device=gate_up.device)
+    if (output.shape != (rows, columns) or output.dtype != gate_up.dtype
+            or output.device != gate_up.device or output.stride(1) != 1):
+        raise ValueError("output must be [rows, F] with contiguous rows, gate_up's dtype and device")
+    _native.check(
+        _native.library().tf_swiglu_rows(
+            gate_up.data_ptr(), gate_up.stride(0), output.data_ptr(), output.stride(0), rows,
+            columns, _native.dtype_code(gate_up.dtype), _native.current_stream(gate_up.device),
+        ),
+        "swiglu_gate_up",
+    )
+    return output
+
+
 def selected_autotune_config(operation: str) -> dict[str, Any] | None:
     """Most recent launch configuration of ``operation`` (reference: triton_ops.py:263-283)."""
 

@@ -25,6 +25,7 @@ from tensorforge_amd.kernels import (
     rms_norm,
     selected_autotune_config,
     swiglu,
+    swiglu_gate_up,
 )
 
 pytestmark = pytest.mark.gpu
@@ -169,3 +170,24 @@ def test_caller_owned_outputs_are_reused_and_numerically_correct(device):
     assert_close(residual_output, expected_residual, 3e-3, 3e-3, "residual")
     assert_close(post_norm_output, expected_post, 3e-3, 3e-3, "post norm")
     assert_close(swiglu_output, swiglu_reference(gate, up), 3e-3, 3e-3, "swiglu")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize(("rows", "ffn", "pad"), [(1, 5632, 0), (64, 5632, 0), (8, 14336, 0),
+                                                  (3, 77, 0), (5, 256, 8), (7, 96, 3)])
+def test_swiglu_gate_up_equals_separate_swiglu(device, dtype, rows, ffn, pad):
+    """The fused gate|up form is bit-identical to swiglu on the two halves
+    (same arithmetic), for vector and scalar paths and padded row strides."""
+
+    generator = torch.Generator().manual_seed(rows * 31 + ffn)
+    gate_up = torch.randn(rows, 2 * ffn + pad, generator=generator).to(dtype).to(device)
+    actual = swiglu_gate_up(gate_up[:, :2 * ffn] if pad else gate_up, output=None)
+    gate = gate_up[:, :ffn].contiguous()
+    up = gate_up[:, ffn:2 * ffn].contiguous()
+    assert_bit_exact(actual, swiglu(gate, up), f"gate_up {rows}x{ffn}+{pad} {dtype}")
+    tol = REFERENCE_TOLERANCE[dtype]
+    assert_close(actual, swiglu_reference(gate.cpu(), up.cpu()), tol, tol, "oracle")
+    wide = torch.zeros(rows, ffn + 5, dtype=dtype, device=device)
+    swiglu_gate_up(gate_up[:, :2 * ffn + pad], output=wide[:, :ffn])
+    assert_bit_exact(wide[:, :ffn], actual, "strided output")
+    assert not wide[:, ffn:].any()
