@@ -21,9 +21,10 @@
  *                            (slot-mapping form of the multi-token scatter)
  *   tf_paged_kv_write_range  tensorforge/cache/paged.py:191-236
  *                            (PagedKVCache.write_layer through a table row)
- *   tf_rope_kv_append        tensorforge/model/layers.py:57-69 (batched RoPE)
+ *   tf_rope_kv_append        tensorforge/model/layers.py:46-69 (RoPE)
  *                            + tensorforge/runtime/decode_bucket.py:448-458
- *                            (the decode step's cache write)
+ *                            (the decode step's cache write) and
+ *                            runtime/prefill.py:99-115 (prefill's)
  *   tf_rms_norm              tensorforge/kernels/triton_ops.py:179-205
  *   tf_residual_rms_norm     tensorforge/kernels/triton_ops.py:208-243
  *   tf_swiglu                tensorforge/kernels/triton_ops.py:246-260
@@ -196,23 +197,27 @@ int32_t tf_paged_kv_write_range(
     int32_t block_size, int32_t dtype, void *stream);
 
 /*
- * Decode-step RoPE fused with the paged KV append.  qkv [batch, row] with
+ * RoPE fused with the paged KV append (a decode step's lanes, or the packed
+ * tokens of several prompts).  qkv [batch, row] with
  * row stride qkv_row_stride elements holds [q heads | k heads | v heads]
  * (head_dim each); cos_table/sin_table [table_rows, head_dim] in the same
  * dtype; positions int64 [batch] (clamped into the table).  Writes the
  * rotated query to query_out [batch, query_heads, head_dim] for every lane,
- * and for lanes with active_mask != 0 the rotated key and the value into
- * cache token row (physical_blocks[b], block_offsets[b]).  Rotation
+ * the rotated key to key_out [batch, kv_heads, head_dim] when key_out is not
+ * NULL, and for lanes with active_mask != 0 the rotated key and the value
+ * into cache token row (physical_blocks[b], block_offsets[b]).  Rotation
  * (half-split): out[j] = x[j] cos[j] - x[j+D/2] sin[j],
  * out[j+D/2] = x[j+D/2] cos[j+D/2] + x[j] sin[j+D/2], fp32 arithmetic,
  * one rounding.  Replaces apply_batched_rotary_embedding
  * (model/layers.py:57-69) and the write at runtime/decode_bucket.py:448-458
- * (kernels/triton_cache.py:23-63), with their .contiguous() copies.
+ * (kernels/triton_cache.py:23-63), with their .contiguous() copies; for
+ * prefill, apply_rotary_embedding and the per-request write_layer loop of
+ * runtime/prefill.py:99-115.
  */
 int32_t tf_rope_kv_append(
     const void *qkv, int64_t qkv_row_stride, const int64_t *positions,
     const void *cos_table, const void *sin_table, int32_t table_rows,
-    void *query_out, void *key_cache, void *value_cache,
+    void *query_out, void *key_out, void *key_cache, void *value_cache,
     const int32_t *physical_blocks, const int32_t *block_offsets,
     const int32_t *active_mask, int32_t batch, int32_t query_heads,
     int32_t kv_heads, int32_t head_dim, int32_t num_blocks, int32_t block_size,

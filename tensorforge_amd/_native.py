@@ -76,7 +76,7 @@ SIGNATURES: dict[str, tuple[Any, ...]] = {
     ),
     "tf_rope_kv_append": (
         _p, _i64, _p, _p, _p, _i32,  # qkv, row stride, positions, cos, sin, table rows
-        _p, _p, _p, _p, _p, _p,  # query out, key/value cache, pages, offsets, active
+        _p, _p, _p, _p, _p, _p, _p,  # query/key out, key/value cache, pages, offsets, active
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p,  # batch .. block size, dtype, stream
     ),
     "tf_rms_norm": (_p, _p, _p, _i64, _i32, _f32, _i32, _p),

@@ -1,6 +1,8 @@
-// Fused decode RoPE + paged KV append: one launch per layer turns the fused
-// QKV projection of a decode batch into the rotated query and writes the
-// rotated key and the value of every active lane into its cache page.
+// Fused RoPE + paged KV append: one launch per layer turns the fused QKV
+// projection of a batch of tokens (one per decode lane, or a packed set of
+// prompts) into the rotated query and writes the rotated key and the value
+// of every active token into its cache page; optionally also the rotated key
+// densely (prefill attention reads it).
 //
 // Input row b of `qkv` holds [q heads | k heads | v heads], head_dim each.
 // RoPE uses the half-split rotation with per-dimension cos/sin tables
@@ -15,7 +17,9 @@
 //   cache write           tensorforge/runtime/decode_bucket.py:448-458 ->
 //                         tensorforge/kernels/triton_cache.py:23-63
 //                         (masked lanes store nothing)
-//   the .contiguous() copies of q, k and v at decode_bucket.py:449-450, 460.
+//   the .contiguous() copies of q, k and v at decode_bucket.py:449-450, 460
+//   prefill RoPE + append runtime/prefill.py:99-115 (apply_rotary_embedding,
+//                         then one write_layer per request)
 #include "tf_common.hpp"
 
 namespace tf {
@@ -29,7 +33,8 @@ __global__ void __launch_bounds__(256)
 rope_kv_append_kernel(const T *__restrict__ qkv, int64_t row_stride,
                       const int64_t *__restrict__ positions, const T *__restrict__ cos_table,
                       const T *__restrict__ sin_table, int32_t table_rows,
-                      T *__restrict__ query_out, T *__restrict__ key_cache,
+                      T *__restrict__ query_out, T *__restrict__ key_out,
+                      T *__restrict__ key_cache,
                       T *__restrict__ value_cache, const int32_t *__restrict__ physical_blocks,
                       const int32_t *__restrict__ block_offsets,
                       const int32_t *__restrict__ active_mask, int32_t query_heads,
@@ -60,14 +65,24 @@ rope_kv_append_kernel(const T *__restrict__ qkv, int64_t row_stride,
     const float x2 = to_float(src[j + half]);
     const float o1 = x1 * to_float(cs[j]) - x2 * to_float(sn[j]);
     const float o2 = x2 * to_float(cs[j + half]) + x1 * to_float(sn[j + half]);
+    const T r1 = from_float<T>(o1);
+    const T r2 = from_float<T>(o2);
     if (head < query_heads) {
       T *dst = q_row + static_cast<int64_t>(head) * head_dim;
-      dst[j] = from_float<T>(o1);
-      dst[j + half] = from_float<T>(o2);
-    } else if (store) {
-      T *dst = key_cache + slot * row_elems + static_cast<int64_t>(head - query_heads) * head_dim;
-      dst[j] = from_float<T>(o1);
-      dst[j + half] = from_float<T>(o2);
+      dst[j] = r1;
+      dst[j + half] = r2;
+    } else {
+      const int64_t kh = static_cast<int64_t>(head - query_heads) * head_dim;
+      if (store) {
+        T *dst = key_cache + slot * row_elems + kh;
+        dst[j] = r1;
+        dst[j + half] = r2;
+      }
+      if (key_out) {
+        T *dst = key_out + b * row_elems + kh;
+        dst[j] = r1;
+        dst[j + half] = r2;
+      }
     }
   }
   if (store) {
@@ -82,7 +97,7 @@ rope_kv_append_kernel(const T *__restrict__ qkv, int64_t row_stride,
 
 extern "C" int32_t tf_rope_kv_append(
     const void *qkv, int64_t qkv_row_stride, const int64_t *positions, const void *cos_table,
-    const void *sin_table, int32_t table_rows, void *query_out, void *key_cache,
+    const void *sin_table, int32_t table_rows, void *query_out, void *key_out, void *key_cache,
     void *value_cache, const int32_t *physical_blocks, const int32_t *block_offsets,
     const int32_t *active_mask, int32_t batch, int32_t query_heads, int32_t kv_heads,
     int32_t head_dim, int32_t num_blocks, int32_t block_size, int32_t dtype, void *stream) {
@@ -109,7 +124,8 @@ extern "C" int32_t tf_rope_kv_append(
   hipLaunchKernelGGL((rope_kv_append_kernel<T>), grid, block, 0, s,                          \
                      static_cast<const T *>(qkv), qkv_row_stride, positions,                 \
                      static_cast<const T *>(cos_table), static_cast<const T *>(sin_table),   \
-                     table_rows, static_cast<T *>(query_out), static_cast<T *>(key_cache),   \
+                     table_rows, static_cast<T *>(query_out), static_cast<T *>(key_out),     \
+                     static_cast<T *>(key_cache),                                            \
                      static_cast<T *>(value_cache), physical_blocks, block_offsets,          \
                      active_mask, query_heads, kv_heads, head_dim, num_blocks, block_size)
   switch (dtype) {

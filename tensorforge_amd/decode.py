@@ -35,6 +35,7 @@ import numpy as np
 import torch
 from torch import Tensor
 from torch.nn import functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from tensorforge_amd.cache import AppendReservation, PagedKVCache
 from tensorforge_amd.kernels import (
@@ -140,14 +141,6 @@ class DecoderWeights:
                    final_norm=ones(h), lm_head=normal(config.vocab_size, h),
                    rope_cos=angles.cos().to(dtype).to(device),
                    rope_sin=angles.sin().to(dtype).to(device))
-
-
-def _rope(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
-    """x [B, heads, D]; cos/sin [B, D]: x cos + rotate_half(x) sin."""
-
-    half = x.shape[-1] // 2
-    rotated = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
-    return x * cos[:, None, :] + rotated * sin[:, None, :]
 
 
 class DecodeGraphBucket:
@@ -373,46 +366,111 @@ class DecodeGraphBucket:
 
 def prefill(weights: DecoderWeights, cache: PagedKVCache, request_id: str,
             prompt: list[int]) -> tuple[int, Tensor]:
-    """Write the prompt's K/V into the cache and return (greedy next token,
-    last-position logits).  Full-prefix forward in fp32 on the device (the
-    reference's prefill path, runtime/prefill.py:36-149): projections in the
-    model dtype, causal attention in fp32 with contiguous operands."""
+    """One prompt: (greedy next token, last-position logits) -- the
+    reference's prefill_request (runtime/prefill.py:19-34)."""
 
+    return prefill_batch(weights, cache, {request_id: prompt})[request_id]
+
+
+def _causal_attention(q: Tensor, k: Tensor, v: Tensor, scale: float) -> Tensor:
+    """q [S, Hq, D], k/v [S, Hkv, D] of one prompt -> context [S, Hq * D]:
+    causal attention through torch's fused (flash / memory-efficient) SDPA
+    kernels with contiguous operands, kv heads expanded to the query heads.
+    The math backend is excluded: it would run batched products on
+    transposed views."""
+
+    seq, hq, d = q.shape
+    group = hq // k.shape[1]
+    qh = q.transpose(0, 1).unsqueeze(0).contiguous()                           # [1, Hq, S, D]
+    kh = k.repeat_interleave(group, dim=1).transpose(0, 1).unsqueeze(0).contiguous()
+    vh = v.repeat_interleave(group, dim=1).transpose(0, 1).unsqueeze(0).contiguous()
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        context = F.scaled_dot_product_attention(qh, kh, vh, is_causal=True, scale=scale)
+    return context[0].transpose(0, 1).reshape(seq, hq * d)
+
+
+def prefill_batch(weights: DecoderWeights, cache: PagedKVCache,
+                  prompts: dict[str, list[int]]) -> dict[str, tuple[int, Tensor]]:
+    """Prefill several fresh prompts together: {request_id: (greedy next
+    token, last-position logits)}.
+
+    The reference pads the prompts into one [batch, longest] causal batch
+    and writes each request's K/V with its own write_layer per layer
+    (runtime/prefill.py:37-149).  Here the prompts' tokens are packed into
+    one [total, H] stream with no padding: every projection is one GEMM over
+    all tokens, and one rope_paged_kv_append launch per layer rotates q and k
+    of every token and writes k, v straight into the pages each token's
+    position maps to.  Attention runs per prompt through torch's fused
+    causal SDPA.  All reservations commit together, or roll back together on
+    an error.
+    """
+
+    if not prompts:
+        raise ValueError("prefill_batch requires at least one prompt")
     config = weights.config
     hq, hkv, d = config.num_attention_heads, config.num_key_value_heads, config.head_dim
     device = cache.config.device
-    seq = len(prompt)
-    reservation = cache.begin_append(request_id, seq)
-    tokens = torch.tensor(prompt, dtype=torch.long, device=device)
-    positions = torch.arange(reservation.start_position, reservation.end_position, device=device)
-    cos = weights.rope_cos.index_select(0, positions)
-    sin = weights.rope_sin.index_select(0, positions)
-    eps = config.rms_norm_eps
-    residual = F.embedding(tokens, weights.embedding)
-    h = rms_norm(residual, weights.layers[0].input_norm, eps)
-    causal = torch.ones(seq, seq, dtype=torch.bool, device=device).triu(1)
-    for index, layer in enumerate(weights.layers):
-        qkv = F.linear(h, layer.qkv)
-        q = _rope(qkv[:, :hq * d].view(seq, hq, d), cos, sin)
-        k = _rope(qkv[:, hq * d:(hq + hkv) * d].view(seq, hkv, d), cos, sin).contiguous()
-        v = qkv[:, (hq + hkv) * d:].reshape(seq, hkv, d).contiguous()
-        cache.write_layer(reservation, index, k, v)
-        qf = q.float().transpose(0, 1).contiguous()                       # [hq, seq, d]
-        kf = k.float().repeat_interleave(hq // hkv, dim=1).transpose(0, 1).contiguous()
-        vf = v.float().repeat_interleave(hq // hkv, dim=1).transpose(0, 1).contiguous()
-        scores = torch.matmul(qf, kf.transpose(1, 2).contiguous()) * d ** -0.5
-        scores = scores.masked_fill(causal, float("-inf"))
-        context = torch.matmul(torch.softmax(scores, dim=-1), vf)          # [hq, seq, d]
-        context = context.transpose(0, 1).reshape(seq, hq * d).to(q.dtype)
-        attn = F.linear(context, layer.o_proj)
-        residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps)
-        act = swiglu_gate_up(F.linear(h, layer.gate_up))
-        next_norm = (weights.layers[index + 1].input_norm
-                     if index + 1 < len(weights.layers) else weights.final_norm)
-        residual, h = residual_rms_norm(F.linear(act, layer.down), residual, next_norm, eps)
-    logits = F.linear(h[-1:], weights.lm_head)[0]
-    cache.commit(reservation)
-    return int(torch.argmax(logits)), logits
+    block_size = cache.config.block_size
+    reservations: dict[str, AppendReservation] = {}
+    try:
+        for request_id, prompt in prompts.items():
+            if not prompt:
+                raise ValueError("prompt must contain at least one token")
+            if cache.sequence_layout(request_id).context_length != 0:
+                raise ValueError("prefill_batch ingests fresh sequences only")
+            if len(prompt) > weights.rope_cos.shape[0]:
+                raise ValueError("prompt exceeds the model's RoPE table")
+            reservations[request_id] = cache.begin_append(request_id, len(prompt))
+        request_ids = list(prompts)
+        lengths = [len(prompts[r]) for r in request_ids]
+        bounds = np.concatenate(([0], np.cumsum(lengths)))
+        total = int(bounds[-1])
+        longs = np.empty((2, total), dtype=np.int64)   # token ids, positions
+        ints = np.ones((3, total), dtype=np.int32)     # pages, offsets, active
+        for i, request_id in enumerate(request_ids):
+            lo, hi = bounds[i], bounds[i + 1]
+            positions = np.arange(hi - lo, dtype=np.int64)
+            pages = np.asarray(cache.page_list(request_id)[0], dtype=np.int32)
+            longs[0, lo:hi] = prompts[request_id]
+            longs[1, lo:hi] = positions
+            ints[0, lo:hi] = pages[positions // block_size]
+            ints[1, lo:hi] = positions % block_size
+        longs_dev = torch.from_numpy(longs).to(device)
+        ints_dev = torch.from_numpy(ints).to(device)
+        tokens, positions_dev = longs_dev[0], longs_dev[1]
+        eps = config.rms_norm_eps
+        residual = F.embedding(tokens, weights.embedding)
+        h = rms_norm(residual, weights.layers[0].input_norm, eps)
+        q = torch.empty((total, hq, d), dtype=residual.dtype, device=device)
+        k = torch.empty((total, hkv, d), dtype=residual.dtype, device=device)
+        context = torch.empty((total, hq * d), dtype=residual.dtype, device=device)
+        for index, layer in enumerate(weights.layers):
+            qkv = F.linear(h, layer.qkv)
+            rope_paged_kv_append(qkv, positions_dev, weights.rope_cos, weights.rope_sin,
+                                 cache.key_cache[index], cache.value_cache[index], ints_dev[0],
+                                 ints_dev[1], ints_dev[2], query_heads=hq, query_output=q,
+                                 key_output=k)
+            v = qkv[:, (hq + hkv) * d:].view(total, hkv, d)
+            for i in range(len(request_ids)):
+                lo, hi = int(bounds[i]), int(bounds[i + 1])
+                context[lo:hi] = _causal_attention(q[lo:hi], k[lo:hi], v[lo:hi], d ** -0.5)
+            attn = F.linear(context, layer.o_proj)
+            residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps)
+            act = swiglu_gate_up(F.linear(h, layer.gate_up))
+            next_norm = (weights.layers[index + 1].input_norm
+                         if index + 1 < len(weights.layers) else weights.final_norm)
+            residual, h = residual_rms_norm(F.linear(act, layer.down), residual, next_norm, eps)
+        last = torch.from_numpy(bounds[1:] - 1).to(device)
+        logits = F.linear(h.index_select(0, last), weights.lm_head)
+        first_tokens = torch.argmax(logits, dim=-1).tolist()
+    except Exception:
+        for reservation in reservations.values():
+            cache.rollback(reservation)
+        raise
+    for reservation in reservations.values():
+        cache.record_all_layers_written(reservation)
+        cache.commit(reservation)
+    return {request_id: (first_tokens[i], logits[i]) for i, request_id in enumerate(request_ids)}
 
 
 DEFAULT_BATCH_BUCKETS = (1, 2, 4, 8, 16, 32, 64)
@@ -489,10 +547,11 @@ class BucketedDecodeExecutor:
         self.cache.release(request_id)
 
     def prefill_prompts(self, prompts: dict[str, list[int]]) -> dict[str, int]:
-        """Prefill each prompt; returns its greedy first token."""
+        """Prefill the prompts together; returns each one's greedy first token
+        (decode_bucket.py:567-570)."""
 
-        return {rid: prefill(self.weights, self.cache, rid, prompt)[0]
-                for rid, prompt in prompts.items()}
+        return {rid: token for rid, (token, _) in
+                prefill_batch(self.weights, self.cache, prompts).items()}
 
     def buffer_addresses(self) -> dict[str, dict[str, int]]:
         return {f"b{batch}-c{context}": bucket.addresses()

@@ -23,6 +23,7 @@ from tensorforge_amd.decode import (
     DecoderWeights,
     greedy_decode,
     prefill,
+    prefill_batch,
     small_config,
 )
 
@@ -75,6 +76,34 @@ def test_prefill_logits_match_the_oracle(device):
         assert err <= 2e-2 * scale, f"{rid}: max |dlogits| {err:.3e} vs scale {scale:.3e}"
         assert token == int(torch.argmax(expected)) or \
             float(expected.max() - expected[token]) <= 4 * err
+
+
+def test_batched_prefill_matches_the_oracle_and_single_prefill(device):
+    """Four prompts packed into one prefill: each one's logits match the
+    oracle and a prefill of that prompt alone, and its pages hold what the
+    single prefill wrote (within one rounding of the projections)."""
+
+    config = small_config()
+    weights = DecoderWeights.random(config, seed=0, dtype=torch.float16, device=device)
+    prompts = _prompts()
+    together = _cache(config, device)
+    for rid in prompts:
+        together.create_sequence(rid)
+    batched = prefill_batch(weights, together, prompts)
+    for rid, prompt in prompts.items():
+        alone = _cache(config, device)
+        alone.create_sequence(rid)
+        token, logits = prefill(weights, alone, rid, prompt)
+        expected = decoder_forward(weights, torch.tensor(prompt))[-1]
+        scale = float(expected.abs().max())
+        assert float((batched[rid][1].float().cpu() - expected).abs().max()) <= 2e-2 * scale
+        assert float((batched[rid][1] - logits).abs().max()) <= 1e-2 * scale
+        for layer in (0, config.num_hidden_layers - 1):
+            k_batched, v_batched = together.materialize(rid, layer)
+            k_alone, v_alone = alone.materialize(rid, layer)
+            torch.testing.assert_close(k_batched.float(), k_alone.float(), rtol=1e-2, atol=1e-2)
+            torch.testing.assert_close(v_batched.float(), v_alone.float(), rtol=1e-2, atol=1e-2)
+        assert together.sequence_layout(rid).context_length == len(prompt)
 
 
 def test_greedy_decode_matches_the_oracle(device):

@@ -73,6 +73,30 @@ def test_rope_append_matches_the_oracle(device, dtype, batch, hq, hkv, d):
     assert_bit_exact(k_dev.cpu()[~touched], key_cache[~touched], "untouched key rows")
 
 
+def test_rope_append_writes_dense_keys(device):
+    """key_output receives every lane's rotated key, masked lanes included,
+    bit-identical to what active lanes store in their pages."""
+
+    case = _case(24, 8, 2, 64, torch.bfloat16, seed=5)
+    qkv, positions, cos, sin, key_cache, value_cache, pages, offsets, active = \
+        [t.to(device) for t in case]
+    keys = torch.empty(24, 2, 64, dtype=torch.bfloat16, device=device)
+    rope_paged_kv_append(qkv, positions, cos, sin, key_cache, value_cache, pages, offsets, active,
+                         query_heads=8, key_output=keys)
+    q_ref, k_ref, _ = rope_kv_append_reference(*case, 8)
+    for lane in range(24):
+        if case[8][lane]:
+            assert_bit_exact(keys[lane], key_cache[pages[lane], offsets[lane]], f"lane {lane}")
+    # The oracle's rotation of lane b's key equals q's formula on the k head.
+    rows = case[0].float().view(24, 12, 64)
+    half = 32
+    cs = case[2].float()[case[1]][:, None, :]
+    sn = case[3].float()[case[1]][:, None, :]
+    k_in = rows[:, 8:10]
+    expected = k_in * cs + torch.cat((-k_in[..., half:], k_in[..., :half]), -1) * sn
+    torch.testing.assert_close(keys.float().cpu(), expected, rtol=3e-2, atol=3e-2)
+
+
 def test_rope_append_reads_strided_rows(device):
     """qkv as a column slice of a wider projection output (row stride >
     row length), as when the projection is fused with another GEMM."""
