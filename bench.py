@@ -18,6 +18,12 @@ call costs the host longer than the kernel takes, so eager steps would
 time the host).  ``roofline`` reports the dominant kernel, the split stage,
 timed the same way from a graph of K split-stage launches alone.
 ``cpu_baseline`` is the CPU oracle on the same rows, on this host's cores.
+
+``decode_step`` is the metric's "decode tokens/s" part: a whole
+graph-captured decode step of the 22-layer TinyLlama-geometry model (random
+init, bf16) for the same 64 rows, with prompts of the rows' context lengths,
+and beside it the oracle's fp32 incremental decode step on 4 rows on the
+host cores.
 """
 
 from __future__ import annotations
@@ -56,6 +62,8 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--cpu-seconds", type=float, default=10.0,
                         help="target CPU time of the oracle baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-decode-step", action="store_true",
+                        help="skip the 22-layer decode-step tokens/s part of the metric")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
                         help="only run a plain device copy of this many MiB (counter calibration)")
     return parser.parse_args()
@@ -107,6 +115,86 @@ def cpu_baseline(case, rows: list[int], seconds: float) -> dict:
             f"CPU oracle paged_gqa_decode_reference (fp32 torch {torch.__version__}) on "
             f"{len(rows)} of the 64 active rows (sum ctx {sum(lengths)}), p50 of "
             f"{len(samples)} reps = {p50 * 1e3:.2f} ms; {platform.processor() or platform.machine()}"
+        ),
+    }
+
+
+def decode_step(lengths: list[int], cpu_seconds: float, with_cpu: bool) -> dict:
+    """The metric's "decode tokens/s" part: one graph-captured decode step of
+    the 22-layer TinyLlama-geometry model (random init, bf16) for the 64
+    active rows of this workload, prompts of the workload's context lengths
+    (less the steps decoded), context bucket 2048.  The CPU baseline is the
+    fp32 incremental decode step of the oracle on 4 of the rows."""
+
+    from tensorforge_amd.decode import DecoderWeights, tinyllama_config
+    from tensorforge_amd.kernel_bench import measure_decode_step
+
+    device = torch.device("cuda", 0)
+    config = tinyllama_config()
+    weights = DecoderWeights.random(config, seed=0, dtype=torch.bfloat16, device=device)
+    active = [n for n in lengths if n > 0]
+    steps = 40
+    prompts = [max(1, min(n, 2048 - steps - 8)) for n in active]
+    gpu = measure_decode_step(weights, len(active), 2048, steps=steps, prompt_lengths=prompts)
+    result = {
+        "model": "TinyLlama-1.1B geometry, 22 layers, random init (seed 0), bf16",
+        "batch": len(active),
+        "tokens_per_second": gpu["tokens_per_second"],
+        "ms_per_step_device_p50": gpu["device_ms_p50"],
+        "ms_per_step_host_inclusive": gpu["host_inclusive_ms_per_step"],
+        "steps": gpu["steps"],
+        "timing": "HIP events around each graph replay; host-inclusive = pipelined "
+                  "launch/collect loop wall time per step",
+    }
+    if with_cpu:
+        result["cpu_baseline"] = decode_step_cpu_baseline(weights, active[:4], cpu_seconds)
+    return result
+
+
+def decode_step_cpu_baseline(weights, contexts: list[int], seconds: float) -> dict:
+    """The oracle's fp32 incremental decode step (oracle/model.py) on the host
+    cores: 4 rows at their contexts, caches filled with random K/V."""
+
+    from oracle.model import decode_step_reference
+    from tensorforge_amd.decode import DecoderWeights, LayerWeights
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    f32 = lambda t: t.detach().float().cpu()  # noqa: E731
+    cpu = DecoderWeights(
+        config=weights.config, embedding=f32(weights.embedding),
+        layers=[LayerWeights(*(f32(getattr(layer, name)) for name in
+                               ("input_norm", "qkv", "o_proj", "post_norm", "gate_up", "down")))
+                for layer in weights.layers],
+        final_norm=f32(weights.final_norm), lm_head=f32(weights.lm_head),
+        rope_cos=f32(weights.rope_cos), rope_sin=f32(weights.rope_sin))
+    config = weights.config
+    batch, capacity = len(contexts), max(contexts) + 64
+    generator = torch.Generator().manual_seed(0)
+    keys = [torch.randn(batch, capacity, config.num_key_value_heads, config.head_dim,
+                        generator=generator) for _ in cpu.layers]
+    values = [torch.randn_like(k) for k in keys]
+    positions = torch.tensor(contexts)
+    tokens = torch.randint(0, config.vocab_size, (batch,), generator=generator)
+    decode_step_reference(cpu, keys, values, tokens, positions)  # warmup
+    samples = []
+    started = time.perf_counter()
+    while len(samples) < 3 or (time.perf_counter() - started < seconds and len(samples) < 60):
+        positions = positions + 1
+        t0 = time.perf_counter_ns()
+        decode_step_reference(cpu, keys, values, tokens, positions)
+        samples.append((time.perf_counter_ns() - t0) / 1e9)
+    samples.sort()
+    p50 = samples[len(samples) // 2]
+    return {
+        "value": round(batch / p50, 2),
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (
+            f"oracle decode_step_reference (fp32 torch {torch.__version__}), 22 layers, "
+            f"{batch} of the 64 rows (contexts {contexts}), p50 of {len(samples)} steps = "
+            f"{p50 * 1e3:.1f} ms; {platform.processor() or platform.machine()}"
         ),
     }
 
@@ -332,6 +420,8 @@ def main() -> int:
     if not args.no_cpu_baseline:
         active = [row for row, ctx in enumerate(lengths) if ctx > 0]
         result["cpu_baseline"] = cpu_baseline(case, active, args.cpu_seconds)
+    if not args.no_decode_step:
+        result["decode_step"] = decode_step(lengths, args.cpu_seconds, not args.no_cpu_baseline)
     print(json.dumps(result))
     return 0
 

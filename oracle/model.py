@@ -12,7 +12,9 @@ Pinning (tests/test_oracle_model.py): RoPE against its closed forms
 (identity at position 0, norm preservation, dot products depending only on
 the position difference, a hand-rotated pair); the last position's
 attention against paged_gqa_decode_reference over the same keys and values;
-the whole block against a pure-Python brute-force block on a tiny model.
+the whole block against a pure-Python brute-force block on a tiny model;
+the incremental decode step (decode_step_reference, the CPU baseline of the
+decode-step benchmark) against decoder_forward, token by token.
 """
 
 from __future__ import annotations
@@ -74,3 +76,48 @@ def decoder_forward(weights, tokens: Tensor) -> Tensor:
         x = x + (torch.nn.functional.silu(gate) * up) @ f32(layer.down).T
     h = rms_norm_reference(x, f32(weights.final_norm), config.rms_norm_eps)
     return h @ f32(weights.lm_head).T
+
+
+def decode_step_reference(weights, keys: list[Tensor], values: list[Tensor], tokens: Tensor,
+                          positions: Tensor) -> Tensor:
+    """One incremental decode step on the CPU in fp32 (the reference's eager
+    decode path, runtime/paged_decode.py, with dense per-row caches instead of
+    pages): logits [B, vocab] for `tokens` [B] at `positions` [B].
+
+    ``keys[layer]`` / ``values[layer]`` are fp32 [B, capacity, Hkv, D]
+    buffers; row b's first positions[b] slots hold its earlier tokens, and
+    the step writes the new token's k/v at slot positions[b] before
+    attending over slots 0..positions[b].  Weights are read as given (call
+    with fp32 CPU copies).
+    """
+
+    config = weights.config
+    hq, hkv, d = config.num_attention_heads, config.num_key_value_heads, config.head_dim
+    group = hq // hkv
+    batch = tokens.shape[0]
+    x = weights.embedding[tokens]
+    cos, sin = rope_tables(d, config.rope_theta, positions)
+    rows = torch.arange(batch)
+    for index, layer in enumerate(weights.layers):
+        h = rms_norm_reference(x, layer.input_norm, config.rms_norm_eps)
+        qkv = h @ layer.qkv.T
+        q = apply_rope(qkv[:, : hq * d].view(batch, hq, d), cos[:, None], sin[:, None])
+        k = apply_rope(qkv[:, hq * d: (hq + hkv) * d].view(batch, hkv, d), cos[:, None],
+                       sin[:, None])
+        keys[index][rows, positions] = k
+        values[index][rows, positions] = qkv[:, (hq + hkv) * d:].view(batch, hkv, d)
+        context = torch.empty(batch, hq, d)
+        for b in range(batch):
+            n = int(positions[b]) + 1
+            kk = keys[index][b, :n].repeat_interleave(group, dim=1).transpose(0, 1)  # [hq, n, d]
+            vv = values[index][b, :n].repeat_interleave(group, dim=1).transpose(0, 1)
+            scores = (kk @ q[b][:, :, None])[..., 0] * d ** -0.5                     # [hq, n]
+            context[b] = (torch.softmax(scores, dim=-1)[:, None, :] @ vv)[:, 0]
+        x = x + context.view(batch, hq * d) @ layer.o_proj.T
+        h = rms_norm_reference(x, layer.post_norm, config.rms_norm_eps)
+        gate = h @ layer.gate.T
+        up = h @ layer.up.T
+        x = x + (torch.nn.functional.silu(gate) * up) @ layer.down.T
+    h = rms_norm_reference(x, weights.final_norm, config.rms_norm_eps)
+    logits = h @ weights.lm_head.T
+    return logits

@@ -149,9 +149,68 @@ def config3(device: torch.device, calls: int) -> None:
            record=selected_attention_autotune_config())
 
 
+def measure_decode_step(weights: DecoderWeights, batch: int, context: int, *,
+                        steps: int = 64, seed: int = 0,
+                        prompt_lengths: list[int] | None = None) -> dict:
+    """One graph-captured decode step of ``weights`` at ``batch`` requests in
+    the context bucket ``context`` (prompts of about context - 40 tokens, or
+    ``prompt_lengths``, prefilled first): device p50/p95 per step from HIP
+    events and the host-inclusive time per step of the pipelined
+    launch/collect loop."""
+
+    import time
+
+    config = weights.config
+    device = weights.embedding.device
+    dtype = weights.embedding.dtype
+    generator = torch.Generator().manual_seed(seed)
+    if prompt_lengths is None:
+        prompt_lengths = [context - steps // 2 - 8 if context > steps else context // 2] * batch
+    if len(prompt_lengths) != batch or max(prompt_lengths) >= context:
+        raise ValueError("one prompt length per request, each below the context bucket")
+    prompt_length = max(prompt_lengths)
+    cache = PagedKVCache(PagedKVCacheConfig(
+        num_layers=config.num_hidden_layers, num_blocks=batch * (context // 16 + 2),
+        block_size=16, num_kv_heads=config.num_key_value_heads,
+        head_dim=config.head_dim, max_sequences=batch, max_sequence_length=context,
+        dtype=dtype, device=device))
+    executor = BucketedDecodeExecutor(weights, cache, batch_buckets=(batch,),
+                                      context_buckets=(context,))
+    rids = [f"s{i}" for i in range(batch)]
+    for rid in rids:
+        executor.create_request(rid)
+    prompts = {rid: torch.randint(0, config.vocab_size, (n,), generator=generator).tolist()
+               for rid, n in zip(rids, prompt_lengths)}
+    tokens = executor.prefill_prompts(prompts)
+    budget = context - prompt_length
+    warm = min(4, budget // 4)
+    timed = min(steps, budget - warm - 1)
+    pending = executor.launch(rids, tokens)
+    for _ in range(warm - 1):
+        ticket = executor.launch(rids)
+        executor.collect(pending)
+        pending = ticket
+    executor.step_records.clear()
+    begin = time.perf_counter()
+    for _ in range(timed):
+        ticket = executor.launch(rids)
+        executor.collect(pending)
+        pending = ticket
+    executor.collect(pending)
+    host_ms = (time.perf_counter() - begin) * 1e3 / timed
+    times = sorted(r.device_ms for r in executor.step_records[1:])
+    p50 = times[len(times) // 2]
+    return {
+        "steps": timed, "prompt_tokens": sum(prompt_lengths),
+        "device_ms_p50": round(p50, 4),
+        "device_ms_p95": round(times[int(0.95 * (len(times) - 1))], 4),
+        "host_inclusive_ms_per_step": round(host_ms, 4),
+        "tokens_per_second": round(batch / (max(host_ms, p50) / 1e3), 1),
+    }
+
+
 def decode_steps(device: torch.device, model: str = "cfg1", steps: int = 64) -> None:
     import dataclasses
-    import time
 
     if model == "cfg1":
         config = dataclasses.replace(small_config(), max_position_embeddings=4096)
@@ -160,47 +219,10 @@ def decode_steps(device: torch.device, model: str = "cfg1", steps: int = 64) -> 
         config = tinyllama_config()
         dtype, grid = torch.bfloat16, [(1024, b) for b in (1, 8, 64)]
     weights = DecoderWeights.random(config, seed=0, dtype=dtype, device=device)
-    generator = torch.Generator().manual_seed(0)
     for context, batch in grid:
-        prompt_length = context - steps // 2 - 8 if context > steps else context // 2
-        cache = PagedKVCache(PagedKVCacheConfig(
-            num_layers=config.num_hidden_layers, num_blocks=batch * (context // 16 + 2),
-            block_size=16, num_kv_heads=config.num_key_value_heads,
-            head_dim=config.head_dim, max_sequences=batch, max_sequence_length=context,
-            dtype=dtype, device=device))
-        executor = BucketedDecodeExecutor(weights, cache, batch_buckets=(batch,),
-                                          context_buckets=(context,))
-        rids = [f"s{i}" for i in range(batch)]
-        for rid in rids:
-            executor.create_request(rid)
-        prompts = {rid: torch.randint(0, config.vocab_size, (prompt_length,),
-                                      generator=generator).tolist() for rid in rids}
-        tokens = executor.prefill_prompts(prompts)
-        budget = context - prompt_length
-        warm = min(4, budget // 4)
-        timed = min(steps, budget - warm - 1)
-        pending = executor.launch(rids, tokens)
-        for _ in range(warm - 1):
-            ticket = executor.launch(rids)
-            executor.collect(pending)
-            pending = ticket
-        executor.step_records.clear()
-        begin = time.perf_counter()
-        for _ in range(timed):
-            ticket = executor.launch(rids)
-            executor.collect(pending)
-            pending = ticket
-        executor.collect(pending)
-        host_ms = (time.perf_counter() - begin) * 1e3 / timed
-        times = sorted(r.device_ms for r in executor.step_records[1:])
-        p50 = times[len(times) // 2]
-        print(json.dumps({
-            "case": f"decode_step {model}-model b{batch}-c{context}", "steps": timed,
-            "device_ms_p50": round(p50, 4),
-            "device_ms_p95": round(times[int(0.95 * (len(times) - 1))], 4),
-            "host_inclusive_ms_per_step": round(host_ms, 4),
-            "tokens_per_second": round(batch / (max(host_ms, p50) / 1e3), 1),
-        }), flush=True)
+        result = measure_decode_step(weights, batch, context, steps=steps)
+        print(json.dumps({"case": f"decode_step {model}-model b{batch}-c{context}", **result}),
+              flush=True)
 
 
 def main() -> int:

@@ -7,7 +7,13 @@ import math
 import pytest
 import torch
 
-from oracle.model import apply_rope, decoder_forward, rope_tables, rotate_half
+from oracle.model import (
+    apply_rope,
+    decode_step_reference,
+    decoder_forward,
+    rope_tables,
+    rotate_half,
+)
 from oracle.reference import (
     paged_gqa_decode_reference,
     rms_norm_reference,
@@ -189,3 +195,28 @@ def test_rope_kv_append_pins_reject_planted_mistakes() -> None:
     for mutant in (negated_sin, position_off_by_one, key_not_rotated):
         with pytest.raises(AssertionError):
             pin_rope_kv_append(mutant)
+
+
+def test_incremental_decode_step_equals_the_full_prefix_forward() -> None:
+    """decode_step_reference fed one token at a time (two rows of different
+    lengths) reproduces decoder_forward's logits at every position."""
+
+    config = tiny_config()
+    weights = DecoderWeights.random(config, seed=7, dtype=torch.float32, device="cpu")
+    for layer in weights.layers:
+        layer.input_norm.uniform_(0.5, 1.5)
+    sequences = [[3, 17, 42, 0, 9, 33, 8], [5, 5, 1, 49]]
+    capacity = 8
+    keys = [torch.zeros(2, capacity, config.num_key_value_heads, config.head_dim)
+            for _ in weights.layers]
+    values = [torch.zeros_like(k) for k in keys]
+    expected = [decoder_forward(weights, torch.tensor(s)) for s in sequences]
+    for step in range(len(sequences[0])):
+        rows = [b for b, s in enumerate(sequences) if step < len(s)]
+        # Rows that have finished keep decoding a pad token at a later slot.
+        tokens = torch.tensor([sequences[b][step] if step < len(sequences[b]) else 0
+                               for b in range(2)])
+        positions = torch.tensor([step, min(step, capacity - 1)])
+        logits = decode_step_reference(weights, keys, values, tokens, positions)
+        for b in rows:
+            torch.testing.assert_close(logits[b], expected[b][step], rtol=1e-4, atol=1e-5)
