@@ -28,6 +28,9 @@
  *   tf_rms_norm              tensorforge/kernels/triton_ops.py:179-205
  *   tf_residual_rms_norm     tensorforge/kernels/triton_ops.py:208-243
  *   tf_swiglu                tensorforge/kernels/triton_ops.py:246-260
+ *   tf_linear_rows           the nn.Linear projections of the decode step
+ *                            (tensorforge/model/layers.py:88-95, 144-146;
+ *                            runtime/decode_bucket.py:441-447, 470, 500-505)
  */
 #ifndef TENSORFORGE_AMD_H_
 #define TENSORFORGE_AMD_H_
@@ -260,6 +263,19 @@ int32_t tf_swiglu(const void *gate, const void *up, void *output,
 int32_t tf_swiglu_rows(const void *gate_up, int64_t gate_up_row_stride,
                        void *output, int64_t output_row_stride, int64_t rows,
                        int32_t columns, int32_t dtype, void *stream);
+
+/*
+ * Decode-shaped linear layer y[m, n] = x[m, k] . weight[n, k]^T (no bias),
+ * fp16 or bf16, fp32 accumulation, one rounding; m <= 64, k a multiple of
+ * 32, x and weight rows 16-byte aligned (strides in elements).  K is split
+ * over waves_per_tile wavefronts per 16-column tile (0 = chosen from the
+ * shape).  Replaces the torch GEMM of the reference's nn.Linear projections
+ * at decode batch sizes (model/layers.py:88-95, 144-146).
+ */
+int32_t tf_linear_rows(const void *x, int64_t x_row_stride, const void *weight,
+                       int64_t weight_row_stride, void *y, int64_t y_row_stride,
+                       int32_t m, int32_t n, int32_t k, int32_t waves_per_tile,
+                       int32_t dtype, void *stream);
 
 #ifdef __cplusplus
 }

@@ -12,8 +12,9 @@ sequences runs as ONE captured HIP graph.  Per layer:
 * ``residual_rms_norm`` of (attention output, residual);
 * one fused gate|up projection, ``swiglu_gate_up``, the down projection.
 
-The gfx950 kernels of this package do the norm, cache and attention work;
-the GEMMs are library GEMMs (torch -> hipBLASLt).  Every per-step input
+The gfx950 kernels of this package do the norm, cache and attention work,
+and the small projections at up to 16 rows; the other GEMMs are library
+GEMMs (torch -> hipBLASLt).  Every per-step input
 lives in one device "control" slab, filled from one pinned host slab with
 one asynchronous copy per step.  So the graph's addresses never change,
 and a step needs no host synchronisation beyond reading back the sampled
@@ -40,6 +41,8 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from tensorforge_amd.cache import AppendReservation, PagedKVCache
 from tensorforge_amd.kernels import (
     PagedAttentionWorkspace,
+    linear_rows,
+    linear_rows_supported,
     paged_gqa_decode_attention,
     residual_rms_norm,
     rms_norm,
@@ -141,6 +144,22 @@ class DecoderWeights:
                    final_norm=ones(h), lm_head=normal(config.vocab_size, h),
                    rope_cos=angles.cos().to(dtype).to(device),
                    rope_sin=angles.sin().to(dtype).to(device))
+
+
+def _project(x: Tensor, weight: Tensor, output: Tensor | None = None) -> Tensor:
+    """x @ weight.T for a decode step.  Up to 16 rows, the K-split MFMA kernel
+    (linear_rows) streams small weights (<= 8M elements: the q/k/v and o
+    projections of TinyLlama) and the LM head faster than the library GEMM,
+    which launches too few workgroups for them; otherwise hipBLASLt (measured
+    on MI355X at the TinyLlama shapes)."""
+
+    rows_kernel = (x.shape[0] <= 16 and linear_rows_supported(x, weight)
+                   and (weight.numel() <= 8 * 1024 * 1024 or weight.shape[0] >= 16384))
+    if rows_kernel:
+        return linear_rows(x, weight, output=output)
+    if output is None:
+        return F.linear(x, weight)
+    return torch.matmul(x, weight.t(), out=output)
 
 
 class DecodeGraphBucket:
@@ -334,7 +353,7 @@ class DecodeGraphBucket:
             residual = x
             h = rms_norm(x, self.weights.layers[0].input_norm, eps, output=self.norm_output)
             for index, layer in enumerate(self.weights.layers):
-                qkv = F.linear(h, layer.qkv)
+                qkv = _project(h, layer.qkv)
                 key_cache = self.cache.key_cache[index]
                 value_cache = self.cache.value_cache[index]
                 # RoPE on q and k, k and v into their pages: one launch.
@@ -347,18 +366,18 @@ class DecodeGraphBucket:
                     q, key_cache, value_cache, self.block_tables, self.context_lengths,
                     scale=d ** -0.5, max_context_length=self.context_capacity,
                     output=self.attention_output, workspace=self.workspace)
-                attn = F.linear(self.attention_output.view(b, hq * d), layer.o_proj)
+                attn = _project(self.attention_output.view(b, hq * d), layer.o_proj)
                 residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps,
                                                 residual_output=torch.empty_like(attn),
                                                 norm_output=self.norm_output)
-                act = swiglu_gate_up(F.linear(h, layer.gate_up), output=self.swiglu_output)
-                mlp = F.linear(act, layer.down)
+                act = swiglu_gate_up(_project(h, layer.gate_up), output=self.swiglu_output)
+                mlp = _project(act, layer.down)
                 next_norm = (self.weights.layers[index + 1].input_norm
                              if index + 1 < len(self.weights.layers) else self.weights.final_norm)
                 residual, h = residual_rms_norm(mlp, residual, next_norm, eps,
                                                 residual_output=torch.empty_like(mlp),
                                                 norm_output=self.norm_output)
-            torch.matmul(h, self.weights.lm_head.t(), out=self.logits)
+            _project(h, self.weights.lm_head, output=self.logits)
             torch.argmax(self.logits, dim=-1, out=self.next_tokens)
         finally:
             set_attention_split_size(previous)
