@@ -4,8 +4,10 @@ Workload: paged GQA decode attention at TinyLlama
 geometry -- 64 rows with context U[128, 2048] plus 8 zero-length rows,
 32 query / 4 KV heads, head_dim 64, 16-token pages on a seeded permutation,
 bf16, N(0,1) inputs, scale 1/8.  A step is one attention call over one
-batch: the split stage (one wavefront per (row, kv head, split)) and the
-log-sum-exp merge launch, as the Python entry point issues them.  To keep
+batch as the Python entry point plans it: at this batch one pass, one
+workgroup per (row, kv head) whose three wavefronts share the row and
+combine in LDS (no partials, no merge launch); ``--split-size`` forces the
+split-KV form (split stage + log-sum-exp merge launch).  To keep
 the 256 MB Infinity Cache from serving the K/V pages, steps rotate over
 several independent copies of the page pool (``--pools``), so every step
 streams its pages from HBM.
@@ -15,8 +17,9 @@ Prints ONE JSON line.  ``value`` is algorithmic GB/s of the whole call
 output of the active rows) over the timed steps.  The K timed steps run as
 one HIP-graph replay bracketed by HIP events on the launch stream (a ctypes
 call costs the host longer than the kernel takes, so eager steps would
-time the host).  ``roofline`` reports the dominant kernel, the split stage,
-timed the same way from a graph of K split-stage launches alone.
+time the host).  ``roofline`` reports the dominant kernel: in one pass the
+whole call; in split-KV form the split stage, timed the same way from a
+graph of K split-stage launches alone.
 ``cpu_baseline`` is the CPU oracle on the same rows, on this host's cores.
 
 ``decode_step`` is the metric's "decode tokens/s" part: a whole
@@ -30,7 +33,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import platform
 import sys
@@ -54,8 +56,8 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--pools", type=int, default=6, help="rotated K/V page pools")
     parser.add_argument("--split-size", type=int, default=0,
-                        help="tokens per split-KV partition (multiple of 32); 0: the "
-                             "per-call choice of the Python entry point")
+                        help="force split-KV with this partition size (multiple of 32); "
+                             "0: the Python entry point's plan (one pass at this batch)")
     parser.add_argument("--merge", choices=("fused", "kernel"), default="kernel",
                         help="separate merge launch (the product path) or the in-kernel "
                              "merge enabled by arrival counters")
@@ -218,7 +220,7 @@ def main() -> int:
 
     from tensorforge_amd import _native
     from tensorforge_amd.kernels import PagedAttentionWorkspace, set_attention_split_size
-    from tensorforge_amd.kernels.attention import attention_split_size_for
+    from tensorforge_amd.kernels.attention import attention_plan, attention_split_size_for
     from tensorforge_amd.workloads import decode_attention_bytes, tinyllama_decode_case
 
     device = torch.device("cuda", 0)
@@ -233,9 +235,16 @@ def main() -> int:
     num_blocks, block_size, kv_heads, _ = gpu.key_cache.shape
     table_width = gpu.block_tables.shape[1]
     max_context = 2048
-    split_size = args.split_size or attention_split_size_for(max_context, batch, kv_heads)
-    set_attention_split_size(split_size)
-    num_splits = math.ceil(max_context / split_size)
+    fused = args.merge == "fused"
+    if args.split_size or fused:  # split-KV forced: the alternative paths
+        split_size = args.split_size or attention_split_size_for(max_context, batch, kv_heads)
+        set_attention_split_size(split_size)
+        path = "split_kv"
+    else:
+        path = "auto"
+    plan = attention_plan(max_context, batch, kv_heads, table_width * block_size, path)
+    split_size, num_splits, flags = plan.split_size, plan.num_splits, plan.flags
+    one_pass = plan.one_pass
     workspace = PagedAttentionWorkspace.allocate(
         batch_capacity=batch, query_heads=query_heads, head_dim=head_dim,
         max_context_length=num_splits * 256, device=device,
@@ -248,12 +257,11 @@ def main() -> int:
     variant = lib.tf_paged_gqa_decode_variant(dtype, head_dim, query_heads // kv_heads, block_size, 0)
 
     counters = workspace.split_counters
-    fused = args.merge == "fused"
 
     def attention_call(pool: int, handle: int) -> None:
-        # tf_paged_gqa_decode: without arrival counters (the product path)
-        # the split kernel is followed by the merge kernel; with them one
-        # launch whose last wavefront per (row, kv head) merges.
+        # tf_paged_gqa_decode as the plan launches it: one pass (one launch);
+        # split-KV without arrival counters (split kernel + merge kernel); or
+        # with them one launch whose last wavefront per (row, kv head) merges.
         key_cache, value_cache = pools[pool]
         _native.check(lib.tf_paged_gqa_decode(
             gpu.query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
@@ -261,7 +269,7 @@ def main() -> int:
             workspace.partial_max.data_ptr(), workspace.partial_sum.data_ptr(),
             workspace.partial_accumulator.data_ptr(), counters.data_ptr() if fused else None,
             capacity, head_bucket, batch, query_heads, kv_heads, head_dim, num_blocks,
-            block_size, table_width, split_size, num_splits, case.scale, dtype, 0, handle),
+            block_size, table_width, split_size, num_splits, case.scale, dtype, flags, handle),
             "attention")
 
     def split_stage(pool: int, handle: int) -> None:
@@ -292,6 +300,7 @@ def main() -> int:
     check = paged_gqa_decode_attention(
         gpu.query, gpu.key_cache, gpu.value_cache, gpu.block_tables, gpu.context_lengths,
         scale=case.scale, max_context_length=max_context, workspace=workspace,
+        attention_path=path,
     )
     torch.cuda.synchronize()
     if not fused:
@@ -303,7 +312,7 @@ def main() -> int:
         return 1
 
     def one_step(step: int, handle: int) -> None:
-        if fused:
+        if fused or one_pass:
             attention_call(step % args.pools, handle)
         else:
             split_stage(step % args.pools, handle)
@@ -336,12 +345,12 @@ def main() -> int:
     wall = time.perf_counter() - wall0
     ms_per_step = replay_begin.elapsed_time(replay_end) / args.steps
 
-    # Kernel duration for the roofline.  With the in-kernel merge a step is
-    # exactly one launch, so the graph replay's time per step is the
-    # kernel's duration (plus the graph's inter-launch gap).  With the
+    # Kernel duration for the roofline.  In one pass or with the in-kernel
+    # merge a step is exactly one launch, so the graph replay's time per step
+    # is the kernel's duration (plus the graph's inter-launch gap).  With the
     # separate merge, K split-stage launches alone are captured in a second
     # graph and timed the same way.
-    if fused:
+    if fused or one_pass:
         split_ms = ms_per_step
         kernel_timing = "HIP events around the timed graph replay; one launch per step"
     else:
@@ -367,7 +376,7 @@ def main() -> int:
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     achieved = nbytes / (split_ms * 1e-3) / 1e9
     traffic = None
-    if TRAFFIC_FILE.exists():
+    if TRAFFIC_FILE.exists() and one_pass:  # the profile covers the default one-pass plan
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
 
     result = {
@@ -394,10 +403,13 @@ def main() -> int:
             "context": "U[128,2048], seed 0",
             "sum_context": sum(lengths),
             "kernel": "mfma" if variant == _native.TF_ATTENTION_MFMA else "generic",
+            "plan": "one_pass" if one_pass else "split_kv",
             "split_size": split_size,
             "num_splits": num_splits,
+            "waves_per_kv_head": plan.waves_per_head,
             "kv_pools_rotated": args.pools,
-            "merge": "in-kernel (arrival counters)" if fused else "separate merge launch",
+            "merge": ("none (one pass)" if one_pass
+                      else "in-kernel (arrival counters)" if fused else "separate merge launch"),
             "algorithmic_bytes_per_call": nbytes,
         },
         "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
@@ -409,8 +421,9 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "kernel": "paged_decode_mfma_kernel"
-            + (" (split stage with in-kernel merge)" if fused else " (split stage)"),
-            "merge_ms": None if fused else round(ms_per_step - split_ms, 6),
+            + (" (one pass, the whole call)" if one_pass
+               else " (split stage with in-kernel merge)" if fused else " (split stage)"),
+            "merge_ms": None if (fused or one_pass) else round(ms_per_step - split_ms, 6),
             "timing": kernel_timing,
             "kernel_ms": round(split_ms, 6),
         },

@@ -31,7 +31,11 @@ from tensorforge_amd.kernels import (
     set_attention_split_size,
     swiglu,
 )
-from tensorforge_amd.kernels.attention import attention_split_size, attention_split_size_for
+from tensorforge_amd.kernels.attention import (
+    attention_plan,
+    attention_split_size,
+    attention_split_size_for,
+)
 from tensorforge_amd.workloads import (
     decode_attention_bytes,
     kv_append_bytes,
@@ -230,6 +234,33 @@ def test_automatic_split_size() -> None:
             size = attention_split_size_for(context, batch, 8)
             assert size >= 256 and size % 32 == 0
             assert -(-context // size) <= max(16, -(-context // 256))
+
+
+def test_attention_plan() -> None:
+    """One pass for wide batches (cfg2: 72 rows x 4 kv heads at 2k, three
+    wavefronts per kv head) and whenever the context fits one partition;
+    split-KV for few workgroups at long contexts (the reference's own 1 x 8
+    case, cfg3) or when the caller fixed the partition size."""
+
+    cfg2 = attention_plan(2048, 72, 4, 2048)
+    assert (cfg2.one_pass, cfg2.num_splits, cfg2.waves_per_head) == (True, 1, 3)
+    assert cfg2.flags == (1 << 20) | (3 << 8)
+    short = attention_plan(200, 2, 4, 2048)
+    assert short.one_pass and short.waves_per_head == 1 and short.flags == 0
+    assert short.split_size == 2048  # the whole table in one partition
+    few = attention_plan(2048, 1, 4, 2048)
+    assert (few.one_pass, few.split_size, few.num_splits) == (False, 256, 8)
+    cfg3 = attention_plan(32768, 4, 8, 32768)
+    assert (cfg3.one_pass, cfg3.split_size, cfg3.num_splits) == (False, 2048, 16)
+    assert attention_plan(4096, 64, 4, 4096).waves_per_head == 6
+    assert attention_plan(32768, 64, 4, 32768).waves_per_head == 8
+    assert not attention_plan(2048, 72, 4, 2048, "split_kv").one_pass
+    previous = set_attention_split_size(512)
+    try:
+        fixed = attention_plan(2048, 72, 4, 2048)
+        assert (fixed.one_pass, fixed.split_size, fixed.num_splits) == (False, 512, 4)
+    finally:
+        set_attention_split_size(previous)
 
 
 def test_workspace_capacity_contract() -> None:

@@ -128,7 +128,9 @@ def test_long_context_with_few_heads_selects_split_kv_path(device):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_tinyllama_batch64_config(device, dtype):
-    """64 rows ctx U[128, 2048] + 8 zero-length rows."""
+    """64 rows ctx U[128, 2048] + 8 zero-length rows, one
+    pass with three wavefronts per kv head (the plan for a wide batch), and
+    the forced split-KV path."""
 
     case = tinyllama_decode_case(seed=0, dtype=dtype)
     gpu = case.to(device)
@@ -137,7 +139,43 @@ def test_tinyllama_batch64_config(device, dtype):
         scale=case.scale, max_context_length=2048,
     )
     assert selected_attention_launch()["kernel"] == "mfma"
+    assert selected_attention_autotune_config()["waves_per_head"] == 3
     _check_against_oracle(case, output.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, f"cfg2 {dtype}")
+    split = paged_gqa_decode_attention(
+        gpu.query, gpu.key_cache, gpu.value_cache, gpu.block_tables, gpu.context_lengths,
+        scale=case.scale, max_context_length=2048, attention_path="split_kv",
+    )
+    assert selected_attention_autotune_config()["split_size"] == 576
+    _check_against_oracle(case, split.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, f"cfg2 split {dtype}")
+
+
+@pytest.mark.parametrize("split_size", [0, 256])
+@pytest.mark.parametrize(("heads_per_wg", "waves_per_head"),
+                         [(1, 2), (1, 3), (1, 4), (1, 8), (2, 2), (2, 4), (4, 2)])
+def test_grid_kernel_multi_wave_workgroups(device, heads_per_wg, waves_per_head, split_size):
+    """Workgroups of several kv heads and several wavefronts per head (their
+    states combined in LDS), in one pass and with 256-token partitions, on
+    ragged rows (including one shorter than a chunk and an empty one)."""
+
+    lengths = [2048, 1, 700, 0, 1333, 31, 96, 2000]
+    case = make_decode_attention_case(
+        lengths, query_heads=32, kv_heads=4, head_dim=64, block_size=16, dtype=torch.bfloat16,
+        seed=heads_per_wg * 10 + waves_per_head,
+    )
+    gpu = case.to(device)
+    workspace = PagedAttentionWorkspace.allocate(
+        batch_capacity=len(lengths), query_heads=32, head_dim=64, max_context_length=2048,
+        device=device,
+    )
+    flags = ((heads_per_wg << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
+             | (waves_per_head << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT))
+    out = torch.full_like(gpu.query, float("nan"))
+    if split_size == 0:
+        _raw_decode(gpu, out, flags, gpu.block_tables.shape[1] * 16, 1, workspace)
+    else:
+        _raw_decode(gpu, out, flags, split_size, 2048 // split_size, workspace)
+    _check_against_oracle(case, out.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL,
+                          f"hpw {heads_per_wg} wph {waves_per_head} split {split_size}")
 
 
 def test_llama3_long_context_split_kv(device):
