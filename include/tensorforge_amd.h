@@ -72,12 +72,15 @@ enum tf_attention_variant {
  *   bits 8-15   grid kernel: wavefronts per kv head (heads x this <= 8);
  *               streaming kernel: wavefronts per compute unit
  *   bits 16-19  streaming kernel: tiles in flight per wavefront (2..4)
- *   bits 20-23  grid kernel: kv heads per workgroup (must divide kv_heads) */
+ *   bits 20-23  grid kernel: kv heads per workgroup (must divide kv_heads)
+ *   bits 24-30  grid kernel: tokens per wavefront / 64; a row then uses
+ *               ceil(its tokens / that) of the head's wavefronts (0: all) */
 #define TF_ATTENTION_FLAG_FORCE_GENERIC 1
 #define TF_ATTENTION_FLAG_STREAM 4
 #define TF_ATTENTION_WAVES_PER_CU_SHIFT 8
 #define TF_ATTENTION_DEPTH_SHIFT 16
 #define TF_ATTENTION_HEADS_PER_WG_SHIFT 20
+#define TF_ATTENTION_TOKENS_PER_WAVE_SHIFT 24
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char *tf_last_error(void);

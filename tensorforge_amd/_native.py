@@ -27,6 +27,7 @@ TF_ATTENTION_FLAG_STREAM = 4
 TF_ATTENTION_WAVES_PER_CU_SHIFT = 8
 TF_ATTENTION_DEPTH_SHIFT = 16
 TF_ATTENTION_HEADS_PER_WG_SHIFT = 20
+TF_ATTENTION_TOKENS_PER_WAVE_SHIFT = 24
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: TF_DTYPE_FLOAT32,

@@ -86,6 +86,7 @@ struct AttnParams {
   int64_t partial_rows;    // rows the partial buffers hold
   int32_t heads_per_wg;    // MFMA grid kernel: kv heads served by one workgroup
   int32_t waves_per_head;  // MFMA grid kernel: wavefronts sharing one kv head
+  int32_t tokens_per_wave; // MFMA grid kernel: > 0 uses ceil(tokens / this) of them per row
   float scale_log2;
 };
 
@@ -509,6 +510,15 @@ paged_decode_mfma_kernel(AttnParams p) {
     return;
   }
   const int32_t s1 = min(s0 + p.split_size, ctx);
+  // Wavefronts of the head that take chunks of this row: all WPH, or with a
+  // token budget per wavefront only as many as the row's length needs (the
+  // rest stay idle), so short rows do not load the memory system with
+  // near-empty streams while long rows still get WPH.
+  int32_t active = WPH;
+  if (p.tokens_per_wave > 0) {
+    active = (s1 - s0 + p.tokens_per_wave - 1) / p.tokens_per_wave;
+    active = active < 1 ? 1 : (active > WPH ? WPH : active);
+  }
 
   const uint32_t token_bytes = static_cast<uint32_t>(p.kv_heads) * D * sizeof(T);
   const unsigned char *kbytes = static_cast<const unsigned char *>(p.key_cache);
@@ -636,9 +646,10 @@ paged_decode_mfma_kernel(AttnParams p) {
     if (seg_first_tile != 0) page_win = load_window(seg_first_tile);
     const int32_t seg_s1 = min(seg_s0 + 16 * kSegmentTiles, s1);
     const int32_t seg_chunks = (seg_s1 - seg_s0 + kChunk - 1) / kChunk;
-    const int32_t mine = seg_chunks > sub ? (seg_chunks - sub + WPH - 1) / WPH : 0;
+    const int32_t mine =
+        sub < active && seg_chunks > sub ? (seg_chunks - sub + active - 1) / active : 0;
     if (mine == 0) continue;
-    auto chunk = [&](int32_t i) { return i < mine ? sub + i * WPH : seg_chunks; };
+    auto chunk = [&](int32_t i) { return i < mine ? sub + i * active : seg_chunks; };
     load_kv(seg_first_tile, seg_s0, seg_s1, chunk(0), ka, va, vala);
     for (int32_t i = 0; i < mine; i += 2) {
       load_kv(seg_first_tile, seg_s0, seg_s1, chunk(i + 1), kb, vb, valb);
@@ -673,7 +684,7 @@ paged_decode_mfma_kernel(AttnParams p) {
     }
     __syncthreads();
     if (sub == 0) {
-      for (int32_t s = 1; s < WPH; ++s) {
+      for (int32_t s = 1; s < active; ++s) {
         const int w = hl + s * HPW;
         const float mo = xm[w * 32 + l16];
         const float lo = xm[w * 32 + 16 + l16];
@@ -1621,6 +1632,7 @@ void mfma_geometry(AttnParams &p, int32_t flags) {
   if (want_wph > 0 && want_wph * hpw <= kMfmaWaves) wph = want_wph;
   p.heads_per_wg = hpw;
   p.waves_per_head = wph;
+  p.tokens_per_wave = ((flags >> TF_ATTENTION_TOKENS_PER_WAVE_SHIFT) & 0x7f) * 64;
 }
 
 template <typename T, int D>
@@ -1712,6 +1724,7 @@ int32_t make_params(AttnParams &p, const void *query, const void *key_cache,
   p.partial_rows = partial_capacity;
   p.heads_per_wg = 1;
   p.waves_per_head = 1;
+  p.tokens_per_wave = 0;
   p.scale_log2 = scale * kLog2e;
   return TF_SUCCESS;
 }

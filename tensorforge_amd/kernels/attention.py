@@ -154,10 +154,14 @@ class AttentionPlan:
 
     @property
     def flags(self) -> int:
+        """Several wavefronts per kv head, each row using one per 768 of its
+        tokens (so short rows leave the memory system to the long ones)."""
+
         if self.waves_per_head <= 1:
             return 0
         return ((1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
-                | (self.waves_per_head << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT))
+                | (self.waves_per_head << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
+                | ((ONE_PASS_TOKENS_PER_WAVE // 64) << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
 
 
 def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capacity: int,

@@ -76,7 +76,7 @@ def test_header_constants_match_the_python_binding() -> None:
     text = HEADER.read_text()
     for name in ("TF_ATTENTION_FLAG_FORCE_GENERIC", "TF_ATTENTION_FLAG_STREAM",
                  "TF_ATTENTION_WAVES_PER_CU_SHIFT", "TF_ATTENTION_DEPTH_SHIFT",
-                 "TF_ATTENTION_HEADS_PER_WG_SHIFT"):
+                 "TF_ATTENTION_HEADS_PER_WG_SHIFT", "TF_ATTENTION_TOKENS_PER_WAVE_SHIFT"):
         match = re.search(rf"#define {name} (\d+)", text)
         assert match and int(match.group(1)) == getattr(_native, name), name
     for name in ("TF_DTYPE_FLOAT32", "TF_DTYPE_FLOAT16", "TF_DTYPE_BFLOAT16",
@@ -244,7 +244,7 @@ def test_attention_plan() -> None:
 
     cfg2 = attention_plan(2048, 72, 4, 2048)
     assert (cfg2.one_pass, cfg2.num_splits, cfg2.waves_per_head) == (True, 1, 3)
-    assert cfg2.flags == (1 << 20) | (3 << 8)
+    assert cfg2.flags == (12 << 24) | (1 << 20) | (3 << 8)
     short = attention_plan(200, 2, 4, 2048)
     assert short.one_pass and short.waves_per_head == 1 and short.flags == 0
     assert short.split_size == 2048  # the whole table in one partition

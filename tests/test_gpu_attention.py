@@ -150,17 +150,20 @@ def test_tinyllama_batch64_config(device, dtype):
 
 
 @pytest.mark.parametrize("split_size", [0, 256])
-@pytest.mark.parametrize(("heads_per_wg", "waves_per_head"),
-                         [(1, 2), (1, 3), (1, 4), (1, 8), (2, 2), (2, 4), (4, 2)])
-def test_grid_kernel_multi_wave_workgroups(device, heads_per_wg, waves_per_head, split_size):
+@pytest.mark.parametrize(("heads_per_wg", "waves_per_head", "tokens_per_wave"),
+                         [(1, 2, 0), (1, 3, 0), (1, 4, 0), (1, 8, 0), (2, 2, 0), (2, 4, 0),
+                          (4, 2, 0), (1, 3, 768), (1, 8, 256), (2, 4, 64)])
+def test_grid_kernel_multi_wave_workgroups(device, heads_per_wg, waves_per_head,
+                                           tokens_per_wave, split_size):
     """Workgroups of several kv heads and several wavefronts per head (their
     states combined in LDS), in one pass and with 256-token partitions, on
-    ragged rows (including one shorter than a chunk and an empty one)."""
+    ragged rows (including one shorter than a chunk and an empty one); with
+    a token budget per wavefront, rows use only as many as they need."""
 
     lengths = [2048, 1, 700, 0, 1333, 31, 96, 2000]
     case = make_decode_attention_case(
         lengths, query_heads=32, kv_heads=4, head_dim=64, block_size=16, dtype=torch.bfloat16,
-        seed=heads_per_wg * 10 + waves_per_head,
+        seed=heads_per_wg * 10 + waves_per_head + tokens_per_wave,
     )
     gpu = case.to(device)
     workspace = PagedAttentionWorkspace.allocate(
@@ -168,14 +171,16 @@ def test_grid_kernel_multi_wave_workgroups(device, heads_per_wg, waves_per_head,
         device=device,
     )
     flags = ((heads_per_wg << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
-             | (waves_per_head << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT))
+             | (waves_per_head << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
+             | ((tokens_per_wave // 64) << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
     out = torch.full_like(gpu.query, float("nan"))
     if split_size == 0:
         _raw_decode(gpu, out, flags, gpu.block_tables.shape[1] * 16, 1, workspace)
     else:
         _raw_decode(gpu, out, flags, split_size, 2048 // split_size, workspace)
     _check_against_oracle(case, out.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL,
-                          f"hpw {heads_per_wg} wph {waves_per_head} split {split_size}")
+                          f"hpw {heads_per_wg} wph {waves_per_head} tpw {tokens_per_wave} "
+                          f"split {split_size}")
 
 
 def test_llama3_long_context_split_kv(device):
