@@ -46,7 +46,10 @@ struct Mma16<_Float16> {
   }
 };
 
-constexpr int kUnroll = 4;  // k-steps (of 32) whose loads are issued together
+// k-steps (of 32) whose loads are issued together: 16 operand loads per
+// batch (kUnroll * (MT + 1) <= 20), so they all stay in registers.
+template <int MT>
+constexpr int unroll_for() { return MT <= 1 ? 8 : (MT == 2 ? 4 : (MT == 3 ? 4 : 4)); }
 
 // blockIdx.x = 16-column tile; wavefront w sums k in [w * kpw, (w + 1) * kpw).
 template <typename T, int MT>
@@ -56,6 +59,7 @@ linear_rows_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restric
                    int32_t k, int32_t k_per_wave) {
   using M = Mma16<T>;
   using vec8 = typename M::vec8;
+  constexpr int kUnroll = unroll_for<MT>();
   extern __shared__ __attribute__((aligned(16))) float partial[];  // [waves][MT * 4][64]
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -88,6 +92,9 @@ linear_rows_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restric
       for (int mt = 0; mt < MT; ++mt)
         xa[u][mt] = *reinterpret_cast<const vec8 *>(xrow[mt] + kk + 32 * u);
     }
+    // Keep the scheduler from interleaving the batch's loads with its
+    // MFMAs: it would otherwise trade loads in flight for registers.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
