@@ -250,6 +250,8 @@ def test_attention_plan() -> None:
     assert short.split_size == 2048  # the whole table in one partition
     few = attention_plan(2048, 1, 4, 2048)
     assert (few.one_pass, few.split_size, few.num_splits) == (False, 256, 8)
+    assert attention_plan(2048, 48, 4, 2048).one_pass      # 192 workgroups
+    assert not attention_plan(2048, 32, 4, 2048).one_pass  # 128 workgroups
     cfg3 = attention_plan(32768, 4, 8, 32768)
     assert (cfg3.one_pass, cfg3.split_size, cfg3.num_splits) == (False, 2048, 16)
     assert attention_plan(4096, 64, 4, 4096).waves_per_head == 6
