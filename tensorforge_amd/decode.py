@@ -633,7 +633,15 @@ class BucketedDecodeExecutor:
             raise
         begin, end, copied = self._events[slot]
         begin.record()
-        bucket.execute()
+        try:
+            bucket.execute()
+        except Exception:
+            # Nothing of this step is committed; its lanes' previous samples
+            # are no longer trusted as inputs either.
+            for reservation in reservations.values():
+                self.cache.rollback(reservation)
+            self._last_lanes = {}
+            raise
         end.record()
         lanes = len(request_ids)
         self._readback[slot][:lanes].copy_(self.token_state[:lanes], non_blocking=True)
