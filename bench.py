@@ -221,7 +221,11 @@ def main() -> int:
     from tensorforge_amd import _native
     from tensorforge_amd.kernels import PagedAttentionWorkspace, set_attention_split_size
     from tensorforge_amd.kernels.attention import attention_plan, attention_split_size_for
-    from tensorforge_amd.workloads import decode_attention_bytes, tinyllama_decode_case
+    from tensorforge_amd.workloads import (
+        decode_attention_bytes,
+        decode_attention_flops,
+        tinyllama_decode_case,
+    )
 
     device = torch.device("cuda", 0)
     lib = _native.library()
@@ -411,6 +415,7 @@ def main() -> int:
             "merge": ("none (one pass)" if one_pass
                       else "in-kernel (arrival counters)" if fused else "separate merge launch"),
             "algorithmic_bytes_per_call": nbytes,
+            "algorithmic_flops_per_call": decode_attention_flops(lengths, query_heads, head_dim),
         },
         "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
         "roofline": {

@@ -28,7 +28,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import math
 from typing import Callable
 
 import torch
