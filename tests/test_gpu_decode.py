@@ -199,3 +199,37 @@ def test_padded_lanes_write_nothing_and_addresses_are_stable(device):
         err = float((logits[rid].float().cpu() - expected).abs().max())
         assert err <= 2e-2 * float(expected.abs().max()), (rid, err)
         assert cache.sequence_layout(rid).context_length == len(prompt) + len(outputs[rid])
+
+
+def test_head_dim_128_and_group_4_decoder(device):
+    """The executor at another geometry: head_dim 128, 4 query heads per kv
+    head (a Llama-3-style layout), bf16, two layers; greedy tokens follow the
+    oracle with the bf16 margin."""
+
+    from tensorforge_amd.decode import DecoderConfig
+
+    config = DecoderConfig(vocab_size=512, hidden_size=512, intermediate_size=1024,
+                           num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=1,
+                           max_position_embeddings=512)
+    assert config.head_dim == 128
+    weights = DecoderWeights.random(config, seed=4, dtype=torch.bfloat16, device=device)
+    order = list(range(64))
+    random.Random(3).shuffle(order)
+    cache = PagedKVCache(
+        PagedKVCacheConfig(num_layers=2, num_blocks=64, block_size=16, num_kv_heads=1,
+                           head_dim=128, max_sequences=4, max_sequence_length=512,
+                           dtype=torch.bfloat16, device=device),
+        page_order=order)
+    executor = BucketedDecodeExecutor(weights, cache, batch_buckets=(4,), context_buckets=(512,))
+    rng = random.Random(5)
+    prompts = {f"p{i}": [rng.randrange(512) for _ in range(n)] for i, n in enumerate((3, 50, 129))}
+    outputs = greedy_decode(executor, prompts, steps=10)
+    flips = 0
+    for rid, prompt in prompts.items():
+        logits = decoder_forward(weights, torch.tensor(prompt + outputs[rid][:-1]))
+        for step, token in enumerate(outputs[rid]):
+            row = logits[len(prompt) - 1 + step]
+            margin = float(row.max() - row[token])
+            assert margin <= 2e-2 * float(row.abs().max()), (rid, step, margin)
+            flips += int(margin > 0)
+    assert flips <= 2
