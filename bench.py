@@ -66,6 +66,9 @@ def parse_args() -> argparse.Namespace:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-decode-step", action="store_true",
                         help="skip the 22-layer decode-step tokens/s part of the metric")
+    parser.add_argument("--kernels", action="store_true",
+                        help="instead of the metric: config 3 and 4 kernels (graph-timed) with "
+                             "the CPU oracle timed beside each case; one JSON line")
     parser.add_argument("--copy-calibration-mib", type=int, default=0,
                         help="only run a plain device copy of this many MiB (counter calibration)")
     return parser.parse_args()
@@ -201,6 +204,76 @@ def decode_step_cpu_baseline(weights, contexts: list[int], seconds: float) -> di
     }
 
 
+def _cpu_p50(fn, seconds: float, reps: int = 3) -> float:
+    fn()  # warmup
+    samples = []
+    started = time.perf_counter()
+    while len(samples) < reps or (time.perf_counter() - started < seconds and len(samples) < 50):
+        t0 = time.perf_counter_ns()
+        fn()
+        samples.append((time.perf_counter_ns() - t0) / 1e9)
+    samples.sort()
+    return samples[len(samples) // 2]
+
+
+def kernels_line(calls: int, seconds_per_case: float) -> dict:
+    """Config 4 (fused ops and the KV append) and config 3 (long-context
+    attention) through the public entry points, graph-timed, each beside the
+    CPU oracle of the same op on the same shape (fp32 torch / numpy on the
+    host cores)."""
+
+    from oracle.reference import (
+        paged_gqa_decode_reference,
+        paged_kv_write_slots_reference,
+        residual_rms_norm_fused_reference,
+        rms_norm_reference,
+        swiglu_fused_reference,
+    )
+    from tensorforge_amd.kernel_bench import config3, config4
+    from tensorforge_amd.workloads import llama3_long_context_case
+
+    device = torch.device("cuda", 0)
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    generator = torch.Generator().manual_seed(0)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=generator).to(torch.bfloat16)
+
+    cases = config4(device, calls)
+    for case in cases:
+        shape = case["shape"]
+        tokens = shape["tokens"]
+        if shape["op"] in ("rms_norm", "residual_rms_norm"):
+            x, r, w = randn(tokens, shape["hidden"]), randn(tokens, shape["hidden"]), randn(
+                shape["hidden"])
+            fn = ((lambda: rms_norm_reference(x, w, 1e-5)) if shape["op"] == "rms_norm"
+                  else (lambda: residual_rms_norm_fused_reference(x, r, w, 1e-5)))
+        elif shape["op"] == "swiglu":
+            g, u = randn(tokens, shape["ffn"]), randn(tokens, shape["ffn"])
+            fn = lambda: swiglu_fused_reference(g, u)  # noqa: E731
+        else:
+            keys, values = randn(tokens, 4, 64), randn(tokens, 4, 64)
+            kc, vc = randn(64, 16, 4, 64), randn(64, 16, 4, 64)
+            slots = torch.arange(5, 5 + tokens, dtype=torch.int64)
+            fn = lambda: paged_kv_write_slots_reference(keys, values, kc, vc, slots)  # noqa: E731
+        p50 = _cpu_p50(fn, seconds_per_case)
+        case["cpu_baseline"] = {"GB/s": round(case["algorithmic_bytes"] / p50 / 1e9, 3),
+                                "us_per_call": round(p50 * 1e6, 1), "cores": cores,
+                                "kind": "port"}
+    attention = config3(device, max(10, calls // 4))
+    cpu = llama3_long_context_case(seed=0)
+    p50 = _cpu_p50(lambda: paged_gqa_decode_reference(
+        cpu.query, cpu.key_cache, cpu.value_cache, cpu.block_tables, cpu.context_lengths,
+        scale=cpu.scale), seconds_per_case * 4, reps=2)
+    attention["cpu_baseline"] = {"GB/s": round(attention["algorithmic_bytes"] / p50 / 1e9, 3),
+                                 "us_per_call": round(p50 * 1e6, 1), "cores": cores,
+                                 "kind": "port"}
+    return {"metric": "config 3 and 4 kernels, graph-timed, CPU oracle beside each",
+            "unit": "GB/s", "cases": cases + [attention],
+            "cpu": platform.processor() or platform.machine()}
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -217,6 +290,9 @@ def main() -> int:
         return 1
     if args.copy_calibration_mib > 0:
         return copy_calibration(args.copy_calibration_mib)
+    if args.kernels:
+        print(json.dumps(kernels_line(100, 0.3)))
+        return 0
 
     from tensorforge_amd import _native
     from tensorforge_amd.kernels import PagedAttentionWorkspace, set_attention_split_size

@@ -77,14 +77,16 @@ def graph_time_us(run: Callable[[int], None], calls: int, device: torch.device) 
     return begin.elapsed_time(end) * 1e3 / calls
 
 
-def report(case: str, us: float, nbytes: int, **extra) -> None:
+def report(case: str, us: float, nbytes: int, **extra) -> dict:
     gbs = nbytes / (us * 1e-6) / 1e9
-    print(json.dumps({"case": case, "us_per_call": round(us, 3), "algorithmic_bytes": nbytes,
-                      "GB/s": round(gbs, 1), "hbm_fraction": round(gbs / HBM_PEAK_GBS, 4),
-                      **extra}), flush=True)
+    return {"case": case, "us_per_call": round(us, 3), "algorithmic_bytes": nbytes,
+            "GB/s": round(gbs, 1), "hbm_fraction": round(gbs / HBM_PEAK_GBS, 4), **extra}
 
 
-def config4(device: torch.device, calls: int) -> None:
+def config4(device: torch.device, calls: int) -> list[dict]:
+    """Config 4 cases, each a dict with its shape under "shape"."""
+
+    results = []
     generator = torch.Generator().manual_seed(0)
     dtype = torch.bfloat16
 
@@ -98,18 +100,23 @@ def config4(device: torch.device, calls: int) -> None:
             res_out, norm_out = torch.empty_like(x), torch.empty_like(x)
             us = graph_time_us(lambda i: residual_rms_norm(
                 x, r, weight, 1e-5, residual_output=res_out, norm_output=norm_out), calls, device)
-            report(f"residual_rms_norm T={tokens} H={hidden}", us,
-                   workloads.rms_norm_bytes(tokens, hidden, 2, residual=True))
+            results.append(report(f"residual_rms_norm T={tokens} H={hidden}", us,
+                                  workloads.rms_norm_bytes(tokens, hidden, 2, residual=True),
+                                  shape={"op": "residual_rms_norm", "tokens": tokens,
+                                         "hidden": hidden}))
             out = torch.empty_like(x)
             us = graph_time_us(lambda i: rms_norm(x, weight, 1e-5, output=out), calls, device)
-            report(f"rms_norm T={tokens} H={hidden}", us,
-                   workloads.rms_norm_bytes(tokens, hidden, 2, residual=False))
+            results.append(report(f"rms_norm T={tokens} H={hidden}", us,
+                                  workloads.rms_norm_bytes(tokens, hidden, 2, residual=False),
+                                  shape={"op": "rms_norm", "tokens": tokens, "hidden": hidden}))
     for ffn in (5632, 14336):
         for tokens in (1, 8, 64, 256):
             gate, up = randn(tokens, ffn), randn(tokens, ffn)
             out = torch.empty_like(gate)
             us = graph_time_us(lambda i: swiglu(gate, up, output=out), calls, device)
-            report(f"swiglu T={tokens} F={ffn}", us, workloads.swiglu_bytes(tokens * ffn, 2))
+            results.append(report(f"swiglu T={tokens} F={ffn}", us,
+                                  workloads.swiglu_bytes(tokens * ffn, 2),
+                                  shape={"op": "swiglu", "tokens": tokens, "ffn": ffn}))
     for tokens in (1, 8, 64, 256):
         config = PagedKVCacheConfig(num_layers=1, num_blocks=64, block_size=16, num_kv_heads=4,
                                     head_dim=64, max_sequences=1, max_sequence_length=1024,
@@ -123,11 +130,13 @@ def config4(device: torch.device, calls: int) -> None:
         keys, values = randn(tokens, 4, 64), randn(tokens, 4, 64)
         us = graph_time_us(lambda i: cache.write_layer(reservation, 0, keys, values), calls,
                            device)
-        report(f"kv_append T={tokens} (4 x 64, 16-token pages, straddling)", us,
-               workloads.kv_append_bytes(tokens, 4, 64, 2))
+        results.append(report(f"kv_append T={tokens} (4 x 64, 16-token pages, straddling)", us,
+                              workloads.kv_append_bytes(tokens, 4, 64, 2),
+                              shape={"op": "kv_append", "tokens": tokens}))
+    return results
 
 
-def config3(device: torch.device, calls: int) -> None:
+def config3(device: torch.device, calls: int) -> dict:
     case = workloads.llama3_long_context_case(seed=0)
     pools = [case.to(device) for _ in range(2)]  # 2 x 671 MB: the MALL cannot hold them
     batch, query_heads, head_dim = case.query.shape
@@ -144,8 +153,8 @@ def config3(device: torch.device, calls: int) -> None:
 
     us = graph_time_us(run, calls, device)
     nbytes = workloads.decode_attention_bytes(case.lengths, query_heads, 8, head_dim, 16, 2)
-    report("paged_gqa_decode cfg3 (4 x 8k..32k, 32/8 heads, D128, bf16)", us, nbytes,
-           record=selected_attention_autotune_config())
+    return report("paged_gqa_decode cfg3 (4 x 8k..32k, 32/8 heads, D128, bf16)", us, nbytes,
+                  record=selected_attention_autotune_config())
 
 
 def measure_decode_step(weights: DecoderWeights, batch: int, context: int, *,
@@ -234,9 +243,10 @@ def main() -> int:
         return 1
     device = torch.device("cuda", 0)
     if args.only in (None, "cfg4"):
-        config4(device, args.calls)
+        for result in config4(device, args.calls):
+            print(json.dumps(result), flush=True)
     if args.only in (None, "cfg3"):
-        config3(device, max(10, args.calls // 4))
+        print(json.dumps(config3(device, max(10, args.calls // 4))), flush=True)
     if args.only in (None, "decode"):
         decode_steps(device, "cfg1")
     if args.only in (None, "decode22"):
