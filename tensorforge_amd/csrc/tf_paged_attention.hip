@@ -25,9 +25,11 @@
 //    two reads per 16-dimension block; P (converted to the storage type) is
 //    already in the B-operand layout.  K/V for the next chunk are loaded
 //    before the current chunk is computed (two chunks in flight per wave).
-//    Wavefronts of a workgroup merge their (max, sum, acc) states in LDS.
-//    With arrival counters the last workgroup of a (row, kv head) to finish
-//    merges the split partials in the same launch.
+//    Several wavefronts of a workgroup may share a (row, kv head, split),
+//    taking its chunks round-robin, and merge their (max, sum, acc) states
+//    in LDS (for wide batches the whole row is one split: one pass, no
+//    partials).  With arrival counters the last workgroup of a (row, kv
+//    head) to finish merges the split partials in the same launch.
 //
 //  * Streaming (opt-in, TF_ATTENTION_FLAG_STREAM): one wavefront per
 //    workgroup, equal contiguous ranges of 16-token tiles per wavefront
@@ -1616,13 +1618,13 @@ int32_t choose_variant(int32_t dtype, int32_t head_dim, int32_t group, int32_t b
 // heads_per_wg * waves_per_head of them).
 constexpr int kMfmaWaves = 8;
 
-// Work split of the MFMA grid kernel: a workgroup serves HPW kv heads (the
-// largest divisor of kv_heads that is <= 8) with WPH = 8 / HPW wavefronts
-// per head.
-// Default: one wavefront per (row, kv head, split) -- measured fastest at
-// batch 64 x 2k (each wavefront finishes its own partial with no workgroup
-// barrier).  Flag bits 20-23 / 8-15 override HPW / WPH (tuning; HPW must
-// divide kv_heads and HPW * WPH <= 8).
+// Work split of the MFMA grid kernel: a workgroup serves HPW kv heads with
+// WPH wavefronts per head (HPW * WPH <= 8), and with a token budget per
+// wavefront (flag bits 24-30) a row uses only as many of the WPH as its
+// length needs.  Without flags: one wavefront per (row, kv head, split),
+// the fastest split-KV form.  The host plan of the Python entry point asks
+// for one pass with WPH = ceil(L / 768) and a 768-token budget for wide
+// batches (bits 20-23 / 8-15 / 24-30; HPW must divide kv_heads).
 void mfma_geometry(AttnParams &p, int32_t flags) {
   int32_t hpw = 1;
   const int32_t want_hpw = (flags >> TF_ATTENTION_HEADS_PER_WG_SHIFT) & 0xf;
