@@ -31,6 +31,8 @@
  *   tf_linear_rows           the nn.Linear projections of the decode step
  *                            (tensorforge/model/layers.py:88-95, 144-146;
  *                            runtime/decode_bucket.py:441-447, 470, 500-505)
+ *   tf_linear_partials,      the same projections at 17..64 rows, split over
+ *   tf_linear_partials_sum   K into fp32 partials and their row sum
  */
 #ifndef TENSORFORGE_AMD_H_
 #define TENSORFORGE_AMD_H_
@@ -249,6 +251,21 @@ int32_t tf_residual_rms_norm(const void *inputs, const void *residual,
                              float eps, int32_t dtype, void *stream);
 
 /*
+ * tf_residual_rms_norm with the inputs given as fp32 split-K partials
+ * (dense [splits, rows, columns], as tf_linear_partials writes them):
+ *   inputs[r][j] = round(sum_s partials[s][r][j])
+ * then exactly tf_residual_rms_norm.  Fuses the K-slice sum of the o and
+ * down projections into the norm that consumes them (the reference runs
+ * the torch GEMM, then residual_rms_norm: runtime/decode_bucket.py:470-483,
+ * 505-515; triton_ops.py:208-243).
+ */
+int32_t tf_residual_rms_norm_partials(const float *partials, int32_t splits,
+                                      const void *residual, const void *weight,
+                                      void *residual_output, void *norm_output,
+                                      int64_t rows, int32_t columns, float eps,
+                                      int32_t dtype, void *stream);
+
+/*
  * Elementwise SwiGLU: output = g * sigmoid(g) * u in fp32, one rounding.
  * Replaces triton_ops.py:246-260.
  */
@@ -279,6 +296,30 @@ int32_t tf_linear_rows(const void *x, int64_t x_row_stride, const void *weight,
                        int64_t weight_row_stride, void *y, int64_t y_row_stride,
                        int32_t m, int32_t n, int32_t k, int32_t waves_per_tile,
                        int32_t dtype, void *stream);
+
+/*
+ * Split-K form of the same product for up to 64 rows:
+ *   partials[s][i][j] = sum over k in slice s of x[i][k] * weight[j][k]  (fp32)
+ * The K / 32 k-steps are dealt into `splits` contiguous non-empty slices
+ * (splits must be in [1, K / 32] and leave no slice empty); partials is
+ * dense [splits, m, n] fp32.  K % 32 == 0, 16-byte aligned rows, fp16/bf16.
+ * Replaces the torch GEMM of the decode projections
+ * (tensorforge/model/layers.py:88-95, 144-146) at 17..64 rows.
+ */
+int32_t tf_linear_partials(const void *x, int64_t x_row_stride, const void *weight,
+                           int64_t weight_row_stride, float *partials, int32_t m,
+                           int32_t n, int32_t k, int32_t splits, int32_t dtype,
+                           void *stream);
+
+/*
+ * y[i][j] = round(sum_s partials[s][i][j]) into fp16/bf16 rows of y
+ * (n and y_row_stride multiples of 4, 16-byte aligned buffers).  With
+ * tf_linear_partials it is the projection x @ weight^T with fp32
+ * accumulation and one rounding, as torch's GEMM computes it.
+ */
+int32_t tf_linear_partials_sum(const float *partials, int32_t splits, int32_t m,
+                               int32_t n, void *y, int64_t y_row_stride,
+                               int32_t dtype, void *stream);
 
 #ifdef __cplusplus
 }

@@ -46,16 +46,22 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
 }
 
 // One workgroup per row.  RESIDUAL selects the fused residual variant.
-template <typename T, int VEC, bool RESIDUAL>
+// PARTIALS (with RESIDUAL) reads no `inputs`:
+// element j of the row is round(sum_s partials[s][row][j]) over `splits`
+// dense fp32 [rows, columns] planes, the rounded result of a split-K
+// projection (tf_linear_partials) whose sum is fused here.
+template <typename T, int VEC, bool RESIDUAL, bool PARTIALS>
 __global__ void __launch_bounds__(1024)
 rms_norm_kernel(const T *__restrict__ inputs, const T *__restrict__ residual,
                 const T *__restrict__ weight, T *__restrict__ residual_output,
-                T *__restrict__ output, int32_t columns, float eps) {
+                T *__restrict__ output, int32_t columns, float eps,
+                const float *__restrict__ partials, int32_t splits, int64_t plane) {
   __shared__ float scratch[16];
   using V = Vec<T, VEC>;
   const int64_t row = blockIdx.x;
   const int32_t nvec = columns / VEC;
-  const V *x = reinterpret_cast<const V *>(inputs + row * columns);
+  const V *x = reinterpret_cast<const V *>(inputs + (PARTIALS ? 0 : row * columns));
+  const float *prow = PARTIALS ? partials + row * columns : nullptr;
   const V *r = reinterpret_cast<const V *>(residual + (RESIDUAL ? row * columns : 0));
   V *ro = reinterpret_cast<V *>(residual_output + (RESIDUAL ? row * columns : 0));
   V *y = reinterpret_cast<V *>(output + row * columns);
@@ -68,7 +74,45 @@ rms_norm_kernel(const T *__restrict__ inputs, const T *__restrict__ residual,
   for (int k = 0; k < kMaxVecs; ++k) {
     const int32_t idx = threadIdx.x + k * blockDim.x;
     if (idx < nvec) {
-      V xv = x[idx];
+      V xv;
+      if constexpr (PARTIALS) {
+        float sum[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) sum[e] = 0.f;
+        // Slices in groups of kGroup whose loads are all issued before any
+        // is added (a slice past the last re-reads slice 0 and is dropped),
+        // so a row costs one memory round trip per kGroup slices; the sum
+        // still runs in slice order.
+        constexpr int kGroup = 8;
+        const float *base = prow + static_cast<int64_t>(idx) * VEC;
+        for (int32_t s0 = 0; s0 < splits; s0 += kGroup) {
+          float v[kGroup][VEC];
+#pragma unroll
+          for (int g = 0; g < kGroup; ++g) {
+            const float *src = base + (s0 + g < splits ? s0 + g : 0) * plane;
+            if constexpr (VEC % 4 == 0) {
+#pragma unroll
+              for (int q = 0; q < VEC / 4; ++q) {
+                const f32x4 x4 = *reinterpret_cast<const f32x4 *>(src + 4 * q);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[g][4 * q + e] = x4[e];
+              }
+            } else {
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) v[g][e] = src[e];
+            }
+          }
+#pragma unroll
+          for (int g = 0; g < kGroup; ++g)
+            if (s0 + g < splits)
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) sum[e] += v[g][e];
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) xv.v[e] = from_float<T>(sum[e]);
+      } else {
+        xv = x[idx];
+      }
       V rv;
       if constexpr (RESIDUAL) rv = r[idx];
       V sv;
@@ -145,38 +189,49 @@ swiglu_rows_kernel(const T *__restrict__ gate_up, int64_t in_stride, T *__restri
 template <typename T, int VEC, bool RESIDUAL>
 void launch_norm(const void *inputs, const void *residual, const void *weight,
                  void *residual_output, void *output, int64_t rows, int32_t columns,
-                 float eps, hipStream_t stream) {
+                 float eps, const float *partials, int32_t splits, hipStream_t stream) {
   constexpr int kMaxVecs = max_vecs<VEC>();
   const int32_t nvec = columns / VEC;
-  // Two vectors per lane where possible; the register cache holds kMaxVecs.
-  int threads = ((nvec + 1) / 2 + 63) / 64 * 64;
+  // Two vectors per lane where possible (one when the inputs are summed
+  // from split-K partials, which costs more loads per vector); the register
+  // cache holds kMaxVecs.
+  int threads = partials ? (nvec + 63) / 64 * 64 : ((nvec + 1) / 2 + 63) / 64 * 64;
   const int min_threads = ((nvec + kMaxVecs - 1) / kMaxVecs + 63) / 64 * 64;
   if (threads < min_threads) threads = min_threads;
   if (threads < 64) threads = 64;
   if (threads > 1024) threads = 1024;
-  hipLaunchKernelGGL((rms_norm_kernel<T, VEC, RESIDUAL>), dim3(static_cast<unsigned>(rows)),
-                     dim3(threads), 0, stream, static_cast<const T *>(inputs),
-                     static_cast<const T *>(residual), static_cast<const T *>(weight),
-                     static_cast<T *>(residual_output), static_cast<T *>(output), columns, eps);
+  const int64_t plane = rows * static_cast<int64_t>(columns);
+  if (RESIDUAL && partials)
+    hipLaunchKernelGGL((rms_norm_kernel<T, VEC, RESIDUAL, RESIDUAL>), dim3(static_cast<unsigned>(rows)),
+                       dim3(threads), 0, stream, static_cast<const T *>(inputs),
+                       static_cast<const T *>(residual), static_cast<const T *>(weight),
+                       static_cast<T *>(residual_output), static_cast<T *>(output), columns, eps,
+                       partials, splits, plane);
+  else
+    hipLaunchKernelGGL((rms_norm_kernel<T, VEC, RESIDUAL, false>), dim3(static_cast<unsigned>(rows)),
+                       dim3(threads), 0, stream, static_cast<const T *>(inputs),
+                       static_cast<const T *>(residual), static_cast<const T *>(weight),
+                       static_cast<T *>(residual_output), static_cast<T *>(output), columns, eps,
+                       nullptr, 0, plane);
 }
 
 template <typename T, bool RESIDUAL>
 int32_t dispatch_norm(const void *inputs, const void *residual, const void *weight,
                       void *residual_output, void *output, int64_t rows, int32_t columns,
-                      float eps, hipStream_t stream) {
+                      float eps, const float *partials, int32_t splits, hipStream_t stream) {
   constexpr int kVec = 16 / sizeof(T);
-  uintptr_t align = reinterpret_cast<uintptr_t>(inputs) | reinterpret_cast<uintptr_t>(weight) |
-                    reinterpret_cast<uintptr_t>(output);
+  uintptr_t align = reinterpret_cast<uintptr_t>(partials ? partials : inputs) |
+                    reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(output);
   if (RESIDUAL)
     align |= reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(residual_output);
   const bool vectorised = columns % kVec == 0 && align % 16 == 0 &&
                           columns / kVec <= 1024 * max_vecs<kVec>();
   if (vectorised) {
     launch_norm<T, kVec, RESIDUAL>(inputs, residual, weight, residual_output, output, rows,
-                                   columns, eps, stream);
+                                   columns, eps, partials, splits, stream);
   } else if (columns <= 1024 * max_vecs<1>()) {
     launch_norm<T, 1, RESIDUAL>(inputs, residual, weight, residual_output, output, rows,
-                                columns, eps, stream);
+                                columns, eps, partials, splits, stream);
   } else {
     return fail(TF_ERROR_UNSUPPORTED, "RMSNorm row does not fit the register cache");
   }
@@ -186,27 +241,29 @@ int32_t dispatch_norm(const void *inputs, const void *residual, const void *weig
 template <bool RESIDUAL>
 int32_t norm_entry(const void *inputs, const void *residual, const void *weight,
                    void *residual_output, void *output, int64_t rows, int32_t columns,
-                   float eps, int32_t dtype, void *stream) {
+                   float eps, int32_t dtype, void *stream, const float *partials = nullptr,
+                   int32_t splits = 0) {
   clear_error();
   if (!valid_dtype(dtype)) return fail(TF_ERROR_INVALID_ARGUMENT, "unsupported dtype code");
   if (rows < 0 || columns <= 0 || columns > 16384)
     return fail(TF_ERROR_INVALID_ARGUMENT, "RMSNorm needs 0 <= rows and 0 < columns <= 16384");
   if (rows > 0x7fffffff) return fail(TF_ERROR_UNSUPPORTED, "too many rows for one launch");
   if (!(eps > 0.f)) return fail(TF_ERROR_INVALID_ARGUMENT, "eps must be positive");
-  if (!inputs || !weight || !output || (RESIDUAL && (!residual || !residual_output)))
+  if (!(partials ? static_cast<const void *>(partials) : inputs) || !weight || !output ||
+      (RESIDUAL && (!residual || !residual_output)))
     return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
   if (rows == 0) return TF_SUCCESS;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case TF_DTYPE_FLOAT32:
       return dispatch_norm<float, RESIDUAL>(inputs, residual, weight, residual_output, output,
-                                            rows, columns, eps, s);
+                                            rows, columns, eps, partials, splits, s);
     case TF_DTYPE_FLOAT16:
       return dispatch_norm<_Float16, RESIDUAL>(inputs, residual, weight, residual_output,
-                                               output, rows, columns, eps, s);
+                                               output, rows, columns, eps, partials, splits, s);
     default:
       return dispatch_norm<__bf16, RESIDUAL>(inputs, residual, weight, residual_output, output,
-                                             rows, columns, eps, s);
+                                             rows, columns, eps, partials, splits, s);
   }
 }
 
@@ -276,6 +333,19 @@ extern "C" int32_t tf_residual_rms_norm(const void *inputs, const void *residual
                                         float eps, int32_t dtype, void *stream) {
   return tf::norm_entry<true>(inputs, residual, weight, residual_output, norm_output, rows,
                               columns, eps, dtype, stream);
+}
+
+extern "C" int32_t tf_residual_rms_norm_partials(const float *partials, int32_t splits,
+                                                 const void *residual, const void *weight,
+                                                 void *residual_output, void *norm_output,
+                                                 int64_t rows, int32_t columns, float eps,
+                                                 int32_t dtype, void *stream) {
+  using namespace tf;
+  clear_error();
+  if (splits < 1) return fail(TF_ERROR_INVALID_ARGUMENT, "splits must be positive");
+  if (!partials) return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  return norm_entry<true>(nullptr, residual, weight, residual_output, norm_output, rows, columns,
+                          eps, dtype, stream, partials, splits);
 }
 
 extern "C" int32_t tf_swiglu(const void *gate, const void *up, void *output, int64_t numel,

@@ -1,0 +1,264 @@
+// Split-K decode linear layer on MFMA for 17..64 rows:
+//   partials[s][m][n] = sum over k in slice s of x[m][k] * w[n][k]   (fp32)
+// and the row sum y[m][n] = round(sum_s partials[s][m][n]).
+//
+// At decode batch sizes a projection streams its weight matrix once (each
+// element is used M <= 64 times) and is HBM-bound; what a library GEMM
+// tiled for large M lacks is parallelism -- a 2048 x 2048 weight in 64 x 64
+// output tiles is 32 workgroups.  Here blockIdx.x is a 64-column tile and
+// blockIdx.y one of S slices of K, so a launch has (N / 64) * S workgroups
+// each streaming a 64-row slab of w that is K / S long.  Inside a workgroup
+// the four wavefronts split the slice's 32-wide k-steps between them and
+// each accumulates the whole 64 x 64 tile (4 row tiles x 4 column tiles of
+// v_mfma_f32_16x16x32), so a wavefront reads as many bytes of x as of w (x
+// is small and stays in L2; a 16-column tiling would read x four times as
+// often as w).  Up to four k-steps of loads (w and x) are issued together.
+// The four wavefront tiles are summed once in LDS and stored as the
+// slice's fp32 partial; the reduction over the S slices is left to the
+// consumer of y (tf_linear_partials_sum here, or a fused consumer), so the
+// launch needs no atomics, counters or second pass of its own.
+//
+// MFMA v_mfma_f32_16x16x32 (bf16 / f16):
+//   A = x rows:  lane (l16, q4) holds x[16 mt + l16][k + 8 q4 .. +8]
+//   B = w rows:  lane (l16, q4) holds w[n0 + 16 nt + l16][k + 8 q4 .. +8]
+//   C:           lane (l16, q4), register r holds y[16 mt + 4 q4 + r][n0 + 16 nt + l16]
+//
+// Reference semantics: torch.nn.functional.linear(x, w) without bias (fp32
+// accumulation, one rounding to the storage type), the nn.Linear
+// projections of tensorforge/model/layers.py:88-95, 144-146 as the decode
+// step calls them (tensorforge/runtime/decode_bucket.py:441-447, 470,
+// 500-505).
+#include "tf_common.hpp"
+
+namespace tf {
+namespace {
+
+template <typename T>
+struct SplitMma;
+
+template <>
+struct SplitMma<__bf16> {
+  typedef __bf16 vec8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x4 mma(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct SplitMma<_Float16> {
+  typedef _Float16 vec8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x4 mma(vec8 a, vec8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int kSplitWaves = 4;    // wavefronts per workgroup
+constexpr int kSplitCols = 64;    // output columns per workgroup
+constexpr int kSplitUnroll = 4;   // k-steps of loads in flight per wavefront
+
+template <typename T, int MT>
+__global__ void __launch_bounds__(kSplitWaves * 64)
+linear_partials_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restrict__ w,
+                       int64_t w_stride, float *__restrict__ partials, int32_t m, int32_t n,
+                       int32_t k, int32_t k_per_split) {
+  using M = SplitMma<T>;
+  using vec8 = typename M::vec8;
+  constexpr int NT = kSplitCols / 16;
+  constexpr int kItems = MT * NT * 4 * 64;  // floats of one wavefront's tile
+  extern __shared__ __attribute__((aligned(16))) float tile_sums[];  // [waves][kItems]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l16 = lane & 15;
+  const int q4 = lane >> 4;
+  const int32_t n0 = blockIdx.x * kSplitCols;
+  const int32_t split = blockIdx.y;
+  const int32_t s0 = split * k_per_split;
+  const int32_t s1 = min(s0 + k_per_split, k);
+  // k-steps of the slice, dealt to the wavefronts in contiguous runs.
+  const int32_t steps = (s1 - s0) / 32;
+  const int32_t per_wave = (steps + kSplitWaves - 1) / kSplitWaves;
+  const int32_t k0 = s0 + 32 * min(wave * per_wave, steps);
+  const int32_t k1 = s0 + 32 * min((wave + 1) * per_wave, steps);
+
+  const T *wrow[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    wrow[nt] = w + static_cast<int64_t>(min(n0 + 16 * nt + l16, n - 1)) * w_stride + 8 * q4;
+  const T *xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xrow[mt] = x + static_cast<int64_t>(min(16 * mt + l16, m - 1)) * x_stride + 8 * q4;
+
+  f32x4 acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Batches of kSplitUnroll k-steps: every load of a batch is issued before
+  // its MFMAs; steps past k1 load the batch's first step again and are
+  // zeroed, so the loads stay unconditional.
+  for (int32_t kk = k0; kk < k1; kk += 32 * kSplitUnroll) {
+    vec8 wb[kSplitUnroll][NT];
+    vec8 xa[kSplitUnroll][MT];
+#pragma unroll
+    for (int u = 0; u < kSplitUnroll; ++u) {
+      const int32_t ku = kk + 32 * u < k1 ? kk + 32 * u : kk;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) wb[u][nt] = *reinterpret_cast<const vec8 *>(wrow[nt] + ku);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) xa[u][mt] = *reinterpret_cast<const vec8 *>(xrow[mt] + ku);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kSplitUnroll; ++u) {
+      if (kk + 32 * u >= k1) break;  // uniform
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = M::mma(xa[u][mt], wb[u][nt], acc[mt][nt]);
+    }
+  }
+
+  // Sum the wavefront tiles: item (mt, nt, r, lane).
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        tile_sums[wave * kItems + ((mt * NT + nt) * 4 + r) * 64 + lane] = acc[mt][nt][r];
+  __syncthreads();
+  float *out = partials + static_cast<int64_t>(split) * m * n;
+  for (int item = threadIdx.x; item < kItems; item += blockDim.x) {
+    float sum = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kSplitWaves; ++wv) sum += tile_sums[wv * kItems + item];
+    const int il = item & 63;
+    const int r = (item >> 6) & 3;
+    const int tile = item >> 8;
+    const int mt = tile / NT;
+    const int nt = tile - mt * NT;
+    const int32_t row = 16 * mt + 4 * (il >> 4) + r;
+    const int32_t col = n0 + 16 * nt + (il & 15);
+    if (row < m && col < n) out[static_cast<int64_t>(row) * n + col] = sum;
+  }
+}
+
+// y[m][n] = round(sum_s partials[s][m][n]), four columns per thread.
+template <typename T>
+__global__ void __launch_bounds__(256)
+partials_sum_kernel(const float *__restrict__ partials, int32_t splits, int32_t m, int32_t n,
+                    T *__restrict__ y, int64_t y_stride) {
+  const int64_t quads = static_cast<int64_t>(m) * (n / 4);
+  const int64_t plane = static_cast<int64_t>(m) * n;
+  for (int64_t q = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; q < quads;
+       q += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int32_t row = static_cast<int32_t>(q / (n / 4));
+    const int32_t col = 4 * static_cast<int32_t>(q - static_cast<int64_t>(row) * (n / 4));
+    const float *src = partials + static_cast<int64_t>(row) * n + col;
+    f32x4 s = *reinterpret_cast<const f32x4 *>(src);
+    for (int32_t sp = 1; sp < splits; ++sp) s += *reinterpret_cast<const f32x4 *>(src + sp * plane);
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    const t4 v = {from_float<T>(s[0]), from_float<T>(s[1]), from_float<T>(s[2]),
+                  from_float<T>(s[3])};
+    *reinterpret_cast<t4 *>(y + static_cast<int64_t>(row) * y_stride + col) = v;
+  }
+}
+
+template <typename T, int MT>
+void launch_partials(const void *x, int64_t x_stride, const void *w, int64_t w_stride,
+                     float *partials, int32_t m, int32_t n, int32_t k, int32_t splits,
+                     int32_t k_per_split, hipStream_t stream) {
+  const size_t lds = static_cast<size_t>(kSplitWaves) * MT * (kSplitCols / 16) * 4 * 64 *
+                     sizeof(float);
+  hipLaunchKernelGGL((linear_partials_kernel<T, MT>),
+                     dim3((n + kSplitCols - 1) / kSplitCols, splits), dim3(kSplitWaves * 64), lds,
+                     stream, static_cast<const T *>(x), x_stride, static_cast<const T *>(w),
+                     w_stride, partials, m, n, k, k_per_split);
+}
+
+template <typename T>
+void launch_partials_mt(const void *x, int64_t x_stride, const void *w, int64_t w_stride,
+                        float *partials, int32_t m, int32_t n, int32_t k, int32_t splits,
+                        int32_t k_per_split, hipStream_t stream) {
+  switch ((m + 15) / 16) {
+    case 1: launch_partials<T, 1>(x, x_stride, w, w_stride, partials, m, n, k, splits, k_per_split, stream); break;
+    case 2: launch_partials<T, 2>(x, x_stride, w, w_stride, partials, m, n, k, splits, k_per_split, stream); break;
+    case 3: launch_partials<T, 3>(x, x_stride, w, w_stride, partials, m, n, k, splits, k_per_split, stream); break;
+    default: launch_partials<T, 4>(x, x_stride, w, w_stride, partials, m, n, k, splits, k_per_split, stream); break;
+  }
+}
+
+}  // namespace
+}  // namespace tf
+
+extern "C" int32_t tf_linear_partials(const void *x, int64_t x_row_stride, const void *weight,
+                                      int64_t weight_row_stride, float *partials, int32_t m,
+                                      int32_t n, int32_t k, int32_t splits, int32_t dtype,
+                                      void *stream) {
+  using namespace tf;
+  clear_error();
+  if (dtype != TF_DTYPE_FLOAT16 && dtype != TF_DTYPE_BFLOAT16)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_partials supports fp16 and bf16");
+  if (m < 0 || n < 0 || k < 0) return fail(TF_ERROR_INVALID_ARGUMENT, "sizes must be non-negative");
+  if (m > 64) return fail(TF_ERROR_UNSUPPORTED, "linear_partials supports at most 64 rows");
+  if (k % 32 != 0 || k == 0)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_partials needs K to be a positive multiple of 32");
+  if (splits < 1 || splits > k / 32)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "splits must be in [1, K / 32]");
+  if (x_row_stride < k || weight_row_stride < k)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "row strides are shorter than the rows");
+  if (n > 65535 * tf::kSplitCols || splits > 65535)
+    return fail(TF_ERROR_UNSUPPORTED, "grid too large");
+  if (m == 0 || n == 0) return TF_SUCCESS;
+  if (!x || !weight || !partials) return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
+                          static_cast<uintptr_t>(x_row_stride * 2) |
+                          static_cast<uintptr_t>(weight_row_stride * 2);
+  if (align % 16 != 0)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_partials needs 16-byte aligned x and weight rows");
+  // Slices of whole k-steps; every slice is non-empty.
+  const int32_t steps = k / 32;
+  const int32_t k_per_split = ((steps + splits - 1) / splits) * 32;
+  const int32_t used = (k + k_per_split - 1) / k_per_split;
+  if (used != splits)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "splits must divide K / 32 into non-empty slices");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TF_DTYPE_BFLOAT16)
+    launch_partials_mt<__bf16>(x, x_row_stride, weight, weight_row_stride, partials, m, n, k,
+                               splits, k_per_split, s);
+  else
+    launch_partials_mt<_Float16>(x, x_row_stride, weight, weight_row_stride, partials, m, n, k,
+                                 splits, k_per_split, s);
+  return check_launch("linear_partials");
+}
+
+extern "C" int32_t tf_linear_partials_sum(const float *partials, int32_t splits, int32_t m,
+                                          int32_t n, void *y, int64_t y_row_stride,
+                                          int32_t dtype, void *stream) {
+  using namespace tf;
+  clear_error();
+  if (!valid_dtype(dtype)) return fail(TF_ERROR_INVALID_ARGUMENT, "unsupported dtype code");
+  if (dtype == TF_DTYPE_FLOAT32)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_partials_sum writes fp16 or bf16");
+  if (m < 0 || n < 0 || splits < 1) return fail(TF_ERROR_INVALID_ARGUMENT, "invalid sizes");
+  if (n % 4 != 0 || y_row_stride % 4 != 0)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_partials_sum needs N and the row stride to be multiples of 4");
+  if (y_row_stride < n) return fail(TF_ERROR_INVALID_ARGUMENT, "row stride is shorter than the rows");
+  if (m == 0 || n == 0) return TF_SUCCESS;
+  if (!partials || !y) return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  if ((reinterpret_cast<uintptr_t>(partials) | reinterpret_cast<uintptr_t>(y)) % 16 != 0)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_partials_sum needs 16-byte aligned buffers");
+  const int64_t quads = static_cast<int64_t>(m) * (n / 4);
+  const int64_t blocks = (quads + 255) / 256;
+  const dim3 grid(static_cast<unsigned>(blocks < 2048 ? blocks : 2048));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TF_DTYPE_BFLOAT16)
+    hipLaunchKernelGGL(partials_sum_kernel<__bf16>, grid, dim3(256), 0, s, partials, splits, m, n,
+                       static_cast<__bf16 *>(y), y_row_stride);
+  else
+    hipLaunchKernelGGL(partials_sum_kernel<_Float16>, grid, dim3(256), 0, s, partials, splits, m,
+                       n, static_cast<_Float16 *>(y), y_row_stride);
+  return check_launch("linear_partials_sum");
+}

@@ -7,7 +7,8 @@ sequences runs as ONE captured HIP graph.  Per layer:
 * ``rms_norm`` (first layer) or the fused ``residual_rms_norm``;
 * one fused QKV projection;
 * ``rope_paged_kv_append``: RoPE on q and k, and k, v into their pages;
-* ``paged_gqa_decode_attention`` (split stage + merge);
+* ``paged_gqa_decode_attention`` (one pass for wide buckets, split-KV
+  with its merge otherwise);
 * the output projection;
 * ``residual_rms_norm`` of (attention output, residual);
 * one fused gate|up projection, ``swiglu_gate_up``, the down projection.
@@ -41,6 +42,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from tensorforge_amd.cache import AppendReservation, PagedKVCache
 from tensorforge_amd.kernels import (
     PagedAttentionWorkspace,
+    linear_partials,
     linear_rows,
     linear_rows_supported,
     paged_gqa_decode_attention,
@@ -49,7 +51,9 @@ from tensorforge_amd.kernels import (
     rope_paged_kv_append,
     swiglu_gate_up,
 )
-from tensorforge_amd.kernels.attention import attention_split_size_for, set_attention_split_size
+from tensorforge_amd.kernels.attention import set_attention_split_size
+from tensorforge_amd.kernels.linear import default_splits, linear_partials_supported
+from tensorforge_amd.kernels.ops import residual_rms_norm_partials
 
 
 @dataclass(frozen=True, slots=True)
@@ -229,7 +233,6 @@ class DecodeGraphBucket:
         self.workspace = PagedAttentionWorkspace.allocate(
             batch_capacity=b, query_heads=hq, head_dim=d, max_context_length=context_capacity,
             device=device)
-        self.split_size = attention_split_size_for(context_capacity, b, hkv)
         self.query = torch.empty((b, hq, d), dtype=dtype, device=device)
         self.attention_output = torch.empty((b, hq, d), dtype=dtype, device=device)
         self.norm_output = torch.empty((b, config.hidden_size), dtype=dtype, device=device)
@@ -237,6 +240,21 @@ class DecodeGraphBucket:
                                          device=device)
         self.logits = torch.empty((b, config.vocab_size), dtype=dtype, device=device)
         self.next_tokens = self.token_state[:b]
+        # Output and down projections at 17..64 rows: split-K partials whose
+        # K-slice sum is fused into the residual RMSNorm that consumes them.
+        self.split_o = self.split_down = 0
+        if 16 < b <= 64 and dtype in (torch.float16, torch.bfloat16):
+            layer0 = weights.layers[0]
+            probe_o = torch.empty((b, hq * d), dtype=dtype, device=device)
+            probe_d = torch.empty((b, config.intermediate_size), dtype=dtype, device=device)
+            if (linear_partials_supported(probe_o, layer0.o_proj)
+                    and linear_partials_supported(probe_d, layer0.down)):
+                self.split_o = default_splits(*layer0.o_proj.shape)
+                self.split_down = default_splits(*layer0.down.shape)
+                self.partials_o = torch.empty((self.split_o, b, config.hidden_size),
+                                              dtype=torch.float32, device=device)
+                self.partials_down = torch.empty((self.split_down, b, config.hidden_size),
+                                                 dtype=torch.float32, device=device)
         self._graph: torch.cuda.CUDAGraph | None = None
 
     def addresses(self) -> dict[str, int]:
@@ -345,7 +363,10 @@ class DecodeGraphBucket:
         hq, hkv, d = config.num_attention_heads, config.num_key_value_heads, config.head_dim
         b = self.batch_capacity
         eps = config.rms_norm_eps
-        previous = set_attention_split_size(self.split_size)
+        # The attention plan is chosen per call from the bucket's sizes (one
+        # pass for wide buckets, split-KV otherwise), whatever partition size
+        # a caller may have fixed globally.
+        previous = set_attention_split_size(None)
         try:
             fed = self.token_state.index_select(0, self.source_lanes.clamp(min=0))
             input_ids = torch.where(self.source_lanes >= 0, fed, self.host_tokens)
@@ -366,17 +387,32 @@ class DecodeGraphBucket:
                     q, key_cache, value_cache, self.block_tables, self.context_lengths,
                     scale=d ** -0.5, max_context_length=self.context_capacity,
                     output=self.attention_output, workspace=self.workspace)
-                attn = _project(self.attention_output.view(b, hq * d), layer.o_proj)
-                residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps,
-                                                residual_output=torch.empty_like(attn),
-                                                norm_output=self.norm_output)
+                attention = self.attention_output.view(b, hq * d)
+                if self.split_o:
+                    linear_partials(attention, layer.o_proj, self.split_o,
+                                    partials=self.partials_o)
+                    residual, h = residual_rms_norm_partials(
+                        self.partials_o, residual, layer.post_norm, eps,
+                        residual_output=torch.empty_like(residual), norm_output=self.norm_output)
+                else:
+                    attn = _project(attention, layer.o_proj)
+                    residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps,
+                                                    residual_output=torch.empty_like(attn),
+                                                    norm_output=self.norm_output)
                 act = swiglu_gate_up(_project(h, layer.gate_up), output=self.swiglu_output)
-                mlp = _project(act, layer.down)
                 next_norm = (self.weights.layers[index + 1].input_norm
                              if index + 1 < len(self.weights.layers) else self.weights.final_norm)
-                residual, h = residual_rms_norm(mlp, residual, next_norm, eps,
-                                                residual_output=torch.empty_like(mlp),
-                                                norm_output=self.norm_output)
+                if self.split_down:
+                    linear_partials(act, layer.down, self.split_down,
+                                    partials=self.partials_down)
+                    residual, h = residual_rms_norm_partials(
+                        self.partials_down, residual, next_norm, eps,
+                        residual_output=torch.empty_like(residual), norm_output=self.norm_output)
+                else:
+                    mlp = _project(act, layer.down)
+                    residual, h = residual_rms_norm(mlp, residual, next_norm, eps,
+                                                    residual_output=torch.empty_like(mlp),
+                                                    norm_output=self.norm_output)
             _project(h, self.weights.lm_head, output=self.logits)
             torch.argmax(self.logits, dim=-1, out=self.next_tokens)
         finally:

@@ -13,7 +13,11 @@
   {32, 128, 512, 2048}, the grid of the reference's decode-step report
   (results/reference/phase7a-rtx3080ti-wsl/execution.md); device time per
   step from HIP events, and host-inclusive time per step of the pipelined
-  launch/collect loop.
+  launch/collect loop;
+* ceiling -- what bounds the config-2 attention call: the graph launch gap,
+  a fit of time against bytes over uniform-length batches (fixed cost per
+  call and marginal rate), config 2 on random and on contiguous pages, and
+  one compute unit's rate with 1..8 wavefronts per kv head.
 
 Each case is captured as ``--calls`` launches in one HIP graph and timed by
 HIP events around one replay (a ctypes call costs the host longer than these
@@ -157,6 +161,112 @@ def config3(device: torch.device, calls: int) -> dict:
                   record=selected_attention_autotune_config())
 
 
+def attention_ceiling(device: torch.device, calls: int) -> list[dict]:
+    """What bounds the config-2 attention call: the fixed cost of a call, the
+    marginal streaming rate, the cost of ragged lengths, and one compute
+    unit's ceiling.
+
+    * the graph launch gap of a one-element kernel;
+    * the public entry point (one pass) at TinyLlama geometry over 64 rows
+      of uniform length L in {16, 512, 1024, 1210, 2048} plus 8 empty rows:
+      a least-squares line through time vs algorithmic bytes gives the
+      fixed microseconds per call and the marginal GB/s; 1210 tokens is the
+      config-2 byte count spread evenly, so it is the time config 2 would
+      take with no length imbalance;
+    * config 2 itself with its random pages and with the same rows on
+      contiguous pages (page locality);
+    * 16 rows x 2048 (64 compute units busy) with 1..8 wavefronts per kv
+      head through the C ABI: one compute unit's ceiling at low load.
+    Every case rotates 6 copies of its page pool (the MALL cannot hold them).
+    """
+
+    from tensorforge_amd import _native
+
+    results = []
+    tiny = torch.zeros(1, device=device)
+    launch_us = graph_time_us(lambda i: tiny.add_(1.0), 200, device)
+    results.append({"case": "graph launch gap (one-element add_ kernel)",
+                    "us_per_call": round(launch_us, 3)})
+
+    def attention_case(name: str, case: workloads.DecodeAttentionCase,
+                       flags: int | None = None) -> dict:
+        gpu = case.to(device)
+        pools = [(gpu.key_cache, gpu.value_cache)] + [
+            (gpu.key_cache.clone(), gpu.value_cache.clone()) for _ in range(5)]
+        output = torch.empty_like(gpu.query)
+        batch, query_heads, head_dim = gpu.query.shape
+        num_blocks, block_size, kv_heads, _ = gpu.key_cache.shape
+        width = gpu.block_tables.shape[1]
+        lib = _native.library()
+
+        def run(i: int) -> None:
+            key_cache, value_cache = pools[i % len(pools)]
+            if flags is None:
+                paged_gqa_decode_attention(query=gpu.query, key_cache=key_cache,
+                                           value_cache=value_cache,
+                                           block_tables=gpu.block_tables,
+                                           context_lengths=gpu.context_lengths,
+                                           scale=case.scale, max_context_length=2048,
+                                           output=output)
+                return
+            _native.check(lib.tf_paged_gqa_decode(
+                gpu.query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+                gpu.block_tables.data_ptr(), gpu.context_lengths.data_ptr(),
+                output.data_ptr(), None, None, None, None, 0, head_dim, batch, query_heads,
+                kv_heads, head_dim, num_blocks, block_size, width,
+                (width * block_size + 31) // 32 * 32, 1, case.scale,
+                _native.dtype_code(gpu.query.dtype), flags,
+                _native.current_stream(device)), "tf_paged_gqa_decode")
+
+        us = graph_time_us(run, calls, device)
+        nbytes = workloads.decode_attention_bytes(case.lengths, query_heads, kv_heads,
+                                                  head_dim, block_size, 2)
+        return report(name, us, nbytes)
+
+    def rows(lengths: list[int]) -> workloads.DecodeAttentionCase:
+        return workloads.make_decode_attention_case(
+            lengths, query_heads=32, kv_heads=4, head_dim=64, block_size=16,
+            dtype=torch.bfloat16, seed=0)
+
+    uniform = []
+    for length in (16, 512, 1024, 1210, 2048):
+        result = attention_case(f"one pass, 64 rows x {length} + 8 empty", rows([length] * 64 + [0] * 8))
+        uniform.append(result)
+        results.append(result)
+    xs = [r["algorithmic_bytes"] / 1e6 for r in uniform]
+    ys = [r["us_per_call"] for r in uniform]
+    mean_x, mean_y = sum(xs) / len(xs), sum(ys) / len(ys)
+    slope = (sum((x - mean_x) * (y - mean_y) for x, y in zip(xs, ys))
+             / sum((x - mean_x) ** 2 for x in xs))
+    fixed_us = mean_y - slope * mean_x
+    results.append({"case": "fit over the uniform rows: time = fixed + bytes / rate",
+                    "fixed_us": round(fixed_us, 2), "marginal_GB/s": round(1e3 / slope, 1)})
+
+    config2 = workloads.tinyllama_decode_case(seed=0, dtype=torch.bfloat16)
+    results.append(attention_case("config 2 (random pages)", config2))
+    contiguous = rows(config2.lengths)
+    tables = contiguous.block_tables.clone()
+    cursor = 0
+    for row, ctx in enumerate(config2.lengths):
+        pages = (ctx + 15) // 16
+        tables[row, :pages] = torch.arange(cursor, cursor + pages, dtype=torch.int32)
+        cursor += pages
+    contiguous.block_tables = tables
+    results.append(attention_case("config 2 rows on contiguous pages", contiguous))
+
+    few = rows([2048] * 16)
+    for waves in (1, 2, 3, 4, 6, 8):
+        flags = ((1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
+                 | (waves << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
+                 | ((256 // 64) << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
+        result = attention_case(f"16 rows x 2048, {waves} wavefronts per kv head", few, flags)
+        # 64 (row, kv head) workgroups, one compute unit each
+        result["GB/s_per_compute_unit_beyond_fixed"] = round(
+            result["algorithmic_bytes"] / 64 / (result["us_per_call"] - fixed_us) / 1e3, 1)
+        results.append(result)
+    return results
+
+
 def measure_decode_step(weights: DecoderWeights, batch: int, context: int, *,
                         steps: int = 64, seed: int = 0,
                         prompt_lengths: list[int] | None = None) -> dict:
@@ -236,7 +346,8 @@ def decode_steps(device: torch.device, model: str = "cfg1", steps: int = 64) -> 
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--calls", type=int, default=100)
-    parser.add_argument("--only", choices=("cfg3", "cfg4", "decode", "decode22"), default=None)
+    parser.add_argument("--only", choices=("cfg3", "cfg4", "decode", "decode22", "ceiling"),
+                        default=None)
     args = parser.parse_args()
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -251,6 +362,9 @@ def main() -> int:
         decode_steps(device, "cfg1")
     if args.only in (None, "decode22"):
         decode_steps(device, "tinyllama")
+    if args.only in (None, "ceiling"):
+        for result in attention_ceiling(device, args.calls):
+            print(json.dumps(result), flush=True)
     return 0
 
 

@@ -14,7 +14,12 @@ from tensorforge_amd.kernels.attention import (
     set_attention_split_size,
 )
 from tensorforge_amd.kernels.cache_write import paged_kv_write_slots, paged_kv_write_token
-from tensorforge_amd.kernels.linear import linear_rows, linear_rows_supported
+from tensorforge_amd.kernels.linear import (
+    linear_partials,
+    linear_partials_sum,
+    linear_rows,
+    linear_rows_supported,
+)
 from tensorforge_amd.kernels.ops import (
     autotune_cache_size,
     is_hip_available,
@@ -31,6 +36,8 @@ __all__ = [
     "autotune_cache_size",
     "is_hip_attention_available",
     "is_hip_available",
+    "linear_partials",
+    "linear_partials_sum",
     "linear_rows",
     "linear_rows_supported",
     "paged_gqa_decode_attention",

@@ -1,4 +1,5 @@
-"""Decode-shaped linear layer on gfx950 MFMA (``csrc/tf_linear_rows.hip``).
+"""Decode-shaped linear layers on gfx950 MFMA (``csrc/tf_linear_rows.hip``,
+``csrc/tf_linear_splitk.hip``).
 
 ``linear_rows(x, weight)`` computes ``x @ weight.T`` like
 ``torch.nn.functional.linear`` without bias, for at most 64 rows -- the
@@ -7,6 +8,12 @@ layers, tensorforge/model/layers.py:88-95, 144-146).  At that shape the
 product streams the weight matrix once and is HBM-bound; the kernel splits
 K across wavefronts so a launch has thousands of wavefronts streaming
 short weight slabs instead of a hundred walking all of K.
+
+``linear_partials(x, weight, splits)`` is the split-K form for 17..64 rows:
+each workgroup owns 64 output columns and one of ``splits`` slices of K, and
+writes the slice's fp32 partial product; ``linear_partials_sum`` (or a
+fused consumer) adds the slices and rounds once, which is the result of a
+GEMM with fp32 accumulation.
 """
 
 from __future__ import annotations
@@ -56,5 +63,77 @@ def linear_rows(x: Tensor, weight: Tensor, *, output: Tensor | None = None,
             _native.current_stream(x.device),
         ),
         "linear_rows",
+    )
+    return output
+
+
+def linear_partials_supported(x: Tensor, weight: Tensor) -> bool:
+    """Whether :func:`linear_partials` takes these operands."""
+
+    return linear_rows_supported(x, weight) and x.shape[1] > 0
+
+
+def default_splits(n: int, k: int) -> int:
+    """K slices for an [n, k] weight: enough 64-column x slice workgroups
+    (>= 256) to stream from every compute unit, slices of >= 256 k, and a
+    count that divides K / 32 into non-empty slices."""
+
+    steps = k // 32
+    tiles = (n + 63) // 64
+    want = max(1, min(-(-256 // tiles), max(1, k // 256)))
+    want = min(want, steps)
+    while want > 1 and -(-steps // -(-steps // want)) != want:
+        want -= 1
+    return want
+
+
+def linear_partials(x: Tensor, weight: Tensor, splits: int, *,
+                    partials: Tensor | None = None) -> Tensor:
+    """fp32 ``[splits, m, n]`` partial products of ``x [m, k] @ weight[n, k].T``
+    over ``splits`` contiguous slices of K (m <= 64, fp16/bf16)."""
+
+    if not _native.is_available():
+        raise RuntimeError(
+            "the gfx950 kernel library is unavailable; build it with "
+            "`python -m tensorforge_amd.build`"
+        )
+    if not linear_partials_supported(x, weight):
+        raise ValueError("linear_partials needs fp16/bf16 CUDA operands [m <= 64, k] and [n, k] "
+                         "with k % 32 == 0 and 16-byte aligned contiguous rows")
+    m, k = x.shape
+    n = weight.shape[0]
+    if partials is None:
+        partials = torch.empty((splits, m, n), dtype=torch.float32, device=x.device)
+    if (partials.shape != (splits, m, n) or partials.dtype != torch.float32
+            or partials.device != x.device or not partials.is_contiguous()):
+        raise ValueError("partials must be a contiguous fp32 [splits, m, n] tensor on x's device")
+    _native.check(
+        _native.library().tf_linear_partials(
+            x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), partials.data_ptr(),
+            m, n, k, splits, _native.dtype_code(x.dtype), _native.current_stream(x.device),
+        ),
+        "linear_partials",
+    )
+    return partials
+
+
+def linear_partials_sum(partials: Tensor, *, dtype: torch.dtype | None = None,
+                        output: Tensor | None = None) -> Tensor:
+    """``round(partials.sum(0))`` into fp16/bf16 rows (one rounding)."""
+
+    if partials.ndim != 3 or partials.dtype != torch.float32 or not partials.is_contiguous():
+        raise ValueError("partials must be a contiguous fp32 [splits, m, n] tensor")
+    splits, m, n = partials.shape
+    if output is None:
+        output = torch.empty((m, n), dtype=dtype or torch.bfloat16, device=partials.device)
+    if (output.shape != (m, n) or output.stride(1) != 1 or output.device != partials.device
+            or output.dtype not in (torch.float16, torch.bfloat16)):
+        raise ValueError("output must be fp16/bf16 [m, n] with contiguous rows on the same device")
+    _native.check(
+        _native.library().tf_linear_partials_sum(
+            partials.data_ptr(), splits, m, n, output.data_ptr(), output.stride(0),
+            _native.dtype_code(output.dtype), _native.current_stream(partials.device),
+        ),
+        "linear_partials_sum",
     )
     return output

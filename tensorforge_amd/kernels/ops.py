@@ -187,6 +187,52 @@ def residual_rms_norm(
     return residual_output, norm_output
 
 
+def residual_rms_norm_partials(
+    partials: Tensor,
+    residual: Tensor,
+    weight: Tensor,
+    eps: float = 1e-6,
+    *,
+    residual_output: Tensor | None = None,
+    norm_output: Tensor | None = None,
+) -> tuple[Tensor, Tensor]:
+    """:func:`residual_rms_norm` whose inputs are the rounded sum of fp32
+    split-K partials ``[splits, rows, columns]`` (``linear_partials``): the
+    projection's K-slice sum is fused into the norm's row read, so the
+    projection output is never written in the storage type."""
+
+    _require_library()
+    _validate_common(residual, weight)
+    if partials.dtype != torch.float32 or partials.ndim != 3 or not partials.is_contiguous():
+        raise ValueError("partials must be a contiguous fp32 [splits, rows, columns] tensor")
+    if partials.device != residual.device:
+        raise ValueError("partials must share the residual's device")
+    rows, columns = _norm_launch_shape(residual)
+    if partials.shape[1:] != (rows, columns):
+        raise ValueError("partials must be [splits, rows, columns] of the residual's rows")
+    if eps <= 0:
+        raise ValueError("eps must be positive")
+    residual_output = _output_or_empty(residual_output, residual, "residual_output")
+    norm_output = _output_or_empty(norm_output, residual, "norm_output")
+    _native.check(
+        _native.library().tf_residual_rms_norm_partials(
+            partials.data_ptr(),
+            partials.shape[0],
+            residual.data_ptr(),
+            weight.data_ptr(),
+            residual_output.data_ptr(),
+            norm_output.data_ptr(),
+            rows,
+            columns,
+            eps,
+            _native.dtype_code(residual.dtype),
+            _native.current_stream(residual.device),
+        ),
+        "residual_rms_norm_partials",
+    )
+    return residual_output, norm_output
+
+
 def swiglu(gate: Tensor, up: Tensor, *, output: Tensor | None = None) -> Tensor:
     """Fuse SiLU and gating after the two projections (reference: triton_ops.py:246-260)."""
 

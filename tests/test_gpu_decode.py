@@ -233,3 +233,26 @@ def test_head_dim_128_and_group_4_decoder(device):
             assert margin <= 2e-2 * float(row.abs().max()), (rid, step, margin)
             flips += int(margin > 0)
     assert flips <= 2
+
+
+def test_wide_bucket_split_k_projections_follow_the_oracle(device):
+    """A 32-lane bucket runs the output and down projections as split-K
+    partials summed inside the residual RMSNorm; 20 requests' greedy tokens
+    must still follow the oracle (at most two margin flips)."""
+
+    config = small_config()
+    weights = DecoderWeights.random(config, seed=1, dtype=torch.float16, device=device)
+    cache = _cache(config, device, pages=256, sequences=32)
+    rng = random.Random(3)
+    prompts = {f"w{i}": [rng.randrange(1024) for _ in range(rng.randrange(16, 120))]
+               for i in range(20)}
+    executor = BucketedDecodeExecutor(weights, cache, batch_buckets=(32,),
+                                      context_buckets=(256,))
+    bucket = executor.bucket(32, 256)
+    assert bucket.split_o >= 1 and bucket.split_down > 1
+    outputs = greedy_decode(executor, prompts, steps=8)
+    flips = 0
+    for rid, prompt in prompts.items():
+        assert len(outputs[rid]) == 8
+        flips += len(_greedy_mismatches(weights, prompt, outputs[rid]))
+    assert flips <= 2

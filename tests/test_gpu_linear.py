@@ -58,3 +58,57 @@ def test_linear_rows_rejects_unsupported_shapes(device):
     with pytest.raises(ValueError):
         linear_rows(x, w)
     assert not linear_rows_supported(x[:4, :48], w[:, :48])  # K % 32
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 17, 33, 64])
+@pytest.mark.parametrize(("n", "k", "splits"), [(2048, 2048, 8), (2048, 5632, 8), (2560, 2048, 7),
+                                                (100, 96, 3), (64, 32, 1), (11264, 2048, 2)])
+def test_linear_partials_sum_matches_fp32(device, dtype, rows, n, k, splits):
+    """Split-K partials summed and rounded once equal the fp32 product within
+    the storage type's bar; each partial is the product over its own K slice
+    (slices of ceil(K / 32 / splits) k-steps)."""
+
+    from tensorforge_amd.kernels import linear_partials, linear_partials_sum
+
+    generator = torch.Generator().manual_seed(rows * 7 + n + k + splits)
+    x = torch.randn(rows, k, generator=generator).to(dtype)
+    w = (torch.randn(n, k, generator=generator) * 0.02).to(dtype)
+    partials = linear_partials(x.to(device), w.to(device), splits)
+    steps = k // 32
+    per = -(-steps // splits) * 32
+    expected_partials = torch.stack([x[:, s * per:(s + 1) * per].float()
+                                     @ w[:, s * per:(s + 1) * per].float().T
+                                     for s in range(splits)])
+    scale = float(expected_partials.abs().max())
+    torch.testing.assert_close(partials.cpu(), expected_partials, rtol=1e-4, atol=1e-4 * scale)
+    out = linear_partials_sum(partials, dtype=dtype)
+    expected = x.float() @ w.float().T
+    tol = TOLERANCE[dtype]
+    torch.testing.assert_close(out.float().cpu(), expected, rtol=tol,
+                               atol=tol * float(expected.abs().max()))
+    # The row sum rounds the fp32 sum of the partials (summed in slice order).
+    running = partials[0].clone()
+    for s in range(1, splits):
+        running += partials[s]
+    assert torch.equal(out.cpu(), running.to(dtype).cpu())
+
+
+def test_linear_partials_strided_x_and_rejections(device):
+    from tensorforge_amd.kernels import linear_partials
+
+    generator = torch.Generator().manual_seed(5)
+    wide = torch.randn(40, 2048 + 64, generator=generator).to(torch.bfloat16).to(device)
+    x = wide[:, 64:]
+    w = (torch.randn(300, 2048, generator=generator) * 0.02).to(torch.bfloat16).to(device)
+    partials = linear_partials(x, w, 4)
+    expected = x.float() @ w.float().T
+    torch.testing.assert_close(partials.sum(0), expected, rtol=1e-3,
+                               atol=1e-3 * float(expected.abs().max()))
+    with pytest.raises(RuntimeError, match="splits"):
+        linear_partials(x, w, 65)  # more slices than k-steps
+    with pytest.raises(RuntimeError, match="non-empty"):
+        linear_partials(x[:, :160], w[:, :160], 4)  # 5 k-steps in slices of 2 fill only 3
+    with pytest.raises(ValueError):
+        linear_partials(torch.randn(65, 64, dtype=torch.bfloat16, device=device),
+                        w[:, :64], 1)

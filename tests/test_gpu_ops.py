@@ -191,3 +191,32 @@ def test_swiglu_gate_up_equals_separate_swiglu(device, dtype, rows, ffn, pad):
     swiglu_gate_up(gate_up[:, :2 * ffn + pad], output=wide[:, :ffn])
     assert_bit_exact(wide[:, :ffn], actual, "strided output")
     assert not wide[:, ffn:].any()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize(("rows", "columns", "splits"), [(64, 2048, 8), (17, 2048, 1), (5, 513, 3),
+                                                         (32, 4096, 11)])
+def test_residual_rms_norm_partials_equals_the_unfused_pair(device, dtype, rows, columns, splits):
+    """The fused form equals rounding the slice sum (summed in slice order)
+    and then running residual_rms_norm on it: the residual output bit for
+    bit; the norm within one rounding of the storage type, since the fused
+    form reduces the sum of squares over a different lane layout (one
+    vector per lane instead of two), which can move inv_rms by an fp32 ulp."""
+
+    from tensorforge_amd.kernels.ops import residual_rms_norm_partials
+
+    generator = torch.Generator().manual_seed(rows + columns + splits)
+    partials = torch.randn(splits, rows, columns, generator=generator).to(device)
+    residual = torch.randn(rows, columns, generator=generator).to(dtype).to(device)
+    weight = (1 + 0.1 * torch.randn(columns, generator=generator)).to(dtype).to(device)
+    running = partials[0].clone()
+    for s in range(1, splits):
+        running += partials[s]
+    inputs = running.to(dtype)
+    want_residual, want_norm = residual_rms_norm(inputs, residual, weight, 1e-5)
+    got_residual, got_norm = residual_rms_norm_partials(partials, residual, weight, 1e-5)
+    assert torch.equal(got_residual, want_residual)
+    ulp = {torch.float16: 2.0**-10, torch.bfloat16: 2.0**-7, torch.float32: 2.0**-22}[dtype]
+    torch.testing.assert_close(got_norm.float(), want_norm.float(), rtol=ulp, atol=1e-6)
+    with pytest.raises(ValueError, match="partials"):
+        residual_rms_norm_partials(partials[:, :, 1:], residual, weight, 1e-5)
