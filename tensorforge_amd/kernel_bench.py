@@ -206,7 +206,8 @@ def attention_ceiling(device: torch.device, calls: int) -> list[dict]:
                                            value_cache=value_cache,
                                            block_tables=gpu.block_tables,
                                            context_lengths=gpu.context_lengths,
-                                           scale=case.scale, max_context_length=2048,
+                                           scale=case.scale,
+                                           max_context_length=min(2048, width * block_size),
                                            output=output)
                 return
             _native.check(lib.tf_paged_gqa_decode(
