@@ -131,6 +131,34 @@ int32_t tf_paged_gqa_decode(
     int32_t flags, void *stream);
 
 /*
+ * tf_paged_gqa_decode fused with the decode step's RoPE and KV append
+ * (MFMA grid kernel only: bf16/fp16, head_dim 32/64/128, group <= 16,
+ * block_size % 16 == 0; no STREAM flag).  Row b of `qkv` (qkv_row_stride
+ * elements apart) holds [query heads | kv heads of k | kv heads of v],
+ * head_dim each, unrotated.  Each workgroup rotates its query group at
+ * positions[b] (half-split RoPE with the cos/sin tables [table_rows,
+ * head_dim], positions clamped into the table, fp32 math rounded once, as
+ * tf_rope_kv_append) and, when active_mask[b] != 0 and the slot
+ * (append_pages[b], append_offsets[b]) lies in the cache, writes the row's
+ * rotated k and its v into that slot before reading the row's tokens.
+ * context_lengths count the new token; everything else is as in
+ * tf_paged_gqa_decode.  Replaces the RoPE, cache write and attention of the
+ * decode step (model/layers.py:57-69; runtime/decode_bucket.py:448-469).
+ */
+int32_t tf_paged_gqa_decode_rope_append(
+    const void *qkv, int64_t qkv_row_stride, const int64_t *positions,
+    const void *cos_table, const void *sin_table, int32_t table_rows,
+    void *key_cache, void *value_cache, const int32_t *append_pages,
+    const int32_t *append_offsets, const int32_t *active_mask,
+    const int32_t *block_tables, const int32_t *context_lengths, void *output,
+    float *partial_max, float *partial_sum, float *partial_accumulator,
+    int32_t *split_counters, int64_t partial_capacity, int32_t partial_row_stride,
+    int32_t batch, int32_t query_heads, int32_t kv_heads, int32_t head_dim,
+    int32_t num_blocks, int32_t block_size, int32_t table_width,
+    int32_t split_size, int32_t num_splits, float scale, int32_t dtype,
+    int32_t flags, void *stream);
+
+/*
  * First stage of tf_paged_gqa_decode alone (num_splits >= 1): writes the
  * partials of every non-empty split.  Partial max values are base-2
  * logarithms of the unnormalised scores (score * scale * log2(e)).

@@ -52,6 +52,15 @@ SIGNATURES: dict[str, tuple[Any, ...]] = {
         _i32, _i32, _i32,  # num blocks, block size, table width
         _i32, _i32, _f32, _i32, _i32, _p,  # split size, splits, scale, dtype, flags, stream
     ),
+    "tf_paged_gqa_decode_rope_append": (
+        _p, _i64, _p, _p, _p, _i32,  # qkv, row stride, positions, cos, sin, table rows
+        _p, _p, _p, _p, _p,  # key/value cache, append pages, offsets, active mask
+        _p, _p, _p,  # tables, lengths, output
+        _p, _p, _p, _p, _i64, _i32,  # partials, counters, capacity, row stride
+        _i32, _i32, _i32, _i32,  # batch, query heads, kv heads, head dim
+        _i32, _i32, _i32,  # num blocks, block size, table width
+        _i32, _i32, _f32, _i32, _i32, _p,  # split size, splits, scale, dtype, flags, stream
+    ),
     "tf_paged_gqa_decode_partials": (
         _p, _p, _p, _p, _p,
         _p, _p, _p, _i64, _i32,

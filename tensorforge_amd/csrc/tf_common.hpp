@@ -69,6 +69,21 @@ __device__ __forceinline__ _Float16 from_float<_Float16>(float v) {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
+// Half-split rotary embedding of one pair (x1 = x[j], x2 = x[j + D/2], j < D/2):
+//   out[j]       = x1 cos[j]       - x2 sin[j]         (rope_lo)
+//   out[j + D/2] = x2 cos[j + D/2] + x1 sin[j + D/2]   (rope_hi)
+// with the fused multiply-adds written out, so every kernel that rotates
+// (the RoPE + append kernel and the attention kernel that rotates its own
+// query group) rounds identically.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float rope_lo(float x1, float x2, float c, float s) {
+  return __builtin_fmaf(x1, c, -(x2 * s));
+}
+__device__ __forceinline__ float rope_hi(float x1, float x2, float c, float s) {
+  return __builtin_fmaf(x2, c, x1 * s);
+}
+
+// ---------------------------------------------------------------------------
 // Wavefront (64-lane) reductions.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {

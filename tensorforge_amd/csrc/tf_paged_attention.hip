@@ -90,6 +90,20 @@ struct AttnParams {
   int32_t waves_per_head;  // MFMA grid kernel: wavefronts sharing one kv head
   int32_t tokens_per_wave; // MFMA grid kernel: > 0 uses ceil(tokens / this) of them per row
   float scale_log2;
+  // Fused RoPE + append (MFMA grid kernel, tf_paged_gqa_decode_rope_append):
+  // the query group is rotated from row b of `rope_qkv` ([q heads | k heads
+  // | v heads], head_dim each) instead of read from `query`, and the row's
+  // new token (rotated k, v) is written to its page slot before the row's
+  // tokens are read.  Null for the plain call.
+  const void *rope_qkv;
+  int64_t rope_row_stride;
+  const int64_t *rope_positions;
+  const void *rope_cos;
+  const void *rope_sin;
+  int32_t rope_table_rows;
+  const int32_t *append_pages;
+  const int32_t *append_offsets;
+  const int32_t *append_active;
 };
 
 __device__ __forceinline__ int32_t clamp_context(const AttnParams &p, int32_t b) {
@@ -446,7 +460,7 @@ constexpr int kSegmentTiles = 64;  // page-window capacity: 64 tiles = 1024 toke
 //            V[4q4 + e][16n + i] for e = 0..3.
 // Requires block_size % 16 == 0 and split_size % 32 == 0 (a tile never
 // straddles a page), so each tile's page is wave-uniform.
-template <typename T, int D, int NW>
+template <typename T, int D, int NW, bool ROPE>
 __global__ void __launch_bounds__(NW * 64)
 paged_decode_mfma_kernel(AttnParams p) {
   using M = Mfma<T>;
@@ -490,26 +504,85 @@ paged_decode_mfma_kernel(AttnParams p) {
     return logical < p.table_width ? table[logical] : -1;
   };
 
-  // Independent start-up loads: row length, query group, first page window.
+  // Independent start-up loads: row length, query group, first page window
+  // (the window first when the query group is rotated, whose arithmetic
+  // waits for its loads).
   const int32_t ctx = clamp_context(p, b);
+  int32_t page_win = ROPE ? load_window(0) : 0;
   vec8 qf[KS];  // B operand of the score MFMA: q[head l16][32ks + 8q4 .. +8]
+  constexpr int kHalf = D / 2;
+  // RoPE inputs of this row: the QKV row and the cos / sin rows of its position.
+  const T *rope_row = nullptr;
+  const T *rope_cs = nullptr;
+  const T *rope_sn = nullptr;
+  if constexpr (ROPE) {
+    rope_row = static_cast<const T *>(p.rope_qkv) + static_cast<int64_t>(b) * p.rope_row_stride;
+    int64_t pos = p.rope_positions[b];
+    pos = pos < 0 ? 0 : (pos >= p.rope_table_rows ? p.rope_table_rows - 1 : pos);
+    rope_cs = static_cast<const T *>(p.rope_cos) + pos * D;
+    rope_sn = static_cast<const T *>(p.rope_sin) + pos * D;
+  }
+  // 8 rotated elements [i0, i0 + 8) of the head at `src` (i0 a multiple of 8;
+  // the pair partner of element i is i + D/2 or i - D/2).
+  auto rotate8 = [&](const T *src, int i0) -> vec8 {
+    const int ip = i0 < kHalf ? i0 + kHalf : i0 - kHalf;
+    const vec8 x = *reinterpret_cast<const vec8 *>(src + i0);
+    const vec8 xp = *reinterpret_cast<const vec8 *>(src + ip);
+    const vec8 c = *reinterpret_cast<const vec8 *>(rope_cs + i0);
+    const vec8 sn = *reinterpret_cast<const vec8 *>(rope_sn + i0);
+    vec8 out;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float o = i0 < kHalf ? rope_lo(to_float(x[j]), to_float(xp[j]), to_float(c[j]), to_float(sn[j]))
+                                 : rope_hi(to_float(xp[j]), to_float(x[j]), to_float(c[j]), to_float(sn[j]));
+      out[j] = from_float<T>(o);
+    }
+    return out;
+  };
   {
-    const T *qrow = static_cast<const T *>(p.query) +
-                    (static_cast<int64_t>(b) * p.query_heads +
-                     static_cast<int64_t>(kvh) * p.group + l16) * D;
+    const int64_t head = static_cast<int64_t>(kvh) * p.group + l16;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      if (l16 < p.group)
-        qf[ks] = *reinterpret_cast<const vec8 *>(qrow + 32 * ks + 8 * q4);
-      else
+      if (l16 >= p.group) {
         qf[ks] = vec8{};
+      } else if constexpr (ROPE) {
+        qf[ks] = rotate8(rope_row + head * D, 32 * ks + 8 * q4);
+      } else {
+        const T *qrow = static_cast<const T *>(p.query) +
+                        (static_cast<int64_t>(b) * p.query_heads + head) * D;
+        qf[ks] = *reinterpret_cast<const vec8 *>(qrow + 32 * ks + 8 * q4);
+      }
     }
   }
-  int32_t page_win = load_window(0);
+  if constexpr (!ROPE) page_win = load_window(0);
 
   if (s0 >= ctx) {
     if (split == 0) zero_rows<T>(p, b, grp * HPW * p.group, HPW * p.group);
     return;
+  }
+  if constexpr (ROPE) {
+    // The row's new token: every wavefront that streams writes the same
+    // rotated k and v into the token's page slot (identical bytes) and
+    // waits for its own stores before its first K/V load, so whichever
+    // wavefront reads that slot sees the token.  Lanes [0, D/8) rotate 8
+    // key elements each, lanes [D/8, D/4) copy 8 value elements.
+    const int32_t page = p.append_pages[b];
+    const int32_t off = p.append_offsets[b];
+    const bool append = p.append_active[b] != 0 && page >= 0 && page < p.num_blocks && off >= 0 &&
+                        off < p.block_size;
+    if (append && lane < D / 4) {
+      const int64_t slot = ((static_cast<int64_t>(page) * p.block_size + off) * p.kv_heads + kvh) * D;
+      if (lane < D / 8) {
+        const vec8 k = rotate8(rope_row + static_cast<int64_t>(p.query_heads + kvh) * D, 8 * lane);
+        *reinterpret_cast<vec8 *>(static_cast<T *>(const_cast<void *>(p.key_cache)) + slot + 8 * lane) = k;
+      } else {
+        const int e0 = 8 * (lane - D / 8);
+        const vec8 v = *reinterpret_cast<const vec8 *>(
+            rope_row + static_cast<int64_t>(p.query_heads + p.kv_heads + kvh) * D + e0);
+        *reinterpret_cast<vec8 *>(static_cast<T *>(const_cast<void *>(p.value_cache)) + slot + e0) = v;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
   }
   const int32_t s1 = min(s0 + p.split_size, ctx);
   // Wavefronts of the head that take chunks of this row: all WPH, or with a
@@ -1641,8 +1714,12 @@ template <typename T, int D>
 void launch_mfma(const AttnParams &p, dim3 grid, hipStream_t stream) {
   const int waves = p.heads_per_wg * p.waves_per_head;
   const size_t lds = static_cast<size_t>(mfma_lds_bytes(D, waves));
-  hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves>), grid, dim3(waves * 64), lds,
-                     stream, p);
+  if (p.rope_qkv)
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves, true>), grid, dim3(waves * 64),
+                       lds, stream, p);
+  else
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves, false>), grid, dim3(waves * 64),
+                       lds, stream, p);
 }
 
 template <typename T>
@@ -1728,6 +1805,15 @@ int32_t make_params(AttnParams &p, const void *query, const void *key_cache,
   p.waves_per_head = 1;
   p.tokens_per_wave = 0;
   p.scale_log2 = scale * kLog2e;
+  p.rope_qkv = nullptr;
+  p.rope_row_stride = 0;
+  p.rope_positions = nullptr;
+  p.rope_cos = nullptr;
+  p.rope_sin = nullptr;
+  p.rope_table_rows = 0;
+  p.append_pages = nullptr;
+  p.append_offsets = nullptr;
+  p.append_active = nullptr;
   return TF_SUCCESS;
 }
 
@@ -1907,6 +1993,58 @@ extern "C" int32_t tf_paged_gqa_decode(
                               head_dim, num_blocks, block_size, table_width, split_size,
                               num_splits, scale, dtype))
     return s;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int32_t st = launch_split_stage(p, dtype, flags, s)) return st;
+  if (num_splits == 1 || split_counters != nullptr) return TF_SUCCESS;
+  return launch_merge(partial_max, partial_sum, partial_accumulator, context_lengths, output,
+                      batch, query_heads, head_dim, split_size, num_splits, partial_row_stride,
+                      p.max_tokens, dtype, s);
+}
+
+extern "C" int32_t tf_paged_gqa_decode_rope_append(
+    const void *qkv, int64_t qkv_row_stride, const int64_t *positions, const void *cos_table,
+    const void *sin_table, int32_t table_rows, void *key_cache, void *value_cache,
+    const int32_t *append_pages, const int32_t *append_offsets, const int32_t *active_mask,
+    const int32_t *block_tables, const int32_t *context_lengths, void *output,
+    float *partial_max, float *partial_sum, float *partial_accumulator,
+    int32_t *split_counters, int64_t partial_capacity, int32_t partial_row_stride, int32_t batch,
+    int32_t query_heads, int32_t kv_heads, int32_t head_dim, int32_t num_blocks,
+    int32_t block_size, int32_t table_width, int32_t split_size, int32_t num_splits, float scale,
+    int32_t dtype, int32_t flags, void *stream) {
+  using namespace tf;
+  clear_error();
+  if (batch > 0 && !output) return fail(TF_ERROR_INVALID_ARGUMENT, "null output pointer");
+  if (table_rows <= 0 || (head_dim & 1))
+    return fail(TF_ERROR_INVALID_ARGUMENT, "table rows must be positive and head_dim even");
+  if (qkv_row_stride < static_cast<int64_t>(query_heads + 2 * kv_heads) * head_dim)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "qkv row stride is shorter than the q, k, v heads");
+  if (batch > 0 && (!qkv || !positions || !cos_table || !sin_table || !append_pages ||
+                    !append_offsets || !active_mask))
+    return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  if (choose_variant(dtype, head_dim, query_heads / (kv_heads > 0 ? kv_heads : 1), block_size,
+                     flags) != TF_ATTENTION_MFMA ||
+      (flags & TF_ATTENTION_FLAG_STREAM) || (num_splits > 1 && split_size % 32 != 0))
+    return fail(TF_ERROR_UNSUPPORTED,
+                "fused RoPE + append attention needs the MFMA grid kernel (bf16/fp16, head_dim "
+                "32/64/128, group <= 16, block_size % 16 == 0, split_size % 32 == 0)");
+  AttnParams p;
+  // `qkv` stands in for the query pointer in the common validation.
+  if (int32_t st = make_params(p, qkv, key_cache, value_cache, block_tables, context_lengths,
+                               output, partial_max, partial_sum, partial_accumulator,
+                               split_counters, partial_capacity, partial_row_stride, batch,
+                               query_heads, kv_heads, head_dim, num_blocks, block_size,
+                               table_width, split_size, num_splits, scale, dtype))
+    return st;
+  p.query = nullptr;
+  p.rope_qkv = qkv;
+  p.rope_row_stride = qkv_row_stride;
+  p.rope_positions = positions;
+  p.rope_cos = cos_table;
+  p.rope_sin = sin_table;
+  p.rope_table_rows = table_rows;
+  p.append_pages = append_pages;
+  p.append_offsets = append_offsets;
+  p.append_active = active_mask;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (int32_t st = launch_split_stage(p, dtype, flags, s)) return st;
   if (num_splits == 1 || split_counters != nullptr) return TF_SUCCESS;

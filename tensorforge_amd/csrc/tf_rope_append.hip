@@ -63,8 +63,8 @@ rope_kv_append_kernel(const T *__restrict__ qkv, int64_t row_stride,
     const T *src = row + static_cast<int64_t>(head) * head_dim;
     const float x1 = to_float(src[j]);
     const float x2 = to_float(src[j + half]);
-    const float o1 = x1 * to_float(cs[j]) - x2 * to_float(sn[j]);
-    const float o2 = x2 * to_float(cs[j + half]) + x1 * to_float(sn[j + half]);
+    const float o1 = rope_lo(x1, x2, to_float(cs[j]), to_float(sn[j]));
+    const float o2 = rope_hi(x1, x2, to_float(cs[j + half]), to_float(sn[j + half]));
     const T r1 = from_float<T>(o1);
     const T r2 = from_float<T>(o2);
     if (head < query_heads) {

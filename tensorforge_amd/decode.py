@@ -6,9 +6,10 @@ sequences runs as ONE captured HIP graph.  Per layer:
 
 * ``rms_norm`` (first layer) or the fused ``residual_rms_norm``;
 * one fused QKV projection;
-* ``rope_paged_kv_append``: RoPE on q and k, and k, v into their pages;
-* ``paged_gqa_decode_attention`` (one pass for wide buckets, split-KV
-  with its merge otherwise);
+* RoPE on q and k, k and v into their pages, and
+  ``paged_gqa_decode_attention`` (one pass for wide buckets, split-KV with
+  its merge otherwise) -- one fused launch where the MFMA attention kernel
+  serves the geometry, else ``rope_paged_kv_append`` then attention;
 * the output projection;
 * ``residual_rms_norm`` of (attention output, residual);
 * one fused gate|up projection, ``swiglu_gate_up``, the down projection.
@@ -39,6 +40,7 @@ from torch import Tensor
 from torch.nn import functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
+from tensorforge_amd import _native
 from tensorforge_amd.cache import AppendReservation, PagedKVCache
 from tensorforge_amd.kernels import (
     PagedAttentionWorkspace,
@@ -51,7 +53,10 @@ from tensorforge_amd.kernels import (
     rope_paged_kv_append,
     swiglu_gate_up,
 )
-from tensorforge_amd.kernels.attention import set_attention_split_size
+from tensorforge_amd.kernels.attention import (
+    paged_gqa_decode_attention_rope_append,
+    set_attention_split_size,
+)
 from tensorforge_amd.kernels.linear import default_splits, linear_partials_supported
 from tensorforge_amd.kernels.ops import residual_rms_norm_partials
 
@@ -240,6 +245,11 @@ class DecodeGraphBucket:
                                          device=device)
         self.logits = torch.empty((b, config.vocab_size), dtype=dtype, device=device)
         self.next_tokens = self.token_state[:b]
+        # RoPE, the KV append and attention in one launch where the MFMA
+        # attention kernel serves the geometry.
+        self.fused_rope = _native.library().tf_paged_gqa_decode_variant(
+            _native.dtype_code(dtype), d, hq // hkv, cache.config.block_size,
+            0) == _native.TF_ATTENTION_MFMA
         # Output and down projections at 17..64 rows: split-K partials whose
         # K-slice sum is fused into the residual RMSNorm that consumes them.
         self.split_o = self.split_down = 0
@@ -377,16 +387,26 @@ class DecodeGraphBucket:
                 qkv = _project(h, layer.qkv)
                 key_cache = self.cache.key_cache[index]
                 value_cache = self.cache.value_cache[index]
-                # RoPE on q and k, k and v into their pages: one launch.
-                q = rope_paged_kv_append(qkv, self.positions, self.weights.rope_cos,
-                                         self.weights.rope_sin, key_cache, value_cache,
-                                         self.physical_blocks, self.block_offsets,
-                                         self.active_mask, query_heads=hq,
-                                         query_output=self.query)
-                paged_gqa_decode_attention(
-                    q, key_cache, value_cache, self.block_tables, self.context_lengths,
-                    scale=d ** -0.5, max_context_length=self.context_capacity,
-                    output=self.attention_output, workspace=self.workspace)
+                if self.fused_rope:
+                    # RoPE, k and v into their pages, and attention: one launch.
+                    paged_gqa_decode_attention_rope_append(
+                        qkv, self.positions, self.weights.rope_cos, self.weights.rope_sin,
+                        key_cache, value_cache, self.physical_blocks, self.block_offsets,
+                        self.active_mask, self.block_tables, self.context_lengths,
+                        query_heads=hq, max_context_length=self.context_capacity,
+                        output=self.attention_output, workspace=self.workspace,
+                        scale=d ** -0.5)
+                else:
+                    # RoPE on q and k, k and v into their pages: one launch.
+                    q = rope_paged_kv_append(qkv, self.positions, self.weights.rope_cos,
+                                             self.weights.rope_sin, key_cache, value_cache,
+                                             self.physical_blocks, self.block_offsets,
+                                             self.active_mask, query_heads=hq,
+                                             query_output=self.query)
+                    paged_gqa_decode_attention(
+                        q, key_cache, value_cache, self.block_tables, self.context_lengths,
+                        scale=d ** -0.5, max_context_length=self.context_capacity,
+                        output=self.attention_output, workspace=self.workspace)
                 attention = self.attention_output.view(b, hq * d)
                 if self.split_o:
                     linear_partials(attention, layer.o_proj, self.split_o,

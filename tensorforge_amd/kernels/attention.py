@@ -409,6 +409,101 @@ def paged_gqa_decode_attention(
     return output
 
 
+def paged_gqa_decode_attention_rope_append(
+    qkv: Tensor,
+    positions: Tensor,
+    cos_table: Tensor,
+    sin_table: Tensor,
+    key_cache: Tensor,
+    value_cache: Tensor,
+    append_pages: Tensor,
+    append_offsets: Tensor,
+    active_mask: Tensor,
+    block_tables: Tensor,
+    context_lengths: Tensor,
+    *,
+    query_heads: int,
+    max_context_length: int,
+    output: Tensor,
+    workspace: PagedAttentionWorkspace,
+    scale: float | None = None,
+) -> Tensor:
+    """The decode step's RoPE, KV append and attention in one launch.
+
+    ``qkv [batch, (query_heads + 2 * kv_heads) * head_dim]`` holds the
+    unrotated projections (rows may be strided).  Each attention workgroup
+    rotates its query group at ``positions`` and writes the row's rotated
+    key and its value into slot (``append_pages``, ``append_offsets``) when
+    ``active_mask`` is set, then attends over ``context_lengths`` tokens
+    (which count the new one).  The same results as
+    :func:`tensorforge_amd.kernels.rope_paged_kv_append` followed by
+    :func:`paged_gqa_decode_attention` (the rotation is computed by the same
+    arithmetic); the plan (one pass or split-KV) is chosen as there.
+    Replaces the decode step's RoPE (model/layers.py:57-69), cache write and
+    attention call (runtime/decode_bucket.py:448-469).
+    """
+
+    if not _native.is_available():
+        raise RuntimeError(
+            "the gfx950 attention library is unavailable; build it with "
+            "`python -m tensorforge_amd.build`"
+        )
+    tensors = (qkv, positions, cos_table, sin_table, key_cache, value_cache, append_pages,
+               append_offsets, active_mask, block_tables, context_lengths, output)
+    if any(not tensor.is_cuda for tensor in tensors):
+        raise ValueError("paged GQA attention requires CUDA tensors")
+    if qkv.ndim != 2 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be [batch, (q + 2 kv heads) * head_dim] with contiguous rows")
+    if key_cache.ndim != 4 or value_cache.shape != key_cache.shape:
+        raise ValueError("key/value cache must share [blocks, block_size, kv_heads, head_dim]")
+    num_blocks, block_size, kv_heads, head_dim = key_cache.shape
+    batch = qkv.shape[0]
+    if qkv.shape[1] != (query_heads + 2 * kv_heads) * head_dim or query_heads % kv_heads:
+        raise ValueError("qkv rows must hold query_heads + 2 * kv_heads heads of head_dim")
+    if qkv.dtype not in (torch.float16, torch.bfloat16) or any(
+            t.dtype != qkv.dtype for t in (key_cache, value_cache, cos_table, sin_table, output)):
+        raise TypeError("fused RoPE attention takes fp16/bf16 qkv, tables, caches and output")
+    if positions.dtype != torch.int64 or positions.shape != (batch,):
+        raise ValueError("positions must be int64 [batch]")
+    if cos_table.shape != sin_table.shape or cos_table.ndim != 2 or cos_table.shape[1] != head_dim:
+        raise ValueError("cos/sin tables must be [positions, head_dim]")
+    for name, tensor in (("append_pages", append_pages), ("append_offsets", append_offsets),
+                         ("active_mask", active_mask), ("context_lengths", context_lengths)):
+        if tensor.dtype != torch.int32 or tensor.shape != (batch,):
+            raise ValueError(f"{name} must be int32 [batch]")
+    if block_tables.dtype != torch.int32 or block_tables.ndim != 2 or block_tables.shape[0] != batch:
+        raise ValueError("block_tables must be int32 with one row per query")
+    if output.shape != (batch, query_heads, head_dim) or not output.is_contiguous():
+        raise ValueError("output must be a contiguous [batch, query_heads, head_dim] tensor")
+    table_width = block_tables.shape[1]
+    context_capacity = table_width * block_size
+    if max_context_length <= 0 or max_context_length > context_capacity:
+        raise ValueError("max_context_length must be positive and within table capacity")
+    plan = attention_plan(max_context_length, batch, kv_heads, context_capacity)
+    head_bucket = _next_power_of_2(head_dim)
+    partial_programs = batch * query_heads * plan.num_splits
+    capacity = min(workspace.partial_max.numel(), workspace.partial_sum.numel(),
+                   workspace.partial_accumulator.shape[0])
+    if not plan.one_pass and (capacity < partial_programs
+                              or workspace.partial_accumulator.shape[1] != head_bucket):
+        raise ValueError("split-KV workspace has insufficient or incompatible capacity")
+    _native.check(
+        _native.library().tf_paged_gqa_decode_rope_append(
+            qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), cos_table.data_ptr(),
+            sin_table.data_ptr(), cos_table.shape[0], key_cache.data_ptr(),
+            value_cache.data_ptr(), append_pages.data_ptr(), append_offsets.data_ptr(),
+            active_mask.data_ptr(), block_tables.data_ptr(), context_lengths.data_ptr(),
+            output.data_ptr(), workspace.partial_max.data_ptr(), workspace.partial_sum.data_ptr(),
+            workspace.partial_accumulator.data_ptr(), None, capacity, head_bucket, batch,
+            query_heads, kv_heads, head_dim, num_blocks, block_size, table_width,
+            plan.split_size, plan.num_splits, head_dim**-0.5 if scale is None else scale,
+            _native.dtype_code(qkv.dtype), plan.flags, _native.current_stream(qkv.device),
+        ),
+        "paged_gqa_decode_attention_rope_append",
+    )
+    return output
+
+
 def selected_attention_autotune_config() -> dict[str, Any] | None:
     """Dispatch record of the last call (reference: triton_attention.py:521-522)."""
 
