@@ -33,6 +33,7 @@
  *                            runtime/decode_bucket.py:441-447, 470, 500-505)
  *   tf_linear_partials,      the same projections at 17..64 rows, split over
  *   tf_linear_partials_sum   K into fp32 partials and their row sum
+ *   tf_prefill_attention     prefill's causal attention (runtime/prefill.py:84-88, 109-118)
  */
 #ifndef TENSORFORGE_AMD_H_
 #define TENSORFORGE_AMD_H_
@@ -348,6 +349,26 @@ int32_t tf_linear_partials(const void *x, int64_t x_row_stride, const void *weig
 int32_t tf_linear_partials_sum(const float *partials, int32_t splits, int32_t m,
                                int32_t n, void *y, int64_t y_row_stride,
                                int32_t dtype, void *stream);
+
+/*
+ * Causal GQA attention over packed prompts (prefill).  Token rows:
+ *   q [T, query_heads * head_dim], k and v [T, kv_heads * head_dim] (row
+ *   strides in elements), output [T, query_heads * head_dim].
+ * tiles [num_tiles][3] int32: (first query token i0, prompt start s, prompt
+ * end e) of each 16-token query tile, s <= i0 < e, i0 - s a multiple of 16;
+ * the tile's tokens [i0, min(i0 + 16, e)) attend to [s, token] of their
+ * prompt.  Heaviest tiles first runs best.  fp16/bf16, head_dim 32/64/128,
+ * groups of 1..16 query heads per kv head; heads_per_wave (0: default)
+ * picks how many of a group's heads one wavefront serves.  Replaces the
+ * masked SDPA of prefill (runtime/prefill.py:84-88, 109-118).
+ */
+int32_t tf_prefill_attention(const void *q, int64_t q_row_stride, const void *k,
+                             int64_t k_row_stride, const void *v, int64_t v_row_stride,
+                             void *output, int64_t output_row_stride,
+                             const int32_t *tiles, int32_t num_tiles,
+                             int32_t query_heads, int32_t kv_heads, int32_t head_dim,
+                             float scale, int32_t heads_per_wave, int32_t dtype,
+                             void *stream);
 
 #ifdef __cplusplus
 }

@@ -59,6 +59,11 @@ from tensorforge_amd.kernels.attention import (
 )
 from tensorforge_amd.kernels.linear import default_splits, linear_partials_supported
 from tensorforge_amd.kernels.ops import residual_rms_norm_partials
+from tensorforge_amd.kernels.prefill import (
+    prefill_attention,
+    prefill_attention_supported,
+    prefill_tiles,
+)
 
 
 @dataclass(frozen=True, slots=True)
@@ -475,9 +480,10 @@ def prefill_batch(weights: DecoderWeights, cache: PagedKVCache,
     one [total, H] stream with no padding: every projection is one GEMM over
     all tokens, and one rope_paged_kv_append launch per layer rotates q and k
     of every token and writes k, v straight into the pages each token's
-    position maps to.  Attention runs per prompt through torch's fused
-    causal SDPA.  All reservations commit together, or roll back together on
-    an error.
+    position maps to.  Attention is one packed causal launch per layer over
+    all prompts (prefill_attention; torch's fused causal SDPA per prompt for
+    geometries that kernel does not serve).  All reservations commit
+    together, or roll back together on an error.
     """
 
     if not prompts:
@@ -512,6 +518,9 @@ def prefill_batch(weights: DecoderWeights, cache: PagedKVCache,
             ints[1, lo:hi] = positions % block_size
         longs_dev = torch.from_numpy(longs).to(device)
         ints_dev = torch.from_numpy(ints).to(device)
+        packed_attention = prefill_attention_supported(weights.embedding.dtype, hq, hkv, d)
+        if packed_attention:
+            tiles = torch.from_numpy(prefill_tiles(lengths)).to(device)
         tokens, positions_dev = longs_dev[0], longs_dev[1]
         eps = config.rms_norm_eps
         residual = F.embedding(tokens, weights.embedding)
@@ -525,10 +534,15 @@ def prefill_batch(weights: DecoderWeights, cache: PagedKVCache,
                                  cache.key_cache[index], cache.value_cache[index], ints_dev[0],
                                  ints_dev[1], ints_dev[2], query_heads=hq, query_output=q,
                                  key_output=k)
-            v = qkv[:, (hq + hkv) * d:].view(total, hkv, d)
-            for i in range(len(request_ids)):
-                lo, hi = int(bounds[i]), int(bounds[i + 1])
-                context[lo:hi] = _causal_attention(q[lo:hi], k[lo:hi], v[lo:hi], d ** -0.5)
+            if packed_attention:  # every prompt's causal attention in one launch
+                prefill_attention(q.view(total, hq * d), k.view(total, hkv * d),
+                                  qkv[:, (hq + hkv) * d:], tiles, query_heads=hq,
+                                  kv_heads=hkv, scale=d ** -0.5, output=context)
+            else:
+                v = qkv[:, (hq + hkv) * d:].view(total, hkv, d)
+                for i in range(len(request_ids)):
+                    lo, hi = int(bounds[i]), int(bounds[i + 1])
+                    context[lo:hi] = _causal_attention(q[lo:hi], k[lo:hi], v[lo:hi], d ** -0.5)
             attn = F.linear(context, layer.o_proj)
             residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps)
             act = swiglu_gate_up(F.linear(h, layer.gate_up))
