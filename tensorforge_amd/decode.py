@@ -164,11 +164,14 @@ def _project(x: Tensor, weight: Tensor, output: Tensor | None = None) -> Tensor:
     """x @ weight.T for a decode step.  Up to 16 rows, the K-split MFMA kernel
     (linear_rows) streams small weights (<= 8M elements: the q/k/v and o
     projections of TinyLlama) and the LM head faster than the library GEMM,
-    which launches too few workgroups for them; otherwise hipBLASLt (measured
-    on MI355X at the TinyLlama shapes)."""
+    which launches too few workgroups for them, and up to 8 rows also the
+    stacked gate|up weight (11264 x 2048: 11.4-12.6 us against 13.8);
+    otherwise hipBLASLt (measured on MI355X at the TinyLlama shapes)."""
 
-    rows_kernel = (x.shape[0] <= 16 and linear_rows_supported(x, weight)
-                   and (weight.numel() <= 8 * 1024 * 1024 or weight.shape[0] >= 16384))
+    rows = x.shape[0]
+    rows_kernel = (rows <= 16 and linear_rows_supported(x, weight)
+                   and (weight.numel() <= 8 * 1024 * 1024 or weight.shape[0] >= 16384
+                        or (rows <= 8 and weight.shape[0] >= 8192)))
     if rows_kernel:
         return linear_rows(x, weight, output=output)
     if output is None:
@@ -255,11 +258,17 @@ class DecodeGraphBucket:
         self.fused_rope = _native.library().tf_paged_gqa_decode_variant(
             _native.dtype_code(dtype), d, hq // hkv, cache.config.block_size,
             0) == _native.TF_ATTENTION_MFMA
-        # Output and down projections at 17..64 rows: split-K partials whose
-        # K-slice sum is fused into the residual RMSNorm that consumes them.
+        # Output and down projections at up to 64 rows: split-K partials
+        # whose K-slice sum is fused into the residual RMSNorm that consumes
+        # them (measured faster than linear_rows and hipBLASLt at 1..64 rows
+        # for the TinyLlama o and down shapes; at up to 16 rows only for
+        # weights of >= 1M elements -- smaller ones make too few 64-column
+        # workgroups and stay on linear_rows).
         self.split_o = self.split_down = 0
-        if 16 < b <= 64 and dtype in (torch.float16, torch.bfloat16):
-            layer0 = weights.layers[0]
+        layer0 = weights.layers[0]
+        large = min(layer0.o_proj.numel(), layer0.down.numel()) >= 1024 * 1024
+        if (b <= 64 and (b > 16 or large)
+                and dtype in (torch.float16, torch.bfloat16)):
             probe_o = torch.empty((b, hq * d), dtype=dtype, device=device)
             probe_d = torch.empty((b, config.intermediate_size), dtype=dtype, device=device)
             if (linear_partials_supported(probe_o, layer0.o_proj)
