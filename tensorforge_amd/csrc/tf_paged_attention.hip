@@ -448,8 +448,11 @@ constexpr float kRescaleThreshold = 8.f;
 constexpr int kSegmentTiles = 64;  // page-window capacity: 64 tiles = 1024 tokens
 
 // Wave-level layout of one 32-token chunk (tiles j = 0, 1 of 16 tokens):
-//   loads    lane (l16, q4) holds K/V of token 16j + l16, head_dim elements
-//            [32ks + 8q4, +8) -- the A operand of the score MFMA;
+//   loads    LINES: lane holds bytes [16 (lane % (D/8)), +16) of the K / V
+//            slice of token 16j + lane / (D/8) + (512/D) ks (whole token
+//            rows), and K is staged in LDS and read back in the A-operand
+//            layout; otherwise lane (l16, q4) loads K / V of token 16j + l16,
+//            head_dim elements [32ks + 8q4, +8) -- the A operand directly;
 //   scores   lane holds S[token 16j + 4q4 + r][head l16], r = 0..3;
 //   P        B operand of the P.V MFMA, k = 8q4 + i <-> token 4q4 + i of
 //            tile 0 (i < 4) or 4q4 + i - 4 of tile 1 (i >= 4);
@@ -460,7 +463,7 @@ constexpr int kSegmentTiles = 64;  // page-window capacity: 64 tiles = 1024 toke
 //            V[4q4 + e][16n + i] for e = 0..3.
 // Requires block_size % 16 == 0 and split_size % 32 == 0 (a tile never
 // straddles a page), so each tile's page is wave-uniform.
-template <typename T, int D, int NW, bool ROPE>
+template <typename T, int D, int NW, bool ROPE, bool LINES>
 __global__ void __launch_bounds__(NW * 64)
 paged_decode_mfma_kernel(AttnParams p) {
   using M = Mfma<T>;
@@ -599,8 +602,20 @@ paged_decode_mfma_kernel(AttnParams p) {
   const unsigned char *kbytes = static_cast<const unsigned char *>(p.key_cache);
   const unsigned char *vbytes = static_cast<const unsigned char *>(p.value_cache);
   const int64_t head_bytes = static_cast<int64_t>(kvh) * D * sizeof(T);
+  // Operand-layout loads: lane (l16, q4) reads 16 bytes of token l16.
   const uint32_t lane_full = static_cast<uint32_t>(l16) * token_bytes + 16u * q4;
   const uint32_t lane_first = 16u * q4;  // stand-in row for absent tokens
+  // LINES: K and V pass through LDS, so their loads need not follow the
+  // MFMA operand layout: D/8 lanes cover one token's head slice and one
+  // load covers 512/D whole tokens (whole cache lines), where a load in
+  // operand layout touches 16 tokens with half a line each.  A compute
+  // unit issues loads of fewer lines faster (its ceiling rises from about
+  // 36 to 55 GB/s), at the price of an LDS round trip for K on every
+  // chunk: the form for several wavefronts per kv head.
+  constexpr int kVLanes = D / 8;
+  constexpr int kVTokens = 64 / kVLanes;
+  const int v_tok = lane / kVLanes;  // token of load ks: v_tok + kVTokens * ks
+  const uint32_t v_piece = 16u * static_cast<uint32_t>(lane % kVLanes);
 
   f32x4 acc[NB];
 #pragma unroll
@@ -632,13 +647,36 @@ paged_decode_mfma_kernel(AttnParams p) {
       const uint32_t lane_off = l16 < ntok ? lane_full : lane_first;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        kf[j][ks] = *reinterpret_cast<const vec8 *>(kbytes + tile_off + lane_off + 64 * ks);
-        vf[j][ks] = *reinterpret_cast<const vec8 *>(vbytes + tile_off + lane_off + 64 * ks);
+        const int tt = v_tok + kVTokens * ks;
+        const uint32_t t_off =
+            LINES ? (tt < ntok ? static_cast<uint32_t>(tt) * token_bytes : 0u) + v_piece
+                  : lane_off + 64u * ks;
+        kf[j][ks] = *reinterpret_cast<const vec8 *>(kbytes + tile_off + t_off);
+        vf[j][ks] = *reinterpret_cast<const vec8 *>(vbytes + tile_off + t_off);
       }
     }
   };
 
   auto compute = [&](vec8(&kf)[2][KS], vec8(&vf)[2][KS], const uint32_t(&valid)[2]) {
+    if constexpr (LINES) {
+      // Stage K token-major in the wavefront's LDS tile and read it back in
+      // the A-operand layout; the V tile below reuses the same bytes (the
+      // wavefront's LDS requests are served in order).
+      __asm__ volatile("" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          *reinterpret_cast<vec8 *>(vt + (16 * j + v_tok + kVTokens * ks) * kRow + v_piece) = kf[j][ks];
+      __asm__ volatile("" ::: "memory");
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          kf[j][ks] =
+              *reinterpret_cast<const vec8 *>(vt + (16 * j + l16) * kRow + (32 * ks + 8 * q4) * 2);
+      __asm__ volatile("" ::: "memory");
+    }
     float sc[8];  // raw q.k of token 16j + 4q4 + r, head l16
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -657,11 +695,12 @@ paged_decode_mfma_kernel(AttnParams p) {
       // Stand-in V rows of absent tokens are cleared so that 0 * (non-finite)
       // cannot leak into the accumulator.
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const bool mine = (valid[j] >> l16) & 1u;
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) vf[j][ks] = mine ? vf[j][ks] : vec8{};
-      }
+        for (int ks = 0; ks < KS; ++ks) {
+          const bool mine = (valid[j] >> (LINES ? v_tok + kVTokens * ks : l16)) & 1u;
+          vf[j][ks] = mine ? vf[j][ks] : vec8{};
+        }
     }
     float mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
                      fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
@@ -689,15 +728,18 @@ paged_decode_mfma_kernel(AttnParams p) {
     }
     l_run += psum;
 
-    // Stage V token-major (one 16-byte LDS write per load), then read V^T
-    // fragments with the transpose read.  LDS requests of one wavefront are
-    // served in order, so compiler barriers are the only ordering needed.
+    // Stage V token-major (one 16-byte LDS write per load, each to its
+    // token's row), then read V^T fragments with the transpose read.  LDS
+    // requests of one wavefront are served in order, so compiler barriers
+    // are the only ordering needed.
     __asm__ volatile("" ::: "memory");
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        *reinterpret_cast<vec8 *>(vt + (16 * j + l16) * kRow + (32 * ks + 8 * q4) * 2) = vf[j][ks];
+        *reinterpret_cast<vec8 *>(
+            vt + (LINES ? (16 * j + v_tok + kVTokens * ks) * kRow + v_piece
+                        : (16 * j + l16) * kRow + (32 * ks + 8 * q4) * 2)) = vf[j][ks];
     __asm__ volatile("" ::: "memory");
     const unsigned char *rd = vt + (4 * q4 + (l16 >> 2)) * kRow + (l16 & 3) * 8;
 #pragma unroll
@@ -1696,7 +1738,7 @@ constexpr int kMfmaWaves = 8;
 // wavefront (flag bits 24-30) a row uses only as many of the WPH as its
 // length needs.  Without flags: one wavefront per (row, kv head, split),
 // the fastest split-KV form.  The host plan of the Python entry point asks
-// for one pass with WPH = ceil(L / 768) and a 768-token budget for wide
+// for one pass with WPH = ceil(L / 576) and a 576-token budget for wide
 // batches (bits 20-23 / 8-15 / 24-30; HPW must divide kv_heads).
 void mfma_geometry(AttnParams &p, int32_t flags) {
   int32_t hpw = 1;
@@ -1710,16 +1752,28 @@ void mfma_geometry(AttnParams &p, int32_t flags) {
   p.tokens_per_wave = ((flags >> TF_ATTENTION_TOKENS_PER_WAVE_SHIFT) & 0x7f) * 64;
 }
 
-template <typename T, int D>
-void launch_mfma(const AttnParams &p, dim3 grid, hipStream_t stream) {
+// Whole-row loads (LINES) when several wavefronts stream one kv head: there
+// a compute unit's load issue rate bounds the longest rows.  One wavefront
+// per (row, kv head, split) is latency-bound and keeps the operand-layout
+// loads, which need no LDS round trip for K.
+template <typename T, int D, bool ROPE>
+void launch_mfma_form(const AttnParams &p, dim3 grid, hipStream_t stream) {
   const int waves = p.heads_per_wg * p.waves_per_head;
   const size_t lds = static_cast<size_t>(mfma_lds_bytes(D, waves));
-  if (p.rope_qkv)
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves, true>), grid, dim3(waves * 64),
-                       lds, stream, p);
+  if (p.waves_per_head > 1)
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves, ROPE, true>), grid,
+                       dim3(waves * 64), lds, stream, p);
   else
-    hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves, false>), grid, dim3(waves * 64),
-                       lds, stream, p);
+    hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, kMfmaWaves, ROPE, false>), grid,
+                       dim3(waves * 64), lds, stream, p);
+}
+
+template <typename T, int D>
+void launch_mfma(const AttnParams &p, dim3 grid, hipStream_t stream) {
+  if (p.rope_qkv)
+    launch_mfma_form<T, D, true>(p, grid, stream);
+  else
+    launch_mfma_form<T, D, false>(p, grid, stream);
 }
 
 template <typename T>

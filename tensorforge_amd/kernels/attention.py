@@ -139,8 +139,10 @@ def attention_split_size_for(max_context_length: int, batch: int, kv_heads: int)
 # 2k contexts, 4 kv heads: 48 rows 20.5 us one pass vs 21.7 split; 32 rows
 # 18.7 vs 16.1).
 ONE_PASS_MIN_WORKGROUPS = 192
-# Tokens per wavefront that set the one-pass wavefronts per kv head.
-ONE_PASS_TOKENS_PER_WAVE = 768
+# Tokens per wavefront that set the one-pass wavefronts per kv head (swept
+# on MI355X at config 2, three seeds: 576 with up to 4 wavefronts per 2k row
+# beats 448 / 512 / 640 and the 768 / 3 of the operand-layout loads).
+ONE_PASS_TOKENS_PER_WAVE = 576
 
 
 @dataclass(frozen=True, slots=True)
@@ -156,7 +158,7 @@ class AttentionPlan:
 
     @property
     def flags(self) -> int:
-        """Several wavefronts per kv head, each row using one per 768 of its
+        """Several wavefronts per kv head, each row using one per 576 of its
         tokens (so short rows leave the memory system to the long ones)."""
 
         if self.waves_per_head <= 1:
@@ -176,7 +178,7 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
     (attention_split_size_for), a call runs one pass when its context fits
     one partition, or when it has at least 192 (row, kv head) workgroups and
     the partition size was not fixed by the caller: each workgroup then
-    splits its row over ceil(L / 768) (at most 8) wavefronts that combine in
+    splits its row over ceil(L / 576) (at most 8) wavefronts that combine in
     LDS, with no partials and no merge launch (measured on MI355X at
     72 rows x 4 kv heads x 2k: 23.1 us against 26.0 us for split 576 plus
     merge).  ``attention_path`` forces either form.

@@ -237,14 +237,14 @@ def test_automatic_split_size() -> None:
 
 
 def test_attention_plan() -> None:
-    """One pass for wide batches (cfg2: 72 rows x 4 kv heads at 2k, three
+    """One pass for wide batches (cfg2: 72 rows x 4 kv heads at 2k, four
     wavefronts per kv head) and whenever the context fits one partition;
     split-KV for few workgroups at long contexts (the reference's own 1 x 8
     case, cfg3) or when the caller fixed the partition size."""
 
     cfg2 = attention_plan(2048, 72, 4, 2048)
-    assert (cfg2.one_pass, cfg2.num_splits, cfg2.waves_per_head) == (True, 1, 3)
-    assert cfg2.flags == (12 << 24) | (1 << 20) | (3 << 8)
+    assert (cfg2.one_pass, cfg2.num_splits, cfg2.waves_per_head) == (True, 1, 4)
+    assert cfg2.flags == (9 << 24) | (1 << 20) | (4 << 8)
     short = attention_plan(200, 2, 4, 2048)
     assert short.one_pass and short.waves_per_head == 1 and short.flags == 0
     assert short.split_size == 2048  # the whole table in one partition
@@ -254,7 +254,8 @@ def test_attention_plan() -> None:
     assert not attention_plan(2048, 32, 4, 2048).one_pass  # 128 workgroups
     cfg3 = attention_plan(32768, 4, 8, 32768)
     assert (cfg3.one_pass, cfg3.split_size, cfg3.num_splits) == (False, 2048, 16)
-    assert attention_plan(4096, 64, 4, 4096).waves_per_head == 6
+    assert attention_plan(4096, 64, 4, 4096).waves_per_head == 8
+    assert attention_plan(1024, 64, 4, 1024).waves_per_head == 2
     assert attention_plan(32768, 64, 4, 32768).waves_per_head == 8
     assert not attention_plan(2048, 72, 4, 2048, "split_kv").one_pass
     previous = set_attention_split_size(512)

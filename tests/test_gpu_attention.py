@@ -129,7 +129,7 @@ def test_long_context_with_few_heads_selects_split_kv_path(device):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_tinyllama_batch64_config(device, dtype):
     """64 rows ctx U[128, 2048] + 8 zero-length rows, one
-    pass with three wavefronts per kv head (the plan for a wide batch), and
+    pass with four wavefronts per kv head (the plan for a wide batch), and
     the forced split-KV path."""
 
     case = tinyllama_decode_case(seed=0, dtype=dtype)
@@ -139,7 +139,7 @@ def test_tinyllama_batch64_config(device, dtype):
         scale=case.scale, max_context_length=2048,
     )
     assert selected_attention_launch()["kernel"] == "mfma"
-    assert selected_attention_autotune_config()["waves_per_head"] == 3
+    assert selected_attention_autotune_config()["waves_per_head"] == 4
     _check_against_oracle(case, output.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, f"cfg2 {dtype}")
     split = paged_gqa_decode_attention(
         gpu.query, gpu.key_cache, gpu.value_cache, gpu.block_tables, gpu.context_lengths,
@@ -181,6 +181,32 @@ def test_grid_kernel_multi_wave_workgroups(device, heads_per_wg, waves_per_head,
     _check_against_oracle(case, out.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL,
                           f"hpw {heads_per_wg} wph {waves_per_head} tpw {tokens_per_wave} "
                           f"split {split_size}")
+
+
+@pytest.mark.parametrize(("head_dim", "dtype"), [(32, torch.float16), (64, torch.float16),
+                                                 (128, torch.bfloat16), (128, torch.float16)])
+def test_whole_row_loads_across_head_dims(device, head_dim, dtype):
+    """Several wavefronts per kv head load K / V as whole token rows and
+    stage K through LDS; every head_dim, both 16-bit types, ragged rows
+    (partial chunks, a one-token row, an empty row) and GQA groups of 4."""
+
+    lengths = [1000, 1, 577, 0, 1152, 33, 2047, 16]
+    case = make_decode_attention_case(
+        lengths, query_heads=16, kv_heads=4, head_dim=head_dim, block_size=16, dtype=dtype,
+        seed=head_dim + (dtype == torch.float16),
+    )
+    gpu = case.to(device)
+    workspace = PagedAttentionWorkspace.allocate(
+        batch_capacity=len(lengths), query_heads=16, head_dim=head_dim, max_context_length=2048,
+        device=device,
+    )
+    flags = ((1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
+             | (4 << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
+             | ((576 // 64) << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
+    out = torch.full_like(gpu.query, float("nan"))
+    _raw_decode(gpu, out, flags, gpu.block_tables.shape[1] * 16, 1, workspace)
+    _check_against_oracle(case, out.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL,
+                          f"whole rows D{head_dim} {dtype}")
 
 
 def test_llama3_long_context_split_kv(device):
