@@ -33,6 +33,8 @@
  *                            runtime/decode_bucket.py:441-447, 470, 500-505)
  *   tf_linear_partials,      the same projections at 17..64 rows, split over
  *   tf_linear_partials_sum   K into fp32 partials and their row sum
+ *   tf_linear_stream         the same projections staged through LDS with
+ *                            whole-row loads (direct or split-K partials)
  *   tf_prefill_attention     prefill's causal attention (runtime/prefill.py:84-88, 109-118)
  */
 #ifndef TENSORFORGE_AMD_H_
@@ -339,6 +341,22 @@ int32_t tf_linear_partials(const void *x, int64_t x_row_stride, const void *weig
                            int64_t weight_row_stride, float *partials, int32_t m,
                            int32_t n, int32_t k, int32_t splits, int32_t dtype,
                            void *stream);
+
+/*
+ * Weight-streaming form of the same product for up to 64 rows: with
+ * partials == NULL and splits == 1, y[i][j] = round(sum_k x[i][k] *
+ * weight[j][k]) into fp16/bf16 rows of y; with a partials buffer, the
+ * fp32 slice sums of tf_linear_partials (same slices, same [splits, m, n]
+ * layout).  Operands are staged through LDS with whole-row loads.  K % 32
+ * == 0, 16-byte aligned x and weight rows.  Replaces the torch GEMM of the
+ * decode projections (tensorforge/model/layers.py:88-95, 144-146) as the
+ * decode step calls them (tensorforge/runtime/decode_bucket.py:441-447,
+ * 470, 500-505).
+ */
+int32_t tf_linear_stream(const void *x, int64_t x_row_stride, const void *weight,
+                         int64_t weight_row_stride, void *y, int64_t y_row_stride,
+                         float *partials, int32_t m, int32_t n, int32_t k, int32_t splits,
+                         int32_t dtype, void *stream);
 
 /*
  * y[i][j] = round(sum_s partials[s][i][j]) into fp16/bf16 rows of y

@@ -145,6 +145,160 @@ linear_partials_kernel(const T *__restrict__ x, int64_t x_stride, const T *__res
   }
 }
 
+// ---------------------------------------------------------------------------
+// Weight-streaming form (tf_linear_stream).  A load in the MFMA operand
+// layout (lane (l16, q4) reading 16 bytes of row l16) touches 16 rows x half
+// a 128-byte line, and a compute unit issues such loads at <= 34 GB/s even
+// when they hit L2; whole-row loads run at ~85 GB/s from L2 and stream HBM
+// ~10% faster.  Here a workgroup stages 256-wide k chunks of x (16 MT rows)
+// and of its 64 weight rows in LDS with whole-row loads (32 threads per
+// 512-byte row piece), with the next two chunks' loads in flight in
+// registers while the MFMAs read the current one, and each wavefront owns
+// 16 output columns over the whole slice -- no cross-wavefront sum.  LDS
+// rows are 512 bytes with their 16-byte pieces permuted by
+// (piece ^ (row & 15)), so the 16 rows an operand read touches at one k
+// fall in distinct banks.
+// ---------------------------------------------------------------------------
+constexpr int kStreamCols = 64;    // output columns per workgroup (4 wavefronts x 16)
+constexpr int kStreamChunk = 256;  // k per LDS chunk (one 512-byte row)
+
+__device__ __forceinline__ int stream_lds_offset(int row, int piece) {
+  return row * kStreamChunk + ((piece ^ (row & 15)) << 3);
+}
+
+template <typename T, int MT>
+__global__ void __launch_bounds__(256)
+linear_stream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restrict__ w,
+                     int64_t w_stride, T *__restrict__ y, int64_t y_stride,
+                     float *__restrict__ partials, int32_t m, int32_t n, int32_t k,
+                     int32_t k_per_split) {
+  using M = SplitMma<T>;
+  using vec8 = typename M::vec8;
+  constexpr int XR = 16 * MT;
+  constexpr int kLoadsX = XR / 8;           // 16-byte loads per thread per chunk
+  constexpr int kLoadsW = kStreamCols / 8;
+  extern __shared__ __attribute__((aligned(16))) unsigned char stream_smem[];
+  T *xl = reinterpret_cast<T *>(stream_smem);  // [XR][256], swizzled pieces
+  T *wl = xl + XR * kStreamChunk;              // [64][256]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15;
+  const int q4 = lane >> 4;
+  const int32_t n0 = blockIdx.x * kStreamCols;
+  const int32_t split = blockIdx.y;
+  const int32_t s0 = split * k_per_split;
+  const int32_t s1 = min(s0 + k_per_split, k);
+  // Staging map: thread t loads piece t % 32 of row 8 i + t / 32.
+  const int lrow = tid >> 5;
+  const int lpiece = tid & 31;
+
+  const T *xsrc[kLoadsX];
+#pragma unroll
+  for (int i = 0; i < kLoadsX; ++i)
+    xsrc[i] = x + static_cast<int64_t>(min(8 * i + lrow, m - 1)) * x_stride + 8 * lpiece;
+  const T *wsrc[kLoadsW];
+#pragma unroll
+  for (int i = 0; i < kLoadsW; ++i)
+    wsrc[i] = w + static_cast<int64_t>(min(n0 + 8 * i + lrow, n - 1)) * w_stride + 8 * lpiece;
+
+  // Two register sets: while the MFMAs read chunk c from LDS, the loads of
+  // chunks c + 1 and c + 2 are in flight (128 KB per workgroup at MT = 4).
+  vec8 xa[kLoadsX], wa[kLoadsW], xb[kLoadsX], wb[kLoadsW];
+  // Pieces past K (only in a last, partial chunk) read the row's first
+  // piece instead; pieces past the slice but inside K are read and unused.
+  auto load_chunk = [&](int32_t kk, vec8(&xr)[kLoadsX], vec8(&wr)[kLoadsW]) {
+    const int32_t c = kk + 8 * lpiece < k ? kk : -8 * lpiece;
+#pragma unroll
+    for (int i = 0; i < kLoadsX; ++i) xr[i] = *reinterpret_cast<const vec8 *>(xsrc[i] + c);
+#pragma unroll
+    for (int i = 0; i < kLoadsW; ++i) wr[i] = *reinterpret_cast<const vec8 *>(wsrc[i] + c);
+  };
+  auto stage_chunk = [&](const vec8(&xr)[kLoadsX], const vec8(&wr)[kLoadsW]) {
+    __syncthreads();  // the previous chunk's operand reads are done
+#pragma unroll
+    for (int i = 0; i < kLoadsX; ++i)
+      *reinterpret_cast<vec8 *>(xl + stream_lds_offset(8 * i + lrow, lpiece)) = xr[i];
+#pragma unroll
+    for (int i = 0; i < kLoadsW; ++i)
+      *reinterpret_cast<vec8 *>(wl + stream_lds_offset(8 * i + lrow, lpiece)) = wr[i];
+    __syncthreads();
+  };
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute_chunk = [&](int32_t kk) {
+    const int32_t steps = min(kStreamChunk, s1 - kk) >> 5;
+#pragma unroll
+    for (int st = 0; st < kStreamChunk / 32; ++st) {
+      if (st >= steps) break;  // uniform
+      const int piece = 4 * st + q4;
+      const vec8 b = *reinterpret_cast<const vec8 *>(wl + stream_lds_offset(16 * wave + l16, piece));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = M::mma(*reinterpret_cast<const vec8 *>(xl + stream_lds_offset(16 * mt + l16, piece)),
+                         b, acc[mt]);
+    }
+  };
+
+  constexpr int32_t C = kStreamChunk;
+  load_chunk(s0, xa, wa);
+  if (s0 + C < s1) load_chunk(s0 + C, xb, wb);
+  for (int32_t kk = s0; kk < s1; kk += 2 * C) {
+    stage_chunk(xa, wa);
+    if (kk + 2 * C < s1) load_chunk(kk + 2 * C, xa, wa);
+    compute_chunk(kk);
+    if (kk + C >= s1) break;
+    stage_chunk(xb, wb);
+    if (kk + 3 * C < s1) load_chunk(kk + 3 * C, xb, wb);
+    compute_chunk(kk + C);
+  }
+
+  // C layout: lane (l16, q4), register r holds y[16 mt + 4 q4 + r][n0 + 16 wave + l16].
+  const int32_t col = n0 + 16 * wave + l16;
+  if (col >= n) return;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int32_t row = 16 * mt + 4 * q4 + r;
+      if (row >= m) continue;
+      if (partials)
+        partials[(static_cast<int64_t>(split) * m + row) * n + col] = acc[mt][r];
+      else
+        y[static_cast<int64_t>(row) * y_stride + col] = from_float<T>(acc[mt][r]);
+    }
+}
+
+template <typename T, int MT>
+void launch_stream(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
+                   int64_t y_stride, float *partials, int32_t m, int32_t n, int32_t k,
+                   int32_t splits, int32_t k_per_split, hipStream_t stream) {
+  const size_t lds = static_cast<size_t>(16 * MT + kStreamCols) * kStreamChunk * sizeof(T);
+  hipLaunchKernelGGL((linear_stream_kernel<T, MT>),
+                     dim3((n + kStreamCols - 1) / kStreamCols, splits), dim3(256), lds, stream,
+                     static_cast<const T *>(x), x_stride, static_cast<const T *>(w), w_stride,
+                     static_cast<T *>(y), y_stride, partials, m, n, k, k_per_split);
+}
+
+template <typename T>
+void launch_stream_mt(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
+                      int64_t y_stride, float *partials, int32_t m, int32_t n, int32_t k,
+                      int32_t splits, int32_t k_per_split, hipStream_t stream) {
+#define TF_STREAM_CASE(MT)                                                                     \
+  launch_stream<T, MT>(x, x_stride, w, w_stride, y, y_stride, partials, m, n, k, splits, \
+                       k_per_split, stream)
+  switch ((m + 15) / 16) {
+    case 1: TF_STREAM_CASE(1); break;
+    case 2: TF_STREAM_CASE(2); break;
+    case 3: TF_STREAM_CASE(3); break;
+    default: TF_STREAM_CASE(4); break;
+  }
+#undef TF_STREAM_CASE
+}
+
 // y[m][n] = round(sum_s partials[s][m][n]), four columns per thread.
 template <typename T>
 __global__ void __launch_bounds__(256)
@@ -261,4 +415,46 @@ extern "C" int32_t tf_linear_partials_sum(const float *partials, int32_t splits,
     hipLaunchKernelGGL(partials_sum_kernel<_Float16>, grid, dim3(256), 0, s, partials, splits, m,
                        n, static_cast<_Float16 *>(y), y_row_stride);
   return check_launch("linear_partials_sum");
+}
+
+extern "C" int32_t tf_linear_stream(const void *x, int64_t x_row_stride, const void *weight,
+                                    int64_t weight_row_stride, void *y, int64_t y_row_stride,
+                                    float *partials, int32_t m, int32_t n, int32_t k,
+                                    int32_t splits, int32_t dtype, void *stream) {
+  using namespace tf;
+  clear_error();
+  if (dtype != TF_DTYPE_FLOAT16 && dtype != TF_DTYPE_BFLOAT16)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_stream supports fp16 and bf16");
+  if (m < 0 || n < 0 || k < 0) return fail(TF_ERROR_INVALID_ARGUMENT, "sizes must be non-negative");
+  if (m > 64) return fail(TF_ERROR_UNSUPPORTED, "linear_stream supports at most 64 rows");
+  if (k % 32 != 0 || k == 0)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_stream needs K to be a positive multiple of 32");
+  if (splits < 1 || splits > k / 32)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "splits must be in [1, K / 32]");
+  if (!partials && splits != 1)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "several K slices need a partials buffer");
+  if (x_row_stride < k || weight_row_stride < k || (!partials && y_row_stride < n))
+    return fail(TF_ERROR_INVALID_ARGUMENT, "row strides are shorter than the rows");
+  if (n > 65535 * tf::kStreamCols || splits > 65535)
+    return fail(TF_ERROR_UNSUPPORTED, "grid too large");
+  if (m == 0 || n == 0) return TF_SUCCESS;
+  if (!x || !weight || (!partials && !y))
+    return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
+                          static_cast<uintptr_t>(x_row_stride * 2) |
+                          static_cast<uintptr_t>(weight_row_stride * 2);
+  if (align % 16 != 0)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_stream needs 16-byte aligned x and weight rows");
+  const int32_t steps = k / 32;
+  const int32_t k_per_split = ((steps + splits - 1) / splits) * 32;
+  if ((k + k_per_split - 1) / k_per_split != splits)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "splits must divide K / 32 into non-empty slices");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TF_DTYPE_BFLOAT16)
+    launch_stream_mt<__bf16>(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, partials,
+                             m, n, k, splits, k_per_split, s);
+  else
+    launch_stream_mt<_Float16>(x, x_row_stride, weight, weight_row_stride, y, y_row_stride,
+                               partials, m, n, k, splits, k_per_split, s);
+  return check_launch("linear_stream");
 }

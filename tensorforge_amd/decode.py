@@ -44,9 +44,9 @@ from tensorforge_amd import _native
 from tensorforge_amd.cache import AppendReservation, PagedKVCache
 from tensorforge_amd.kernels import (
     PagedAttentionWorkspace,
-    linear_partials,
     linear_rows,
     linear_rows_supported,
+    linear_stream,
     paged_gqa_decode_attention,
     residual_rms_norm,
     rms_norm,
@@ -161,14 +161,21 @@ class DecoderWeights:
 
 
 def _project(x: Tensor, weight: Tensor, output: Tensor | None = None) -> Tensor:
-    """x @ weight.T for a decode step.  Up to 16 rows, the K-split MFMA kernel
-    (linear_rows) streams small weights (<= 8M elements: the q/k/v and o
-    projections of TinyLlama) and the LM head faster than the library GEMM,
-    which launches too few workgroups for them, and up to 8 rows also the
-    stacked gate|up weight (11264 x 2048: 11.4-12.6 us against 13.8);
-    otherwise hipBLASLt (measured on MI355X at the TinyLlama shapes)."""
+    """x @ weight.T for a decode step (measured on MI355X at the TinyLlama
+    shapes).  Weights of >= 16384 rows (the LM head) up to 32 rows and of
+    >= 8192 rows (the stacked gate|up) up to 16 rows go through the
+    LDS-staged weight stream (linear_stream: 24.6-25.0 us against 30.4-30.7
+    for hipBLASLt at 32000 x 2048; 12.6-12.8 us against 12.5-14.7 at
+    11264 x 2048).  Other weights up to 16 rows use the K-split MFMA kernel
+    (linear_rows) when small (<= 8M elements: the q/k/v and o projections),
+    where the library GEMM launches too few workgroups; otherwise
+    hipBLASLt."""
 
     rows = x.shape[0]
+    if (linear_rows_supported(x, weight)
+            and ((weight.shape[0] >= 16384 and rows <= 32)
+                 or (weight.shape[0] >= 8192 and rows <= 16))):
+        return linear_stream(x, weight, output=output)
     rows_kernel = (rows <= 16 and linear_rows_supported(x, weight)
                    and (weight.numel() <= 8 * 1024 * 1024 or weight.shape[0] >= 16384
                         or (rows <= 8 and weight.shape[0] >= 8192)))
@@ -258,12 +265,14 @@ class DecodeGraphBucket:
         self.fused_rope = _native.library().tf_paged_gqa_decode_variant(
             _native.dtype_code(dtype), d, hq // hkv, cache.config.block_size,
             0) == _native.TF_ATTENTION_MFMA
-        # Output and down projections at up to 64 rows: split-K partials
-        # whose K-slice sum is fused into the residual RMSNorm that consumes
-        # them (measured faster than linear_rows and hipBLASLt at 1..64 rows
-        # for the TinyLlama o and down shapes; at up to 16 rows only for
-        # weights of >= 1M elements -- smaller ones make too few 64-column
-        # workgroups and stay on linear_rows).
+        # Output and down projections at up to 64 rows: split-K partials of
+        # the LDS-staged weight stream, whose K-slice sum is fused into the
+        # residual RMSNorm that consumes them (measured faster than
+        # linear_rows and hipBLASLt at 1..64 rows for the TinyLlama o and
+        # down shapes: at 64 rows 6.1 / 10.6 us against 10.9 / 18.2 for
+        # hipBLASLt; at up to 16 rows only for weights of >= 1M elements --
+        # smaller ones make too few 64-column workgroups and stay on
+        # linear_rows).
         self.split_o = self.split_down = 0
         layer0 = weights.layers[0]
         large = min(layer0.o_proj.numel(), layer0.down.numel()) >= 1024 * 1024
@@ -423,8 +432,8 @@ class DecodeGraphBucket:
                         output=self.attention_output, workspace=self.workspace)
                 attention = self.attention_output.view(b, hq * d)
                 if self.split_o:
-                    linear_partials(attention, layer.o_proj, self.split_o,
-                                    partials=self.partials_o)
+                    linear_stream(attention, layer.o_proj, splits=self.split_o,
+                                  partials=self.partials_o)
                     residual, h = residual_rms_norm_partials(
                         self.partials_o, residual, layer.post_norm, eps,
                         residual_output=torch.empty_like(residual), norm_output=self.norm_output)
@@ -437,8 +446,8 @@ class DecodeGraphBucket:
                 next_norm = (self.weights.layers[index + 1].input_norm
                              if index + 1 < len(self.weights.layers) else self.weights.final_norm)
                 if self.split_down:
-                    linear_partials(act, layer.down, self.split_down,
-                                    partials=self.partials_down)
+                    linear_stream(act, layer.down, splits=self.split_down,
+                                  partials=self.partials_down)
                     residual, h = residual_rms_norm_partials(
                         self.partials_down, residual, next_norm, eps,
                         residual_output=torch.empty_like(residual), norm_output=self.norm_output)

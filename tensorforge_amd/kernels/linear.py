@@ -14,6 +14,10 @@ each workgroup owns 64 output columns and one of ``splits`` slices of K, and
 writes the slice's fp32 partial product; ``linear_partials_sum`` (or a
 fused consumer) adds the slices and rounds once, which is the result of a
 GEMM with fp32 accumulation.
+
+``linear_stream`` computes the same products (direct, or as split-K slice
+sums) with both operands staged through LDS by whole-row loads, which a
+compute unit issues about 2.5x faster than loads in the MFMA operand layout.
 """
 
 from __future__ import annotations
@@ -115,6 +119,51 @@ def linear_partials(x: Tensor, weight: Tensor, splits: int, *,
         "linear_partials",
     )
     return partials
+
+
+def linear_stream(x: Tensor, weight: Tensor, *, splits: int = 1, output: Tensor | None = None,
+                  partials: Tensor | None = None) -> Tensor:
+    """``x [m, k] @ weight[n, k].T`` for m <= 64 with both operands staged
+    through LDS by whole-row loads.  With ``partials`` (fp32 ``[splits, m,
+    n]``) it writes the split-K slice sums of :func:`linear_partials` and
+    returns them; otherwise ``splits`` must be 1 and it returns the rounded
+    product in ``output`` (allocated when None)."""
+
+    if not _native.is_available():
+        raise RuntimeError(
+            "the gfx950 kernel library is unavailable; build it with "
+            "`python -m tensorforge_amd.build`"
+        )
+    if not linear_rows_supported(x, weight):
+        raise ValueError("linear_stream needs fp16/bf16 CUDA operands [m <= 64, k] and [n, k] "
+                         "with k % 32 == 0 and 16-byte aligned contiguous rows")
+    m, k = x.shape
+    n = weight.shape[0]
+    y_ptr, y_stride, p_ptr = None, 0, None
+    if partials is not None:
+        if (partials.shape != (splits, m, n) or partials.dtype != torch.float32
+                or partials.device != x.device or not partials.is_contiguous()):
+            raise ValueError("partials must be a contiguous fp32 [splits, m, n] tensor on x's device")
+        p_ptr = partials.data_ptr()
+        result = partials
+    else:
+        if splits != 1:
+            raise ValueError("several K slices need a partials buffer")
+        if output is None:
+            output = torch.empty((m, n), dtype=x.dtype, device=x.device)
+        if (output.shape != (m, n) or output.dtype != x.dtype or output.device != x.device
+                or output.stride(1) != 1):
+            raise ValueError("output must be [m, n] with contiguous rows, x's dtype and device")
+        y_ptr, y_stride = output.data_ptr(), output.stride(0)
+        result = output
+    _native.check(
+        _native.library().tf_linear_stream(
+            x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), y_ptr, y_stride,
+            p_ptr, m, n, k, splits, _native.dtype_code(x.dtype), _native.current_stream(x.device),
+        ),
+        "linear_stream",
+    )
+    return result
 
 
 def linear_partials_sum(partials: Tensor, *, dtype: torch.dtype | None = None,

@@ -94,6 +94,69 @@ def test_linear_partials_sum_matches_fp32(device, dtype, rows, n, k, splits):
     assert torch.equal(out.cpu(), running.to(dtype).cpu())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 17, 33, 64])
+@pytest.mark.parametrize(("n", "k", "splits"), [(2048, 2048, 8), (2048, 5632, 8), (2560, 2048, 1),
+                                                (11264, 2048, 1), (100, 96, 3), (64, 32, 1),
+                                                (300, 800, 5), (96, 2080, 1)])
+def test_linear_stream_matches_fp32(device, dtype, rows, n, k, splits):
+    """The LDS-staged weight stream: slice sums within fp32 accumulation
+    error of the fp32 slice products, and the direct (one-slice) output
+    within the storage type's bar of the fp32 product -- on partial 256-wide
+    chunks (K = 800 in slices of 160, K = 2080), tail column tiles and
+    every row count the decode step uses."""
+
+    from tensorforge_amd.kernels import linear_stream
+
+    generator = torch.Generator().manual_seed(rows * 11 + n + k + splits)
+    x = torch.randn(rows, k, generator=generator).to(dtype)
+    w = (torch.randn(n, k, generator=generator) * 0.02).to(dtype)
+    steps = k // 32
+    per = -(-steps // splits) * 32
+    expected_partials = torch.stack([x[:, s * per:(s + 1) * per].float()
+                                     @ w[:, s * per:(s + 1) * per].float().T
+                                     for s in range(splits)])
+    partials = torch.full((splits, rows, n), float("nan"), device=device)
+    linear_stream(x.to(device), w.to(device), splits=splits, partials=partials)
+    scale = float(expected_partials.abs().max())
+    torch.testing.assert_close(partials.cpu(), expected_partials, rtol=1e-4, atol=1e-4 * scale)
+    if splits == 1:
+        out = torch.full((rows, n), float("nan"), device=device, dtype=dtype)
+        linear_stream(x.to(device), w.to(device), output=out)
+        expected = x.float() @ w.float().T
+        tol = TOLERANCE[dtype]
+        torch.testing.assert_close(out.float().cpu(), expected, rtol=tol,
+                                   atol=tol * float(expected.abs().max()))
+        # The direct output is the one-slice partial rounded once.
+        assert torch.equal(out.cpu(), partials[0].to(dtype).cpu())
+
+
+def test_linear_stream_strided_rows_and_rejections(device):
+    from tensorforge_amd.kernels import linear_stream
+
+    generator = torch.Generator().manual_seed(9)
+    wide = torch.randn(40, 2048 + 64, generator=generator).to(torch.bfloat16).to(device)
+    x = wide[:, 64:]
+    w = (torch.randn(300, 2048, generator=generator) * 0.02).to(torch.bfloat16).to(device)
+    out_wide = torch.zeros(40, 320, dtype=torch.bfloat16, device=device)
+    linear_stream(x, w, output=out_wide[:, :300])
+    expected = x.float() @ w.float().T
+    torch.testing.assert_close(out_wide[:, :300].float(), expected, rtol=2e-2,
+                               atol=2e-2 * float(expected.abs().max()))
+    assert bool((out_wide[:, 300:] == 0).all())
+    with pytest.raises(ValueError, match="partials buffer"):
+        linear_stream(x, w, splits=2)
+    with pytest.raises(ValueError):
+        linear_stream(torch.zeros(65, 2048, dtype=torch.bfloat16, device=device), w)
+    partials = torch.empty(4, 40, 300, device=device)
+    linear_stream(x[:, :96], w[:, :96], splits=3, partials=partials[:3])  # one k-step each
+    torch.testing.assert_close(partials[:3].sum(0), x[:, :96].float() @ w[:, :96].float().T,
+                               rtol=1e-4, atol=1e-3)
+    with pytest.raises(RuntimeError, match="non-empty"):
+        # 5 k-steps in slices of 2 fill only 3 slices
+        linear_stream(x[:, :160], w[:, :160], splits=4, partials=partials)
+
+
 def test_linear_partials_strided_x_and_rejections(device):
     from tensorforge_amd.kernels import linear_partials
 
