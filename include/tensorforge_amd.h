@@ -35,6 +35,8 @@
  *   tf_linear_partials_sum   K into fp32 partials and their row sum
  *   tf_linear_stream         the same projections staged through LDS with
  *                            whole-row loads (direct or split-K partials)
+ *   tf_linear_swiglu         the MLP's gate|up projection with its SwiGLU
+ *                            (model/layers.py:144-158)
  *   tf_prefill_attention     prefill's causal attention (runtime/prefill.py:84-88, 109-118)
  */
 #ifndef TENSORFORGE_AMD_H_
@@ -357,6 +359,22 @@ int32_t tf_linear_stream(const void *x, int64_t x_row_stride, const void *weight
                          int64_t weight_row_stride, void *y, int64_t y_row_stride,
                          float *partials, int32_t m, int32_t n, int32_t k, int32_t splits,
                          int32_t dtype, void *stream);
+
+/*
+ * The MLP's stacked gate|up projection and its SwiGLU in one launch:
+ *   y[i][j] = round(swiglu(round(x[i] . w[j]), round(x[i] . w[intermediate + j])))
+ * for j < intermediate, with gate_up_weight stacking the gate rows
+ * [0, intermediate) over the up rows [intermediate, 2 * intermediate) and
+ * swiglu(g, u) = g * sigmoid(g) * u in fp32 -- bit for bit
+ * tf_linear_stream of the stacked weight followed by tf_swiglu_rows.  Up to
+ * 64 rows, K % 32 == 0, 16-byte aligned x and weight rows.  Replaces
+ * silu(gate(x)) * up(x) of the MLP (tensorforge/model/layers.py:144-158;
+ * the activation tensorforge/kernels/triton_ops.py:246-260) as the decode
+ * step calls it (tensorforge/runtime/decode_bucket.py:500-505).
+ */
+int32_t tf_linear_swiglu(const void *x, int64_t x_row_stride, const void *gate_up_weight,
+                         int64_t weight_row_stride, void *y, int64_t y_row_stride, int32_t m,
+                         int32_t intermediate, int32_t k, int32_t dtype, void *stream);
 
 /*
  * y[i][j] = round(sum_s partials[s][i][j]) into fp16/bf16 rows of y

@@ -84,6 +84,16 @@ __device__ __forceinline__ float rope_hi(float x1, float x2, float c, float s) {
 }
 
 // ---------------------------------------------------------------------------
+// SwiGLU activation of one element, g * sigmoid(g) * u in fp32 (the caller
+// rounds once to the storage type); one definition for every kernel that
+// applies it, so they round identically.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float swiglu_act(float g, float u) {
+  const float silu = g / (1.0f + expf(-g));
+  return silu * u;
+}
+
+// ---------------------------------------------------------------------------
 // Wavefront (64-lane) reductions.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {

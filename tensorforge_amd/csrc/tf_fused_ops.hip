@@ -147,11 +147,7 @@ template <typename T, int VEC>
 __device__ __forceinline__ Vec<T, VEC> swiglu_vec(const Vec<T, VEC> &gv, const Vec<T, VEC> &uv) {
   Vec<T, VEC> out;
 #pragma unroll
-  for (int e = 0; e < VEC; ++e) {
-    const float x = to_float(gv.v[e]);
-    const float silu = x / (1.0f + expf(-x));
-    out.v[e] = from_float<T>(silu * to_float(uv.v[e]));
-  }
+  for (int e = 0; e < VEC; ++e) out.v[e] = from_float<T>(swiglu_act(to_float(gv.v[e]), to_float(uv.v[e])));
   return out;
 }
 

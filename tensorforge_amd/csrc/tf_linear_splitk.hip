@@ -166,7 +166,12 @@ __device__ __forceinline__ int stream_lds_offset(int row, int piece) {
   return row * kStreamChunk + ((piece ^ (row & 15)) << 3);
 }
 
-template <typename T, int MT>
+// SWIGLU: the weight stacks gate rows [0, n) over up rows [n, 2n) and the
+// workgroup covers 32 output columns j: wavefronts 0-1 compute the gate
+// columns and 2-3 the matching up columns, which reach 0-1 through LDS; the
+// output is round(swiglu_act(round(g), round(u))), the SwiGLU of the
+// rounded projection.
+template <typename T, int MT, bool SWIGLU>
 __global__ void __launch_bounds__(256)
 linear_stream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restrict__ w,
                      int64_t w_stride, T *__restrict__ y, int64_t y_stride,
@@ -186,7 +191,7 @@ linear_stream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restr
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15;
   const int q4 = lane >> 4;
-  const int32_t n0 = blockIdx.x * kStreamCols;
+  const int32_t n0 = blockIdx.x * (SWIGLU ? kStreamCols / 2 : kStreamCols);
   const int32_t split = blockIdx.y;
   const int32_t s0 = split * k_per_split;
   const int32_t s1 = min(s0 + k_per_split, k);
@@ -200,8 +205,12 @@ linear_stream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restr
     xsrc[i] = x + static_cast<int64_t>(min(8 * i + lrow, m - 1)) * x_stride + 8 * lpiece;
   const T *wsrc[kLoadsW];
 #pragma unroll
-  for (int i = 0; i < kLoadsW; ++i)
-    wsrc[i] = w + static_cast<int64_t>(min(n0 + 8 * i + lrow, n - 1)) * w_stride + 8 * lpiece;
+  for (int i = 0; i < kLoadsW; ++i) {
+    const int tr = 8 * i + lrow;  // tile row
+    const int64_t row = SWIGLU ? (tr < 32 ? 0 : n) + min(n0 + (tr & 31), n - 1)
+                               : min(n0 + tr, n - 1);
+    wsrc[i] = w + row * w_stride + 8 * lpiece;
+  }
 
   // Two register sets: while the MFMAs read chunk c from LDS, the loads of
   // chunks c + 1 and c + 2 are in flight (128 KB per workgroup at MT = 4).
@@ -257,6 +266,31 @@ linear_stream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restr
   }
 
   // C layout: lane (l16, q4), register r holds y[16 mt + 4 q4 + r][n0 + 16 wave + l16].
+  if constexpr (SWIGLU) {
+    float *up = reinterpret_cast<float *>(stream_smem);  // [2 waves][MT * 4][64 lanes]
+    __syncthreads();  // the last chunk's operand reads are done
+    if (wave >= 2) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          up[((wave - 2) * MT * 4 + mt * 4 + r) * 64 + lane] = to_float(from_float<T>(acc[mt][r]));
+    }
+    __syncthreads();
+    const int32_t col = n0 + 16 * wave + l16;
+    if (wave >= 2 || col >= n) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int32_t row = 16 * mt + 4 * q4 + r;
+        if (row >= m) continue;
+        const float g = to_float(from_float<T>(acc[mt][r]));
+        const float u = up[(wave * MT * 4 + mt * 4 + r) * 64 + lane];
+        y[static_cast<int64_t>(row) * y_stride + col] = from_float<T>(swiglu_act(g, u));
+      }
+    return;
+  }
   const int32_t col = n0 + 16 * wave + l16;
   if (col >= n) return;
 #pragma unroll
@@ -272,24 +306,25 @@ linear_stream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restr
     }
 }
 
-template <typename T, int MT>
+template <typename T, int MT, bool SWIGLU>
 void launch_stream(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
                    int64_t y_stride, float *partials, int32_t m, int32_t n, int32_t k,
                    int32_t splits, int32_t k_per_split, hipStream_t stream) {
   const size_t lds = static_cast<size_t>(16 * MT + kStreamCols) * kStreamChunk * sizeof(T);
-  hipLaunchKernelGGL((linear_stream_kernel<T, MT>),
-                     dim3((n + kStreamCols - 1) / kStreamCols, splits), dim3(256), lds, stream,
+  const int32_t cols = SWIGLU ? kStreamCols / 2 : kStreamCols;
+  hipLaunchKernelGGL((linear_stream_kernel<T, MT, SWIGLU>),
+                     dim3((n + cols - 1) / cols, splits), dim3(256), lds, stream,
                      static_cast<const T *>(x), x_stride, static_cast<const T *>(w), w_stride,
                      static_cast<T *>(y), y_stride, partials, m, n, k, k_per_split);
 }
 
-template <typename T>
+template <typename T, bool SWIGLU>
 void launch_stream_mt(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
                       int64_t y_stride, float *partials, int32_t m, int32_t n, int32_t k,
                       int32_t splits, int32_t k_per_split, hipStream_t stream) {
-#define TF_STREAM_CASE(MT)                                                                     \
-  launch_stream<T, MT>(x, x_stride, w, w_stride, y, y_stride, partials, m, n, k, splits, \
-                       k_per_split, stream)
+#define TF_STREAM_CASE(MT)                                                                   \
+  launch_stream<T, MT, SWIGLU>(x, x_stride, w, w_stride, y, y_stride, partials, m, n, k,    \
+                               splits, k_per_split, stream)
   switch ((m + 15) / 16) {
     case 1: TF_STREAM_CASE(1); break;
     case 2: TF_STREAM_CASE(2); break;
@@ -417,11 +452,13 @@ extern "C" int32_t tf_linear_partials_sum(const float *partials, int32_t splits,
   return check_launch("linear_partials_sum");
 }
 
-extern "C" int32_t tf_linear_stream(const void *x, int64_t x_row_stride, const void *weight,
-                                    int64_t weight_row_stride, void *y, int64_t y_row_stride,
-                                    float *partials, int32_t m, int32_t n, int32_t k,
-                                    int32_t splits, int32_t dtype, void *stream) {
-  using namespace tf;
+namespace tf {
+namespace {
+
+int32_t linear_stream_entry(const void *x, int64_t x_row_stride, const void *weight,
+                            int64_t weight_row_stride, void *y, int64_t y_row_stride,
+                            float *partials, int32_t m, int32_t n, int32_t k, int32_t splits,
+                            int32_t dtype, void *stream, bool swiglu, const char *name) {
   clear_error();
   if (dtype != TF_DTYPE_FLOAT16 && dtype != TF_DTYPE_BFLOAT16)
     return fail(TF_ERROR_UNSUPPORTED, "linear_stream supports fp16 and bf16");
@@ -435,7 +472,7 @@ extern "C" int32_t tf_linear_stream(const void *x, int64_t x_row_stride, const v
     return fail(TF_ERROR_INVALID_ARGUMENT, "several K slices need a partials buffer");
   if (x_row_stride < k || weight_row_stride < k || (!partials && y_row_stride < n))
     return fail(TF_ERROR_INVALID_ARGUMENT, "row strides are shorter than the rows");
-  if (n > 65535 * tf::kStreamCols || splits > 65535)
+  if (n > 65535 * (kStreamCols / 2) || splits > 65535)
     return fail(TF_ERROR_UNSUPPORTED, "grid too large");
   if (m == 0 || n == 0) return TF_SUCCESS;
   if (!x || !weight || (!partials && !y))
@@ -450,11 +487,35 @@ extern "C" int32_t tf_linear_stream(const void *x, int64_t x_row_stride, const v
   if ((k + k_per_split - 1) / k_per_split != splits)
     return fail(TF_ERROR_INVALID_ARGUMENT, "splits must divide K / 32 into non-empty slices");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == TF_DTYPE_BFLOAT16)
-    launch_stream_mt<__bf16>(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, partials,
-                             m, n, k, splits, k_per_split, s);
-  else
-    launch_stream_mt<_Float16>(x, x_row_stride, weight, weight_row_stride, y, y_row_stride,
-                               partials, m, n, k, splits, k_per_split, s);
-  return check_launch("linear_stream");
+#define TF_STREAM_LAUNCH(T, G)                                                                \
+  launch_stream_mt<T, G>(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, partials, \
+                         m, n, k, splits, k_per_split, s)
+  if (dtype == TF_DTYPE_BFLOAT16) {
+    if (swiglu) TF_STREAM_LAUNCH(__bf16, true); else TF_STREAM_LAUNCH(__bf16, false);
+  } else {
+    if (swiglu) TF_STREAM_LAUNCH(_Float16, true); else TF_STREAM_LAUNCH(_Float16, false);
+  }
+#undef TF_STREAM_LAUNCH
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace tf
+
+extern "C" int32_t tf_linear_stream(const void *x, int64_t x_row_stride, const void *weight,
+                                    int64_t weight_row_stride, void *y, int64_t y_row_stride,
+                                    float *partials, int32_t m, int32_t n, int32_t k,
+                                    int32_t splits, int32_t dtype, void *stream) {
+  return tf::linear_stream_entry(x, x_row_stride, weight, weight_row_stride, y, y_row_stride,
+                                 partials, m, n, k, splits, dtype, stream, false,
+                                 "linear_stream");
+}
+
+extern "C" int32_t tf_linear_swiglu(const void *x, int64_t x_row_stride, const void *gate_up_weight,
+                                    int64_t weight_row_stride, void *y, int64_t y_row_stride,
+                                    int32_t m, int32_t intermediate, int32_t k, int32_t dtype,
+                                    void *stream) {
+  return tf::linear_stream_entry(x, x_row_stride, gate_up_weight, weight_row_stride, y,
+                                 y_row_stride, nullptr, m, intermediate, k, 1, dtype, stream,
+                                 true, "linear_swiglu");
 }

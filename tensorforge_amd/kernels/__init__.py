@@ -18,6 +18,7 @@ from tensorforge_amd.kernels.linear import (
     linear_partials,
     linear_partials_sum,
     linear_stream,
+    linear_swiglu,
     linear_rows,
     linear_rows_supported,
 )
@@ -40,6 +41,7 @@ __all__ = [
     "linear_partials",
     "linear_partials_sum",
     "linear_stream",
+    "linear_swiglu",
     "linear_rows",
     "linear_rows_supported",
     "paged_gqa_decode_attention",

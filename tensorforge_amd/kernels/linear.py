@@ -18,6 +18,8 @@ GEMM with fp32 accumulation.
 ``linear_stream`` computes the same products (direct, or as split-K slice
 sums) with both operands staged through LDS by whole-row loads, which a
 compute unit issues about 2.5x faster than loads in the MFMA operand layout.
+``linear_swiglu`` is its form for the MLP's stacked gate|up weight with the
+SwiGLU applied in the epilogue.
 """
 
 from __future__ import annotations
@@ -164,6 +166,40 @@ def linear_stream(x: Tensor, weight: Tensor, *, splits: int = 1, output: Tensor 
         "linear_stream",
     )
     return result
+
+
+def linear_swiglu(x: Tensor, gate_up_weight: Tensor, *, output: Tensor | None = None) -> Tensor:
+    """``swiglu(x @ gate.T, x @ up.T)`` for m <= 64 rows, with
+    ``gate_up_weight`` stacking the gate rows over the up rows (``[2I, k]``)
+    -- the stacked projection and its activation in one launch, bit-identical
+    to :func:`linear_stream` of the stacked weight followed by
+    ``swiglu_gate_up``.  Returns ``[m, I]`` in ``output`` (allocated when
+    None)."""
+
+    if not _native.is_available():
+        raise RuntimeError(
+            "the gfx950 kernel library is unavailable; build it with "
+            "`python -m tensorforge_amd.build`"
+        )
+    if not linear_rows_supported(x, gate_up_weight) or gate_up_weight.shape[0] % 2:
+        raise ValueError("linear_swiglu needs fp16/bf16 CUDA operands [m <= 64, k] and a "
+                         "stacked [2I, k] weight with k % 32 == 0 and 16-byte aligned rows")
+    m, k = x.shape
+    inter = gate_up_weight.shape[0] // 2
+    if output is None:
+        output = torch.empty((m, inter), dtype=x.dtype, device=x.device)
+    if (output.shape != (m, inter) or output.dtype != x.dtype or output.device != x.device
+            or output.stride(1) != 1):
+        raise ValueError("output must be [m, I] with contiguous rows, x's dtype and device")
+    _native.check(
+        _native.library().tf_linear_swiglu(
+            x.data_ptr(), x.stride(0), gate_up_weight.data_ptr(), gate_up_weight.stride(0),
+            output.data_ptr(), output.stride(0), m, inter, k, _native.dtype_code(x.dtype),
+            _native.current_stream(x.device),
+        ),
+        "linear_swiglu",
+    )
+    return output
 
 
 def linear_partials_sum(partials: Tensor, *, dtype: torch.dtype | None = None,

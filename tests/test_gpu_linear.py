@@ -131,6 +131,32 @@ def test_linear_stream_matches_fp32(device, dtype, rows, n, k, splits):
         assert torch.equal(out.cpu(), partials[0].to(dtype).cpu())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 9, 33, 64])
+@pytest.mark.parametrize(("inter", "k"), [(5632, 2048), (768, 256), (100, 800), (48, 96)])
+def test_linear_swiglu_equals_projection_then_activation(device, dtype, rows, inter, k):
+    """The gate|up projection with SwiGLU in its epilogue is bit-identical
+    to linear_stream of the stacked weight followed by swiglu_gate_up, and
+    within the storage bar of the fp32 reference; tail column groups
+    (intermediate not a multiple of 32) included."""
+
+    from tensorforge_amd.kernels import linear_stream, linear_swiglu, swiglu_gate_up
+
+    generator = torch.Generator().manual_seed(rows * 17 + inter + k)
+    x = torch.randn(rows, k, generator=generator).to(dtype).to(device)
+    w = (torch.randn(2 * inter, k, generator=generator) * 0.05).to(dtype).to(device)
+    want = swiglu_gate_up(linear_stream(x, w))
+    got = torch.full((rows, inter), float("nan"), dtype=dtype, device=device)
+    linear_swiglu(x, w, output=got)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    gu = (x.float() @ w.float().T).to(dtype).float().cpu()
+    g, u = gu[:, :inter], gu[:, inter:]
+    expected = g * torch.sigmoid(g) * u
+    tol = TOLERANCE[dtype]
+    torch.testing.assert_close(got.float().cpu(), expected, rtol=tol,
+                               atol=tol * float(expected.abs().max()))
+
+
 def test_linear_stream_strided_rows_and_rejections(device):
     from tensorforge_amd.kernels import linear_stream
 
