@@ -143,29 +143,56 @@ ONE_PASS_MIN_WORKGROUPS = 192
 # on MI355X at config 2, three seeds: 576 with up to 4 wavefronts per 2k row
 # beats 448 / 512 / 640 and the 768 / 3 of the operand-layout loads).
 ONE_PASS_TOKENS_PER_WAVE = 576
+# Narrow calls (fewer workgroups than ONE_PASS_MIN_WORKGROUPS) are latency-
+# bound: one pass with up to 8 wavefronts per kv head, a row using one per
+# 64 of its tokens, when the context is short (<= 1024 tokens, or <= 2048
+# with >= 128 workgroups); otherwise split-KV with up to 4 wavefronts per
+# (row, kv head, split) -- see attention_plan for the measurements.
+NARROW_ONE_PASS_CONTEXT = 1024
+NARROW_ONE_PASS_MIN_WORKGROUPS = 128
+NARROW_WAVES = 8
+NARROW_SPLIT_WAVES = 4
+NARROW_TOKENS_PER_WAVE = 64
 
 
 @dataclass(frozen=True, slots=True)
 class AttentionPlan:
-    """How one call is launched: one pass (one workgroup per (row, kv head)
-    with ``waves_per_head`` wavefronts that combine in LDS) or split-KV
-    (``num_splits`` partitions of ``split_size`` tokens and a merge)."""
+    """Launch shape of one decode-attention call: one pass or split-KV
+    (``num_splits`` partitions of ``split_size`` tokens and a merge), with
+    ``waves_per_head`` wavefronts per (row, kv head, split), a row using one
+    per ``tokens_per_wave`` of its tokens in the partition."""
 
     one_pass: bool
     split_size: int
     num_splits: int
     waves_per_head: int
+    tokens_per_wave: int = ONE_PASS_TOKENS_PER_WAVE
 
     @property
     def flags(self) -> int:
-        """Several wavefronts per kv head, each row using one per 576 of its
-        tokens (so short rows leave the memory system to the long ones)."""
+        """The C ABI's launch flags for several wavefronts per kv head (0 for one)."""
 
         if self.waves_per_head <= 1:
             return 0
         return ((1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
                 | (self.waves_per_head << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
-                | ((ONE_PASS_TOKENS_PER_WAVE // 64) << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
+                | ((self.tokens_per_wave // 64) << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
+
+
+def narrow_split_size_for(max_context_length: int, batch: int, kv_heads: int) -> int:
+    """Partition size of a narrow split-KV call with several wavefronts per
+    split: the smallest size >= 256 that keeps the grid near 256 (row, kv
+    head, split) workgroups, and at most 16 splits per row --
+    ``max(256, ceil64(L * B * Hkv / 256), ceil64(L / 16))``."""
+
+    def ceil64(value: int) -> int:
+        return (value + 63) // 64 * 64
+
+    return max(
+        REFERENCE_SPLIT_SIZE,
+        ceil64(max_context_length * max(batch, 1) * kv_heads // 256),
+        ceil64((max_context_length + 15) // 16),
+    )
 
 
 def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capacity: int,
@@ -174,27 +201,46 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
 
     The reference runs one pass unless the batch has few programs
     (``triton_attention.py:400-404``: split-KV only for contexts >= 1024 with
-    batch * query heads <= 32).  Here, with the per-call split size
-    (attention_split_size_for), a call runs one pass when its context fits
-    one partition, or when it has at least 192 (row, kv head) workgroups and
-    the partition size was not fixed by the caller: each workgroup then
-    splits its row over ceil(L / 576) (at most 8) wavefronts that combine in
-    LDS, with no partials and no merge launch (measured on MI355X at
-    72 rows x 4 kv heads x 2k: 23.1 us against 26.0 us for split 576 plus
-    merge).  ``attention_path`` forces either form.
+    batch * query heads <= 32).  Here (measured on MI355X, TinyLlama
+    geometry unless noted):
+
+    * at least 192 (row, kv head) workgroups and no caller-fixed partition
+      size: one pass, each workgroup splitting its row over ceil(L / 576)
+      (at most 8) wavefronts that combine in LDS -- no partials, no merge
+      launch (72 rows x 4 kv heads x 2k: 21.3 us against 26.0 us for split
+      576 plus merge);
+    * fewer workgroups, context <= 1024 (or <= 2048 with >= 128 workgroups):
+      one pass with up to 8 wavefronts per kv head, one per 64 tokens of a
+      row (1-16 rows x 1k: 9.8-10.1 us against 12.5-12.9 for 256-token
+      splits with one wavefront each; 32 x 2k: 17.9 against 20.9);
+    * otherwise split-KV with up to 4 wavefronts per split and the partition
+      size of narrow_split_size_for (1 x 4k: 11.9 against 13.5 us; 8 x 4k:
+      14.2 against 15.5; config 3, 4 x 8-32k x 8 kv heads at D 128: 74.7
+      against 78.4);
+    * a partition size fixed by the caller (set_attention_split_size) or
+      ``attention_path="split_kv"``: split-KV with one wavefront per split
+      and attention_split_size_for; ``"one_pass"`` forces one pass.
     """
 
-    split_size = (_SPLIT_SIZE if _SPLIT_SIZE is not None
+    fixed = _SPLIT_SIZE is not None
+    split_size = (_SPLIT_SIZE if fixed
                   else attention_split_size_for(launch_context, batch, kv_heads))
-    wide = _SPLIT_SIZE is None and batch * kv_heads >= ONE_PASS_MIN_WORKGROUPS
-    one_pass = attention_path == "one_pass" or (
-        attention_path == "auto" and (launch_context <= split_size or wide))
-    if one_pass:
-        waves = 1
-        if wide:
-            waves = max(1, min(8, -(-launch_context // ONE_PASS_TOKENS_PER_WAVE)))
-        return AttentionPlan(True, (context_capacity + 31) // 32 * 32, 1, waves)
-    return AttentionPlan(False, split_size, (launch_context + split_size - 1) // split_size, 1)
+    workgroups = batch * kv_heads
+    capacity32 = (context_capacity + 31) // 32 * 32
+    if fixed or attention_path == "split_kv":
+        if attention_path == "one_pass" or (attention_path == "auto"
+                                            and launch_context <= split_size):
+            return AttentionPlan(True, capacity32, 1, 1)
+        return AttentionPlan(False, split_size, (launch_context + split_size - 1) // split_size, 1)
+    if workgroups >= ONE_PASS_MIN_WORKGROUPS:
+        waves = max(1, min(8, -(-launch_context // ONE_PASS_TOKENS_PER_WAVE)))
+        return AttentionPlan(True, capacity32, 1, waves)
+    if (attention_path == "one_pass" or launch_context <= NARROW_ONE_PASS_CONTEXT
+            or (workgroups >= NARROW_ONE_PASS_MIN_WORKGROUPS and launch_context <= 2048)):
+        return AttentionPlan(True, capacity32, 1, NARROW_WAVES, NARROW_TOKENS_PER_WAVE)
+    narrow = narrow_split_size_for(launch_context, batch, kv_heads)
+    return AttentionPlan(False, narrow, (launch_context + narrow - 1) // narrow,
+                         NARROW_SPLIT_WAVES, NARROW_TOKENS_PER_WAVE)
 
 
 def paged_gqa_decode_attention(
@@ -349,7 +395,7 @@ def paged_gqa_decode_attention(
                 num_splits,
                 attention_scale,
                 dtype,
-                0,
+                plan.flags,
                 stream,
             ),
             "paged_gqa_decode_attention",
@@ -358,6 +404,7 @@ def paged_gqa_decode_attention(
             "path": "split_kv",
             "split_size": split_size,
             "num_splits": num_splits,
+            "waves_per_head": plan.waves_per_head if kernel == "mfma" else 1,
         }
     else:
         # One partition spanning the whole table: every present token of a

@@ -238,30 +238,47 @@ def test_automatic_split_size() -> None:
 
 def test_attention_plan() -> None:
     """One pass for wide batches (cfg2: 72 rows x 4 kv heads at 2k, four
-    wavefronts per kv head) and whenever the context fits one partition;
-    split-KV for few workgroups at long contexts (the reference's own 1 x 8
-    case, cfg3) or when the caller fixed the partition size."""
+    wavefronts per kv head, one per 576 tokens); for narrow calls one pass
+    with up to 8 wavefronts (one per 64 tokens) at short contexts and
+    split-KV with up to 4 wavefronts per split at long ones (the reference's
+    own 1 x 8 case keeps its 256-token partitions; cfg3 takes 4096); one
+    wavefront per split when the caller fixes the partition size or forces
+    split-KV."""
+
+    from tensorforge_amd.kernels.attention import narrow_split_size_for
 
     cfg2 = attention_plan(2048, 72, 4, 2048)
     assert (cfg2.one_pass, cfg2.num_splits, cfg2.waves_per_head) == (True, 1, 4)
     assert cfg2.flags == (9 << 24) | (1 << 20) | (4 << 8)
     short = attention_plan(200, 2, 4, 2048)
-    assert short.one_pass and short.waves_per_head == 1 and short.flags == 0
+    assert short.one_pass and short.waves_per_head == 8
+    assert short.flags == (1 << 24) | (1 << 20) | (8 << 8)
     assert short.split_size == 2048  # the whole table in one partition
+    assert attention_plan(1000, 16, 4, 1024).one_pass
     few = attention_plan(2048, 1, 4, 2048)
-    assert (few.one_pass, few.split_size, few.num_splits) == (False, 256, 8)
-    assert attention_plan(2048, 48, 4, 2048).one_pass      # 192 workgroups
-    assert not attention_plan(2048, 32, 4, 2048).one_pass  # 128 workgroups
+    assert (few.one_pass, few.split_size, few.num_splits, few.waves_per_head) == (False, 256, 8, 4)
+    assert few.flags == (1 << 24) | (1 << 20) | (4 << 8)
+    assert attention_plan(2048, 48, 4, 2048).one_pass  # 192 workgroups: wide
+    narrow32 = attention_plan(2048, 32, 4, 2048)        # 128 workgroups, <= 2k
+    assert narrow32.one_pass and narrow32.waves_per_head == 8
+    assert not attention_plan(2100, 32, 4, 2112).one_pass
+    long8 = attention_plan(4000, 8, 4, 4096)
+    assert (long8.one_pass, long8.split_size, long8.num_splits) == (False, 512, 8)
     cfg3 = attention_plan(32768, 4, 8, 32768)
-    assert (cfg3.one_pass, cfg3.split_size, cfg3.num_splits) == (False, 2048, 16)
+    assert (cfg3.one_pass, cfg3.split_size, cfg3.num_splits) == (False, 4096, 8)
+    assert narrow_split_size_for(32768, 1, 4) == 2048  # at most 16 splits per row
+    assert narrow_split_size_for(4000, 1, 4) == 256
     assert attention_plan(4096, 64, 4, 4096).waves_per_head == 8
     assert attention_plan(1024, 64, 4, 1024).waves_per_head == 2
     assert attention_plan(32768, 64, 4, 32768).waves_per_head == 8
-    assert not attention_plan(2048, 72, 4, 2048, "split_kv").one_pass
+    forced = attention_plan(2048, 72, 4, 2048, "split_kv")
+    assert (forced.one_pass, forced.split_size, forced.waves_per_head) == (False, 576, 1)
     previous = set_attention_split_size(512)
     try:
         fixed = attention_plan(2048, 72, 4, 2048)
         assert (fixed.one_pass, fixed.split_size, fixed.num_splits) == (False, 512, 4)
+        assert fixed.flags == 0
+        assert attention_plan(400, 2, 4, 2048).waves_per_head == 1
     finally:
         set_attention_split_size(previous)
 

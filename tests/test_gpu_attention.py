@@ -123,7 +123,8 @@ def test_long_context_with_few_heads_selects_split_kv_path(device):
     assert actual is output and actual.data_ptr() == output.data_ptr()
     assert_close(actual, expected, 3e-3, 3e-3, "split")
     assert_close(one_pass, expected, 3e-3, 3e-3, "one pass")
-    assert selected == {"path": "split_kv", "split_size": 256, "num_splits": 8}
+    assert selected == {"path": "split_kv", "split_size": 256, "num_splits": 8,
+                        "waves_per_head": 4}
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -225,11 +226,28 @@ def test_llama3_long_context_split_kv(device):
             max_context_length=32768, workspace=workspace,
         )
         assert selected_attention_autotune_config() == {
-            "path": "split_kv", "split_size": 512, "num_splits": 64,
+            "path": "split_kv", "split_size": 512, "num_splits": 64, "waves_per_head": 1,
         }
     finally:
         set_attention_split_size(previous)
     _check_against_oracle(case, output.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, "cfg3")
+
+
+def test_llama3_long_context_auto_plan(device):
+    """BASELINE config 3 under the entry point's own plan: 4096-token
+    partitions with up to four wavefronts each (whole-row loads at D 128),
+    then the merge launch."""
+
+    case = llama3_long_context_case(seed=1)
+    gpu = case.to(device)
+    output = paged_gqa_decode_attention(
+        gpu.query, gpu.key_cache, gpu.value_cache, gpu.block_tables, gpu.context_lengths,
+        max_context_length=32768,
+    )
+    assert selected_attention_autotune_config() == {
+        "path": "split_kv", "split_size": 4096, "num_splits": 8, "waves_per_head": 4,
+    }
+    _check_against_oracle(case, output.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, "cfg3 auto")
 
 
 @pytest.mark.parametrize("block_size", [1, 4, 8, 12, 16, 32, 48])
