@@ -4,7 +4,8 @@ paged_gqa_decode_attention) and against the CPU oracle.
 
 The fused kernel rotates with the same arithmetic as the RoPE kernel, so the
 attention output and both caches must be bit-identical to the unfused pair,
-in one-pass and split-KV plans, with padded lanes that write nothing.  The
+in the wide and narrow one-pass plans and the narrow split-KV plan, with
+padded lanes that write nothing.  The
 oracle check (RoPE oracle, then the paged attention oracle over the updated
 caches) uses the north-star bar (max-abs 2e-2 + rel 1e-2).
 """
@@ -45,7 +46,7 @@ def _inputs(lengths, hq, hkv, d, dtype, seed, row_pad=0):
 @pytest.mark.parametrize(("hq", "hkv", "d", "dtype"),
                          [(32, 4, 64, torch.bfloat16), (8, 2, 32, torch.float16),
                           (32, 8, 128, torch.bfloat16), (16, 1, 64, torch.float16)])
-@pytest.mark.parametrize("rows", ["wide", "narrow"])
+@pytest.mark.parametrize("rows", ["wide", "narrow", "long"])
 def test_fused_rope_attention_equals_the_two_launches(device, hq, hkv, d, dtype, rows):
     generator = torch.Generator().manual_seed(hq + d)
     if rows == "wide":  # >= 192 (row, kv head) workgroups: the one-pass plan
@@ -53,8 +54,10 @@ def test_fused_rope_attention_equals_the_two_launches(device, hq, hkv, d, dtype,
         lengths = [int(x) for x in torch.randint(1, 700, (count,), generator=generator)]
         lengths[3] = 0
         lengths[7] = 1
-    else:  # few rows: split-KV with its merge launch
+    elif rows == "narrow":  # few rows, short: one pass, up to 8 wavefronts per kv head
         lengths = [700, 1, 0, 33, 512, 17]
+    else:  # few rows, long: split-KV with several wavefronts per split, merge launch
+        lengths = [3000, 1, 0, 1500, 2047, 17]
     case, qkv, positions, cos, sin, pages, offsets, active = _inputs(lengths, hq, hkv, d, dtype,
                                                                      seed=len(lengths) + d,
                                                                      row_pad=8)
