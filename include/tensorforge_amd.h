@@ -35,6 +35,8 @@
  *   tf_linear_partials_sum   K into fp32 partials and their row sum
  *   tf_linear_stream         the same projections staged through LDS with
  *                            whole-row loads (direct or split-K partials)
+ *   tf_linear_kstream        the same projections, K split over a 16-column
+ *                            workgroup's wavefronts (narrow weights)
  *   tf_linear_swiglu         the MLP's gate|up projection with its SwiGLU
  *                            (model/layers.py:144-158)
  *   tf_prefill_attention     prefill's causal attention (runtime/prefill.py:84-88, 109-118)
@@ -359,6 +361,19 @@ int32_t tf_linear_stream(const void *x, int64_t x_row_stride, const void *weight
                          int64_t weight_row_stride, void *y, int64_t y_row_stride,
                          float *partials, int32_t m, int32_t n, int32_t k, int32_t splits,
                          int32_t dtype, void *stream);
+
+/*
+ * y = round(x @ weight^T) for up to 64 rows with K split over the four
+ * wavefronts of a 16-column workgroup, each staging its k chunks of x and
+ * weight through LDS with whole-row loads: the form for weights with few
+ * 64-column tiles (a 2560-row qkv projection).  K % 32 == 0, 16-byte aligned
+ * x and weight rows, fp16/bf16.  Replaces the torch GEMM of the decode
+ * projections (tensorforge/model/layers.py:88-95) as the decode step calls
+ * them (tensorforge/runtime/decode_bucket.py:441-447).
+ */
+int32_t tf_linear_kstream(const void *x, int64_t x_row_stride, const void *weight,
+                          int64_t weight_row_stride, void *y, int64_t y_row_stride, int32_t m,
+                          int32_t n, int32_t k, int32_t dtype, void *stream);
 
 /*
  * The MLP's stacked gate|up projection and its SwiGLU in one launch:

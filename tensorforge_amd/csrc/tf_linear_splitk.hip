@@ -306,6 +306,156 @@ linear_stream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restr
     }
 }
 
+// ---------------------------------------------------------------------------
+// K-split form of the weight stream for narrow weights (few 64-column tiles,
+// e.g. a 2560-row qkv projection): a workgroup owns 16 output columns over
+// all of K and its four wavefronts take a quarter of K each.  Every
+// wavefront stages its own 128-wide k chunks of x (16 MT rows) and of the 16
+// weight rows in a private LDS region with whole-row loads (16 lanes per
+// 256-byte row piece), so the x re-reads (once per 16 columns) run at the
+// L2 rate of whole-line loads, and the four tiles meet once in LDS.  Chunk
+// rows are 256 bytes with pieces permuted by (piece ^ (row & 15)).
+// ---------------------------------------------------------------------------
+constexpr int kKStreamChunk = 128;
+
+__device__ __forceinline__ int kstream_lds_offset(int row, int piece) {
+  return row * kKStreamChunk + ((piece ^ (row & 15)) << 3);
+}
+
+template <typename T, int MT>
+__global__ void __launch_bounds__(256)
+linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restrict__ w,
+                      int64_t w_stride, T *__restrict__ y, int64_t y_stride, int32_t m,
+                      int32_t n, int32_t k, int32_t k_per_wave) {
+  using M = SplitMma<T>;
+  using vec8 = typename M::vec8;
+  constexpr int XR = 16 * MT;
+  constexpr int kLoadsX = XR / 4;  // 4 rows per load instruction (16 lanes per row)
+  constexpr int kLoadsW = 16 / 4;
+  constexpr int kWaveElems = (XR + 16) * kKStreamChunk;
+  extern __shared__ __attribute__((aligned(16))) unsigned char kstream_smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  T *xl = reinterpret_cast<T *>(kstream_smem) + wave * kWaveElems;  // [XR][128]
+  T *wl = xl + XR * kKStreamChunk;                                  // [16][128]
+  const int l16 = lane & 15;
+  const int q4 = lane >> 4;
+  const int32_t n0 = blockIdx.x * 16;
+  const int32_t k0 = min(wave * k_per_wave, k);
+  const int32_t k1 = min(k0 + k_per_wave, k);
+  const int lrow = lane >> 4;   // staging: lane loads piece lane % 16 of row 4 i + lane / 16
+  const int lpiece = lane & 15;
+
+  const T *xsrc[kLoadsX];
+#pragma unroll
+  for (int i = 0; i < kLoadsX; ++i)
+    xsrc[i] = x + static_cast<int64_t>(min(4 * i + lrow, m - 1)) * x_stride + 8 * lpiece;
+  const T *wsrc[kLoadsW];
+#pragma unroll
+  for (int i = 0; i < kLoadsW; ++i)
+    wsrc[i] = w + static_cast<int64_t>(min(n0 + 4 * i + lrow, n - 1)) * w_stride + 8 * lpiece;
+
+  vec8 xa[kLoadsX], wa[kLoadsW], xb[kLoadsX], wb[kLoadsW];
+  // Pieces past K read the row's first piece; those past the wavefront's
+  // range but inside K are read and unused.
+  auto load_chunk = [&](int32_t kk, vec8(&xr)[kLoadsX], vec8(&wr)[kLoadsW]) {
+    const int32_t c = kk + 8 * lpiece < k ? kk : -8 * lpiece;
+#pragma unroll
+    for (int i = 0; i < kLoadsX; ++i) xr[i] = *reinterpret_cast<const vec8 *>(xsrc[i] + c);
+#pragma unroll
+    for (int i = 0; i < kLoadsW; ++i) wr[i] = *reinterpret_cast<const vec8 *>(wsrc[i] + c);
+  };
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // The region is private to the wavefront, whose LDS requests are served in
+  // order: compiler barriers order the stores, the operand reads and the
+  // next chunk's stores.
+  auto stage_compute = [&](int32_t kk, const vec8(&xr)[kLoadsX], const vec8(&wr)[kLoadsW]) {
+    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < kLoadsX; ++i)
+      *reinterpret_cast<vec8 *>(xl + kstream_lds_offset(4 * i + lrow, lpiece)) = xr[i];
+#pragma unroll
+    for (int i = 0; i < kLoadsW; ++i)
+      *reinterpret_cast<vec8 *>(wl + kstream_lds_offset(4 * i + lrow, lpiece)) = wr[i];
+    __asm__ volatile("" ::: "memory");
+    const int32_t steps = min(kKStreamChunk, k1 - kk) >> 5;
+#pragma unroll
+    for (int st = 0; st < kKStreamChunk / 32; ++st) {
+      if (st >= steps) break;  // uniform
+      const int piece = 4 * st + q4;
+      const vec8 b = *reinterpret_cast<const vec8 *>(wl + kstream_lds_offset(l16, piece));
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = M::mma(*reinterpret_cast<const vec8 *>(xl + kstream_lds_offset(16 * mt + l16, piece)),
+                         b, acc[mt]);
+    }
+    __asm__ volatile("" ::: "memory");
+  };
+
+  constexpr int32_t C = kKStreamChunk;
+  if (k0 < k1) {
+    load_chunk(k0, xa, wa);
+    if (k0 + C < k1) load_chunk(k0 + C, xb, wb);
+    for (int32_t kk = k0; kk < k1; kk += 2 * C) {
+      stage_compute(kk, xa, wa);
+      if (kk + 2 * C < k1) load_chunk(kk + 2 * C, xa, wa);
+      if (kk + C >= k1) break;
+      stage_compute(kk + C, xb, wb);
+      if (kk + 3 * C < k1) load_chunk(kk + 3 * C, xb, wb);
+    }
+  }
+
+  // Sum the four wavefront tiles: item (mt, r, lane) is y[16 mt + 4 q4 + r][n0 + l16].
+  constexpr int kItems = MT * 4 * 64;
+  __syncthreads();  // every wavefront's operand reads are done
+  float *tiles = reinterpret_cast<float *>(kstream_smem);  // [4][kItems]
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) tiles[wave * kItems + (mt * 4 + r) * 64 + lane] = acc[mt][r];
+  __syncthreads();
+  for (int item = threadIdx.x; item < kItems; item += 256) {
+    const float sum = tiles[item] + tiles[kItems + item] + tiles[2 * kItems + item] +
+                      tiles[3 * kItems + item];
+    const int mt = item >> 8;
+    const int r = (item >> 6) & 3;
+    const int il = item & 63;
+    const int32_t row = 16 * mt + 4 * (il >> 4) + r;
+    const int32_t col = n0 + (il & 15);
+    if (row < m && col < n) y[static_cast<int64_t>(row) * y_stride + col] = from_float<T>(sum);
+  }
+}
+
+template <typename T, int MT>
+void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
+                    int64_t y_stride, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
+  const int32_t steps = k / 32;
+  const int32_t k_per_wave = ((steps + 3) / 4) * 32;
+  const size_t lds = static_cast<size_t>(4) * (16 * MT + 16) * kKStreamChunk * sizeof(T);
+  if (lds > 64 * 1024) {  // 80 KB at MT = 4: raise the launch's dynamic LDS limit once
+    static const hipError_t raised = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&linear_kstream_kernel<T, MT>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    (void)raised;
+  }
+  hipLaunchKernelGGL((linear_kstream_kernel<T, MT>), dim3((n + 15) / 16), dim3(256), lds, stream,
+                     static_cast<const T *>(x), x_stride, static_cast<const T *>(w), w_stride,
+                     static_cast<T *>(y), y_stride, m, n, k, k_per_wave);
+}
+
+template <typename T>
+void launch_kstream_mt(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
+                       int64_t y_stride, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
+  switch ((m + 15) / 16) {
+    case 1: launch_kstream<T, 1>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
+    case 2: launch_kstream<T, 2>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
+    case 3: launch_kstream<T, 3>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
+    default: launch_kstream<T, 4>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
+  }
+}
+
 template <typename T, int MT, bool SWIGLU>
 void launch_stream(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
                    int64_t y_stride, float *partials, int32_t m, int32_t n, int32_t k,
@@ -518,4 +668,33 @@ extern "C" int32_t tf_linear_swiglu(const void *x, int64_t x_row_stride, const v
   return tf::linear_stream_entry(x, x_row_stride, gate_up_weight, weight_row_stride, y,
                                  y_row_stride, nullptr, m, intermediate, k, 1, dtype, stream,
                                  true, "linear_swiglu");
+}
+
+extern "C" int32_t tf_linear_kstream(const void *x, int64_t x_row_stride, const void *weight,
+                                     int64_t weight_row_stride, void *y, int64_t y_row_stride,
+                                     int32_t m, int32_t n, int32_t k, int32_t dtype, void *stream) {
+  using namespace tf;
+  clear_error();
+  if (dtype != TF_DTYPE_FLOAT16 && dtype != TF_DTYPE_BFLOAT16)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_kstream supports fp16 and bf16");
+  if (m < 0 || n < 0 || k < 0) return fail(TF_ERROR_INVALID_ARGUMENT, "sizes must be non-negative");
+  if (m > 64) return fail(TF_ERROR_UNSUPPORTED, "linear_kstream supports at most 64 rows");
+  if (k % 32 != 0 || k == 0)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_kstream needs K to be a positive multiple of 32");
+  if (x_row_stride < k || weight_row_stride < k || y_row_stride < n)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "row strides are shorter than the rows");
+  if (n > 65535 * 16) return fail(TF_ERROR_UNSUPPORTED, "grid too large");
+  if (m == 0 || n == 0) return TF_SUCCESS;
+  if (!x || !weight || !y) return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
+                          static_cast<uintptr_t>(x_row_stride * 2) |
+                          static_cast<uintptr_t>(weight_row_stride * 2);
+  if (align % 16 != 0)
+    return fail(TF_ERROR_UNSUPPORTED, "linear_kstream needs 16-byte aligned x and weight rows");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TF_DTYPE_BFLOAT16)
+    launch_kstream_mt<__bf16>(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, m, n, k, s);
+  else
+    launch_kstream_mt<_Float16>(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, m, n, k, s);
+  return check_launch("linear_kstream");
 }

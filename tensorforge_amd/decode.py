@@ -44,6 +44,7 @@ from tensorforge_amd import _native
 from tensorforge_amd.cache import AppendReservation, PagedKVCache
 from tensorforge_amd.kernels import (
     PagedAttentionWorkspace,
+    linear_kstream,
     linear_rows,
     linear_rows_supported,
     linear_stream,
@@ -167,16 +168,20 @@ def _project(x: Tensor, weight: Tensor, output: Tensor | None = None) -> Tensor:
     >= 8192 rows (the stacked gate|up) up to 16 rows go through the
     LDS-staged weight stream (linear_stream: 24.6-25.0 us against 30.4-30.7
     for hipBLASLt at 32000 x 2048; 12.6-12.8 us against 12.5-14.7 at
-    11264 x 2048).  Other weights up to 16 rows use the K-split MFMA kernel
-    (linear_rows) when small (<= 8M elements: the q/k/v and o projections),
-    where the library GEMM launches too few workgroups; otherwise
-    hipBLASLt."""
+    11264 x 2048).  Narrower weights with K >= 1024 (the stacked q/k/v)
+    take the K-split weight stream (linear_kstream: 5.2-9.4 us at 1..64 rows
+    against 5.7-12.7 for linear_rows and 11.1-11.9 for hipBLASLt at
+    2560 x 2048).  Other weights up to 16 rows use the K-split MFMA kernel
+    (linear_rows) when small (<= 8M elements), where the library GEMM
+    launches too few workgroups; otherwise hipBLASLt."""
 
     rows = x.shape[0]
     if (linear_rows_supported(x, weight)
             and ((weight.shape[0] >= 16384 and rows <= 32)
                  or (weight.shape[0] >= 8192 and rows <= 16))):
         return linear_stream(x, weight, output=output)
+    if linear_rows_supported(x, weight) and weight.shape[0] < 8192 and weight.shape[1] >= 1024:
+        return linear_kstream(x, weight, output=output)
     rows_kernel = (rows <= 16 and linear_rows_supported(x, weight)
                    and (weight.numel() <= 8 * 1024 * 1024 or weight.shape[0] >= 16384
                         or (rows <= 8 and weight.shape[0] >= 8192)))

@@ -17,6 +17,7 @@ from tensorforge_amd.kernels.cache_write import paged_kv_write_slots, paged_kv_w
 from tensorforge_amd.kernels.linear import (
     linear_partials,
     linear_partials_sum,
+    linear_kstream,
     linear_stream,
     linear_swiglu,
     linear_rows,
@@ -40,6 +41,7 @@ __all__ = [
     "is_hip_available",
     "linear_partials",
     "linear_partials_sum",
+    "linear_kstream",
     "linear_stream",
     "linear_swiglu",
     "linear_rows",

@@ -168,6 +168,37 @@ def linear_stream(x: Tensor, weight: Tensor, *, splits: int = 1, output: Tensor 
     return result
 
 
+def linear_kstream(x: Tensor, weight: Tensor, *, output: Tensor | None = None) -> Tensor:
+    """``x [m, k] @ weight[n, k].T`` for m <= 64 with K split over the four
+    wavefronts of 16-column workgroups, each staging its chunks through LDS
+    with whole-row loads (the form for weights with few 64-column tiles)."""
+
+    if not _native.is_available():
+        raise RuntimeError(
+            "the gfx950 kernel library is unavailable; build it with "
+            "`python -m tensorforge_amd.build`"
+        )
+    if not linear_rows_supported(x, weight):
+        raise ValueError("linear_kstream needs fp16/bf16 CUDA operands [m <= 64, k] and [n, k] "
+                         "with k % 32 == 0 and 16-byte aligned contiguous rows")
+    m, k = x.shape
+    n = weight.shape[0]
+    if output is None:
+        output = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    if (output.shape != (m, n) or output.dtype != x.dtype or output.device != x.device
+            or output.stride(1) != 1):
+        raise ValueError("output must be [m, n] with contiguous rows, x's dtype and device")
+    _native.check(
+        _native.library().tf_linear_kstream(
+            x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), output.data_ptr(),
+            output.stride(0), m, n, k, _native.dtype_code(x.dtype),
+            _native.current_stream(x.device),
+        ),
+        "linear_kstream",
+    )
+    return output
+
+
 def linear_swiglu(x: Tensor, gate_up_weight: Tensor, *, output: Tensor | None = None) -> Tensor:
     """``swiglu(x @ gate.T, x @ up.T)`` for m <= 64 rows, with
     ``gate_up_weight`` stacking the gate rows over the up rows (``[2I, k]``)

@@ -157,6 +157,29 @@ def test_linear_swiglu_equals_projection_then_activation(device, dtype, rows, in
                                atol=tol * float(expected.abs().max()))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 17, 33, 64])
+@pytest.mark.parametrize(("n", "k"), [(2560, 2048), (100, 96), (48, 800), (256, 4128)])
+def test_linear_kstream_matches_fp32(device, dtype, rows, n, k):
+    """K split over a 16-column workgroup's wavefronts: within the storage
+    bar of the fp32 product, on tail column tiles, K that ends inside a
+    chunk or leaves a wavefront without work (K = 96: 3 k-steps for 4
+    wavefronts) and strided output rows."""
+
+    from tensorforge_amd.kernels import linear_kstream
+
+    generator = torch.Generator().manual_seed(rows * 19 + n + k)
+    x = torch.randn(rows, k, generator=generator).to(dtype)
+    w = (torch.randn(n, k, generator=generator) * 0.02).to(dtype)
+    out_wide = torch.full((rows, n + 8), float("nan"), dtype=dtype, device=device)
+    linear_kstream(x.to(device), w.to(device), output=out_wide[:, :n])
+    expected = x.float() @ w.float().T
+    tol = TOLERANCE[dtype]
+    torch.testing.assert_close(out_wide[:, :n].float().cpu(), expected, rtol=tol,
+                               atol=tol * float(expected.abs().max()))
+    assert bool(out_wide[:, n:].isnan().all())
+
+
 def test_linear_stream_strided_rows_and_rejections(device):
     from tensorforge_amd.kernels import linear_stream
 
