@@ -37,6 +37,7 @@
  *                            whole-row loads (direct or split-K partials)
  *   tf_linear_kstream        the same projections, K split over a 16-column
  *                            workgroup's wavefronts (narrow weights)
+ *   tf_linear_kswiglu        its K-split form
  *   tf_linear_swiglu         the MLP's gate|up projection with its SwiGLU
  *                            (model/layers.py:144-158)
  *   tf_prefill_attention     prefill's causal attention (runtime/prefill.py:84-88, 109-118)
@@ -374,6 +375,16 @@ int32_t tf_linear_stream(const void *x, int64_t x_row_stride, const void *weight
 int32_t tf_linear_kstream(const void *x, int64_t x_row_stride, const void *weight,
                           int64_t weight_row_stride, void *y, int64_t y_row_stride, int32_t m,
                           int32_t n, int32_t k, int32_t dtype, void *stream);
+
+/*
+ * tf_linear_swiglu's result (the stacked gate|up projection and its SwiGLU,
+ * bit for bit tf_linear_kstream of the stacked weight followed by
+ * tf_swiglu_rows) with K split over the four wavefronts of a workgroup of
+ * 16 activation columns: the form for 33..64 rows, where x is large.
+ */
+int32_t tf_linear_kswiglu(const void *x, int64_t x_row_stride, const void *gate_up_weight,
+                          int64_t weight_row_stride, void *y, int64_t y_row_stride, int32_t m,
+                          int32_t intermediate, int32_t k, int32_t dtype, void *stream);
 
 /*
  * The MLP's stacked gate|up projection and its SwiGLU in one launch:

@@ -308,21 +308,27 @@ linear_stream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restr
 
 // ---------------------------------------------------------------------------
 // K-split form of the weight stream for narrow weights (few 64-column tiles,
-// e.g. a 2560-row qkv projection): a workgroup owns 16 output columns over
-// all of K and its four wavefronts take a quarter of K each.  Every
-// wavefront stages its own 128-wide k chunks of x (16 MT rows) and of the 16
-// weight rows in a private LDS region with whole-row loads (16 lanes per
-// 256-byte row piece), so the x re-reads (once per 16 columns) run at the
-// L2 rate of whole-line loads, and the four tiles meet once in LDS.  Chunk
-// rows are 256 bytes with pieces permuted by (piece ^ (row & 15)).
+// e.g. a 2560-row qkv projection) and for the gate|up + SwiGLU launch: a
+// workgroup owns 16 output columns over all of K and its four wavefronts
+// take a quarter of K each.  Every wavefront stages its own KC-wide k
+// chunks of x (16 MT rows) and of its weight rows in a private LDS region
+// with whole-row loads (KC / 8 lanes per row piece), so the x re-reads (once
+// per 16 columns) run at the L2 rate of whole-line loads, and the four
+// tiles meet once in LDS.
 // ---------------------------------------------------------------------------
-constexpr int kKStreamChunk = 128;
-
+// Chunk rows are KC * 2 bytes; pieces are permuted by (piece ^ (row & mask))
+// with mask = min(KC / 8, 16) - 1.
+template <int KC>
 __device__ __forceinline__ int kstream_lds_offset(int row, int piece) {
-  return row * kKStreamChunk + ((piece ^ (row & 15)) << 3);
+  constexpr int kMask = (KC / 8 < 16 ? KC / 8 : 16) - 1;
+  return row * KC + ((piece ^ (row & kMask)) << 3);
 }
 
-template <typename T, int MT>
+// SWIGLU: the workgroup's 16 columns j are activation columns; the weight
+// stacks gate rows [0, n) over up rows [n, 2n), each wavefront accumulates
+// both tiles over its quarter of K, and the output is
+// round(swiglu_act(round(g), round(u))).
+template <typename T, int MT, int KC, bool SWIGLU>
 __global__ void __launch_bounds__(256)
 linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restrict__ w,
                       int64_t w_stride, T *__restrict__ y, int64_t y_stride, int32_t m,
@@ -330,30 +336,37 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
   using M = SplitMma<T>;
   using vec8 = typename M::vec8;
   constexpr int XR = 16 * MT;
-  constexpr int kLoadsX = XR / 4;  // 4 rows per load instruction (16 lanes per row)
-  constexpr int kLoadsW = 16 / 4;
-  constexpr int kWaveElems = (XR + 16) * kKStreamChunk;
+  constexpr int WR = SWIGLU ? 32 : 16;
+  constexpr int kLanesPerRow = KC / 8;
+  constexpr int kRowsPerLoad = 64 / kLanesPerRow;
+  constexpr int kLoadsX = XR / kRowsPerLoad;
+  constexpr int kLoadsW = WR / kRowsPerLoad;
+  constexpr int kWaveElems = (XR + WR) * KC;
   extern __shared__ __attribute__((aligned(16))) unsigned char kstream_smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  T *xl = reinterpret_cast<T *>(kstream_smem) + wave * kWaveElems;  // [XR][128]
-  T *wl = xl + XR * kKStreamChunk;                                  // [16][128]
+  T *xl = reinterpret_cast<T *>(kstream_smem) + wave * kWaveElems;  // [XR][KC]
+  T *wl = xl + XR * KC;                                             // [WR][KC]
   const int l16 = lane & 15;
   const int q4 = lane >> 4;
   const int32_t n0 = blockIdx.x * 16;
   const int32_t k0 = min(wave * k_per_wave, k);
   const int32_t k1 = min(k0 + k_per_wave, k);
-  const int lrow = lane >> 4;   // staging: lane loads piece lane % 16 of row 4 i + lane / 16
-  const int lpiece = lane & 15;
+  const int lrow = lane / kLanesPerRow;  // staging: piece lane % (KC/8) of row R i + lane / (KC/8)
+  const int lpiece = lane % kLanesPerRow;
 
   const T *xsrc[kLoadsX];
 #pragma unroll
   for (int i = 0; i < kLoadsX; ++i)
-    xsrc[i] = x + static_cast<int64_t>(min(4 * i + lrow, m - 1)) * x_stride + 8 * lpiece;
+    xsrc[i] = x + static_cast<int64_t>(min(kRowsPerLoad * i + lrow, m - 1)) * x_stride + 8 * lpiece;
   const T *wsrc[kLoadsW];
 #pragma unroll
-  for (int i = 0; i < kLoadsW; ++i)
-    wsrc[i] = w + static_cast<int64_t>(min(n0 + 4 * i + lrow, n - 1)) * w_stride + 8 * lpiece;
+  for (int i = 0; i < kLoadsW; ++i) {
+    const int tr = kRowsPerLoad * i + lrow;  // tile row
+    const int64_t row = SWIGLU ? (tr < 16 ? 0 : n) + min(n0 + (tr & 15), n - 1)
+                               : min(n0 + tr, n - 1);
+    wsrc[i] = w + row * w_stride + 8 * lpiece;
+  }
 
   vec8 xa[kLoadsX], wa[kLoadsW], xb[kLoadsX], wb[kLoadsW];
   // Pieces past K read the row's first piece; those past the wavefront's
@@ -365,9 +378,11 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
 #pragma unroll
     for (int i = 0; i < kLoadsW; ++i) wr[i] = *reinterpret_cast<const vec8 *>(wsrc[i] + c);
   };
-  f32x4 acc[MT];
+  f32x4 acc[MT], accu[SWIGLU ? MT : 1];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int mt = 0; mt < (SWIGLU ? MT : 1); ++mt) accu[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   // The region is private to the wavefront, whose LDS requests are served in
   // order: compiler barriers order the stores, the operand reads and the
   // next chunk's stores.
@@ -375,84 +390,107 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
     __asm__ volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < kLoadsX; ++i)
-      *reinterpret_cast<vec8 *>(xl + kstream_lds_offset(4 * i + lrow, lpiece)) = xr[i];
+      *reinterpret_cast<vec8 *>(xl + kstream_lds_offset<KC>(kRowsPerLoad * i + lrow, lpiece)) = xr[i];
 #pragma unroll
     for (int i = 0; i < kLoadsW; ++i)
-      *reinterpret_cast<vec8 *>(wl + kstream_lds_offset(4 * i + lrow, lpiece)) = wr[i];
+      *reinterpret_cast<vec8 *>(wl + kstream_lds_offset<KC>(kRowsPerLoad * i + lrow, lpiece)) = wr[i];
     __asm__ volatile("" ::: "memory");
-    const int32_t steps = min(kKStreamChunk, k1 - kk) >> 5;
+    const int32_t steps = min(KC, k1 - kk) >> 5;
 #pragma unroll
-    for (int st = 0; st < kKStreamChunk / 32; ++st) {
+    for (int st = 0; st < KC / 32; ++st) {
       if (st >= steps) break;  // uniform
       const int piece = 4 * st + q4;
-      const vec8 b = *reinterpret_cast<const vec8 *>(wl + kstream_lds_offset(l16, piece));
+      const vec8 b = *reinterpret_cast<const vec8 *>(wl + kstream_lds_offset<KC>(l16, piece));
+      vec8 bu;
+      if constexpr (SWIGLU)
+        bu = *reinterpret_cast<const vec8 *>(wl + kstream_lds_offset<KC>(16 + l16, piece));
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        acc[mt] = M::mma(*reinterpret_cast<const vec8 *>(xl + kstream_lds_offset(16 * mt + l16, piece)),
-                         b, acc[mt]);
+      for (int mt = 0; mt < MT; ++mt) {
+        const vec8 a = *reinterpret_cast<const vec8 *>(xl + kstream_lds_offset<KC>(16 * mt + l16, piece));
+        acc[mt] = M::mma(a, b, acc[mt]);
+        if constexpr (SWIGLU) accu[mt] = M::mma(a, bu, accu[mt]);
+      }
     }
     __asm__ volatile("" ::: "memory");
   };
 
-  constexpr int32_t C = kKStreamChunk;
   if (k0 < k1) {
     load_chunk(k0, xa, wa);
-    if (k0 + C < k1) load_chunk(k0 + C, xb, wb);
-    for (int32_t kk = k0; kk < k1; kk += 2 * C) {
+    if (k0 + KC < k1) load_chunk(k0 + KC, xb, wb);
+    for (int32_t kk = k0; kk < k1; kk += 2 * KC) {
       stage_compute(kk, xa, wa);
-      if (kk + 2 * C < k1) load_chunk(kk + 2 * C, xa, wa);
-      if (kk + C >= k1) break;
-      stage_compute(kk + C, xb, wb);
-      if (kk + 3 * C < k1) load_chunk(kk + 3 * C, xb, wb);
+      if (kk + 2 * KC < k1) load_chunk(kk + 2 * KC, xa, wa);
+      if (kk + KC >= k1) break;
+      stage_compute(kk + KC, xb, wb);
+      if (kk + 3 * KC < k1) load_chunk(kk + 3 * KC, xb, wb);
     }
   }
 
   // Sum the four wavefront tiles: item (mt, r, lane) is y[16 mt + 4 q4 + r][n0 + l16].
   constexpr int kItems = MT * 4 * 64;
+  constexpr int kTiles = SWIGLU ? 2 : 1;
   __syncthreads();  // every wavefront's operand reads are done
-  float *tiles = reinterpret_cast<float *>(kstream_smem);  // [4][kItems]
+  float *tiles = reinterpret_cast<float *>(kstream_smem);  // [4 waves][kTiles][kItems]
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) tiles[wave * kItems + (mt * 4 + r) * 64 + lane] = acc[mt][r];
+    for (int r = 0; r < 4; ++r) {
+      tiles[(wave * kTiles) * kItems + (mt * 4 + r) * 64 + lane] = acc[mt][r];
+      if constexpr (SWIGLU) tiles[(wave * kTiles + 1) * kItems + (mt * 4 + r) * 64 + lane] = accu[mt][r];
+    }
   __syncthreads();
   for (int item = threadIdx.x; item < kItems; item += 256) {
-    const float sum = tiles[item] + tiles[kItems + item] + tiles[2 * kItems + item] +
-                      tiles[3 * kItems + item];
+    float sum = 0.f, sumu = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < 4; ++wv) {
+      sum += tiles[(wv * kTiles) * kItems + item];
+      if constexpr (SWIGLU) sumu += tiles[(wv * kTiles + 1) * kItems + item];
+    }
     const int mt = item >> 8;
     const int r = (item >> 6) & 3;
     const int il = item & 63;
     const int32_t row = 16 * mt + 4 * (il >> 4) + r;
     const int32_t col = n0 + (il & 15);
-    if (row < m && col < n) y[static_cast<int64_t>(row) * y_stride + col] = from_float<T>(sum);
+    if (row >= m || col >= n) continue;
+    T out;
+    if constexpr (SWIGLU)
+      out = from_float<T>(swiglu_act(to_float(from_float<T>(sum)), to_float(from_float<T>(sumu))));
+    else
+      out = from_float<T>(sum);
+    y[static_cast<int64_t>(row) * y_stride + col] = out;
   }
 }
 
-template <typename T, int MT>
+template <typename T, int MT, int KC, bool SWIGLU>
 void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
                     int64_t y_stride, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
   const int32_t steps = k / 32;
   const int32_t k_per_wave = ((steps + 3) / 4) * 32;
-  const size_t lds = static_cast<size_t>(4) * (16 * MT + 16) * kKStreamChunk * sizeof(T);
-  if (lds > 64 * 1024) {  // 80 KB at MT = 4: raise the launch's dynamic LDS limit once
+  const size_t lds =
+      static_cast<size_t>(4) * (16 * MT + (SWIGLU ? 32 : 16)) * KC * sizeof(T);
+  if (lds > 64 * 1024) {  // raise the launch's dynamic LDS limit once
     static const hipError_t raised = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&linear_kstream_kernel<T, MT>),
+        reinterpret_cast<const void *>(&linear_kstream_kernel<T, MT, KC, SWIGLU>),
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     (void)raised;
   }
-  hipLaunchKernelGGL((linear_kstream_kernel<T, MT>), dim3((n + 15) / 16), dim3(256), lds, stream,
-                     static_cast<const T *>(x), x_stride, static_cast<const T *>(w), w_stride,
-                     static_cast<T *>(y), y_stride, m, n, k, k_per_wave);
+  hipLaunchKernelGGL((linear_kstream_kernel<T, MT, KC, SWIGLU>), dim3((n + 15) / 16), dim3(256),
+                     lds, stream, static_cast<const T *>(x), x_stride, static_cast<const T *>(w),
+                     w_stride, static_cast<T *>(y), y_stride, m, n, k, k_per_wave);
 }
 
-template <typename T>
+// Chunk 128 for a plain projection (80 KB of LDS at 64 rows: one workgroup
+// per compute unit, enough for a 160-workgroup qkv), 64 for the SwiGLU form
+// (48 KB: several of its 352 TinyLlama workgroups share a compute unit).
+template <typename T, bool SWIGLU>
 void launch_kstream_mt(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
                        int64_t y_stride, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
+  constexpr int KC = SWIGLU ? 64 : 128;
   switch ((m + 15) / 16) {
-    case 1: launch_kstream<T, 1>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
-    case 2: launch_kstream<T, 2>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
-    case 3: launch_kstream<T, 3>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
-    default: launch_kstream<T, 4>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
+    case 1: launch_kstream<T, 1, KC, SWIGLU>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
+    case 2: launch_kstream<T, 2, KC, SWIGLU>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
+    case 3: launch_kstream<T, 3, KC, SWIGLU>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
+    default: launch_kstream<T, 4, KC, SWIGLU>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
   }
 }
 
@@ -670,10 +708,13 @@ extern "C" int32_t tf_linear_swiglu(const void *x, int64_t x_row_stride, const v
                                  true, "linear_swiglu");
 }
 
-extern "C" int32_t tf_linear_kstream(const void *x, int64_t x_row_stride, const void *weight,
-                                     int64_t weight_row_stride, void *y, int64_t y_row_stride,
-                                     int32_t m, int32_t n, int32_t k, int32_t dtype, void *stream) {
-  using namespace tf;
+namespace tf {
+namespace {
+
+int32_t kstream_entry(const void *x, int64_t x_row_stride, const void *weight,
+                      int64_t weight_row_stride, void *y, int64_t y_row_stride, int32_t m,
+                      int32_t n, int32_t k, int32_t dtype, void *stream, bool swiglu,
+                      const char *name) {
   clear_error();
   if (dtype != TF_DTYPE_FLOAT16 && dtype != TF_DTYPE_BFLOAT16)
     return fail(TF_ERROR_UNSUPPORTED, "linear_kstream supports fp16 and bf16");
@@ -692,9 +733,32 @@ extern "C" int32_t tf_linear_kstream(const void *x, int64_t x_row_stride, const 
   if (align % 16 != 0)
     return fail(TF_ERROR_UNSUPPORTED, "linear_kstream needs 16-byte aligned x and weight rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == TF_DTYPE_BFLOAT16)
-    launch_kstream_mt<__bf16>(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, m, n, k, s);
-  else
-    launch_kstream_mt<_Float16>(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, m, n, k, s);
-  return check_launch("linear_kstream");
+#define TF_KSTREAM_LAUNCH(T, G) \
+  launch_kstream_mt<T, G>(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, m, n, k, s)
+  if (dtype == TF_DTYPE_BFLOAT16) {
+    if (swiglu) TF_KSTREAM_LAUNCH(__bf16, true); else TF_KSTREAM_LAUNCH(__bf16, false);
+  } else {
+    if (swiglu) TF_KSTREAM_LAUNCH(_Float16, true); else TF_KSTREAM_LAUNCH(_Float16, false);
+  }
+#undef TF_KSTREAM_LAUNCH
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace tf
+
+extern "C" int32_t tf_linear_kstream(const void *x, int64_t x_row_stride, const void *weight,
+                                     int64_t weight_row_stride, void *y, int64_t y_row_stride,
+                                     int32_t m, int32_t n, int32_t k, int32_t dtype, void *stream) {
+  return tf::kstream_entry(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, m, n, k,
+                           dtype, stream, false, "linear_kstream");
+}
+
+extern "C" int32_t tf_linear_kswiglu(const void *x, int64_t x_row_stride,
+                                     const void *gate_up_weight, int64_t weight_row_stride,
+                                     void *y, int64_t y_row_stride, int32_t m,
+                                     int32_t intermediate, int32_t k, int32_t dtype,
+                                     void *stream) {
+  return tf::kstream_entry(x, x_row_stride, gate_up_weight, weight_row_stride, y, y_row_stride,
+                           m, intermediate, k, dtype, stream, true, "linear_kswiglu");
 }

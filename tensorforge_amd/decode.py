@@ -294,12 +294,12 @@ class DecodeGraphBucket:
                                               dtype=torch.float32, device=device)
                 self.partials_down = torch.empty((self.split_down, b, config.hidden_size),
                                                  dtype=torch.float32, device=device)
-        # The MLP's gate|up projection with SwiGLU in its epilogue up to 32
-        # rows (TinyLlama 11264 x 2048: 12.7-14.8 us against 14.1-16.8 for
-        # the best projection + SwiGLU pair; at 64 rows hipBLASLt + SwiGLU
-        # stays ahead, 18.5 against 19.1 us).
+        # The MLP's gate|up projection with SwiGLU in its epilogue, K split
+        # over 16-column workgroups (TinyLlama 11264 x 2048: 11.0-13.9 us at
+        # 1..32 rows and 18.2 at 64, against 14.7-16.8 and 18.8 for the best
+        # projection + SwiGLU pair).
         probe_h = torch.empty((b, config.hidden_size), dtype=dtype, device=device)
-        self.fused_gate_up = b <= 32 and linear_rows_supported(probe_h, layer0.gate_up)
+        self.fused_gate_up = linear_rows_supported(probe_h, layer0.gate_up)
         self._graph: torch.cuda.CUDAGraph | None = None
 
     def addresses(self) -> dict[str, int]:
@@ -455,7 +455,8 @@ class DecodeGraphBucket:
                                                     residual_output=torch.empty_like(attn),
                                                     norm_output=self.norm_output)
                 if self.fused_gate_up:
-                    act = linear_swiglu(h, layer.gate_up, output=self.swiglu_output)
+                    act = linear_swiglu(h, layer.gate_up, output=self.swiglu_output,
+                                        k_split=True)
                 else:
                     act = swiglu_gate_up(_project(h, layer.gate_up), output=self.swiglu_output)
                 next_norm = (self.weights.layers[index + 1].input_norm

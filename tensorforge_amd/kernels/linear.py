@@ -199,13 +199,16 @@ def linear_kstream(x: Tensor, weight: Tensor, *, output: Tensor | None = None) -
     return output
 
 
-def linear_swiglu(x: Tensor, gate_up_weight: Tensor, *, output: Tensor | None = None) -> Tensor:
+def linear_swiglu(x: Tensor, gate_up_weight: Tensor, *, output: Tensor | None = None,
+                  k_split: bool = False) -> Tensor:
     """``swiglu(x @ gate.T, x @ up.T)`` for m <= 64 rows, with
     ``gate_up_weight`` stacking the gate rows over the up rows (``[2I, k]``)
-    -- the stacked projection and its activation in one launch, bit-identical
-    to :func:`linear_stream` of the stacked weight followed by
-    ``swiglu_gate_up``.  Returns ``[m, I]`` in ``output`` (allocated when
-    None)."""
+    -- the stacked projection and its activation in one launch.  The default
+    form is bit-identical to :func:`linear_stream` of the stacked weight
+    followed by ``swiglu_gate_up``; ``k_split=True`` splits K over the
+    wavefronts of 16-column workgroups (bit-identical to
+    :func:`linear_kstream` followed by ``swiglu_gate_up``).  Returns
+    ``[m, I]`` in ``output`` (allocated when None)."""
 
     if not _native.is_available():
         raise RuntimeError(
@@ -222,13 +225,14 @@ def linear_swiglu(x: Tensor, gate_up_weight: Tensor, *, output: Tensor | None = 
     if (output.shape != (m, inter) or output.dtype != x.dtype or output.device != x.device
             or output.stride(1) != 1):
         raise ValueError("output must be [m, I] with contiguous rows, x's dtype and device")
+    entry = "tf_linear_kswiglu" if k_split else "tf_linear_swiglu"
     _native.check(
-        _native.library().tf_linear_swiglu(
+        getattr(_native.library(), entry)(
             x.data_ptr(), x.stride(0), gate_up_weight.data_ptr(), gate_up_weight.stride(0),
             output.data_ptr(), output.stride(0), m, inter, k, _native.dtype_code(x.dtype),
             _native.current_stream(x.device),
         ),
-        "linear_swiglu",
+        entry,
     )
     return output
 

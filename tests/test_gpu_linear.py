@@ -180,6 +180,31 @@ def test_linear_kstream_matches_fp32(device, dtype, rows, n, k):
     assert bool(out_wide[:, n:].isnan().all())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 33, 64])
+@pytest.mark.parametrize(("inter", "k"), [(5632, 2048), (100, 800), (48, 96)])
+def test_linear_kswiglu_equals_kstream_then_activation(device, dtype, rows, inter, k):
+    """The K-split gate|up + SwiGLU launch is bit-identical to linear_kstream
+    of the stacked weight followed by swiglu_gate_up, and within the storage
+    bar of the fp32 reference."""
+
+    from tensorforge_amd.kernels import linear_kstream, linear_swiglu, swiglu_gate_up
+
+    generator = torch.Generator().manual_seed(rows * 23 + inter + k)
+    x = torch.randn(rows, k, generator=generator).to(dtype).to(device)
+    w = (torch.randn(2 * inter, k, generator=generator) * 0.05).to(dtype).to(device)
+    want = swiglu_gate_up(linear_kstream(x, w))
+    got = torch.full((rows, inter), float("nan"), dtype=dtype, device=device)
+    linear_swiglu(x, w, output=got, k_split=True)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    gu = (x.float() @ w.float().T).to(dtype).float().cpu()
+    g, u = gu[:, :inter], gu[:, inter:]
+    expected = g * torch.sigmoid(g) * u
+    tol = TOLERANCE[dtype]
+    torch.testing.assert_close(got.float().cpu(), expected, rtol=tol,
+                               atol=tol * float(expected.abs().max()))
+
+
 def test_linear_stream_strided_rows_and_rejections(device):
     from tensorforge_amd.kernels import linear_stream
 
