@@ -179,6 +179,19 @@ class AttentionPlan:
                 | ((self.tokens_per_wave // 64) << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
 
 
+def wide_tokens_per_wave(max_context_length: int) -> int:
+    """Token budget per wavefront of a wide one-pass call: 576 above 1536
+    tokens (config 2's ragged rows up to 2k: four wavefronts for the
+    longest), else about a quarter of the context and at least 128, so a
+    row gets ~4 wavefronts (measured on MI355X with the fused RoPE + append
+    at 64 rows: 512 tokens 9.5 us with 4 against 13.7 with 1; 1000 tokens
+    16.3 us with 4 against 17.0 with 2)."""
+
+    if max_context_length > 1536:
+        return ONE_PASS_TOKENS_PER_WAVE
+    return max(128, (-(-max_context_length // 4) + 63) // 64 * 64)
+
+
 def narrow_split_size_for(max_context_length: int, batch: int, kv_heads: int) -> int:
     """Partition size of a narrow split-KV call with several wavefronts per
     split: the smallest size >= 256 that keeps the grid near 256 (row, kv
@@ -205,10 +218,10 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
     geometry unless noted):
 
     * at least 192 (row, kv head) workgroups and no caller-fixed partition
-      size: one pass, each workgroup splitting its row over ceil(L / 576)
-      (at most 8) wavefronts that combine in LDS -- no partials, no merge
-      launch (72 rows x 4 kv heads x 2k: 21.3 us against 26.0 us for split
-      576 plus merge);
+      size: one pass, each workgroup splitting its row over up to 8
+      wavefronts (one per wide_tokens_per_wave tokens of the row) that
+      combine in LDS -- no partials, no merge launch (72 rows x 4 kv heads
+      x 2k: 21.3 us against 26.0 us for split 576 plus merge);
     * fewer workgroups, context <= 1024 (or <= 2048 with >= 128 workgroups):
       one pass with up to 8 wavefronts per kv head, one per 64 tokens of a
       row (1-16 rows x 1k: 9.8-10.1 us against 12.5-12.9 for 256-token
@@ -233,8 +246,9 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
             return AttentionPlan(True, capacity32, 1, 1)
         return AttentionPlan(False, split_size, (launch_context + split_size - 1) // split_size, 1)
     if workgroups >= ONE_PASS_MIN_WORKGROUPS:
-        waves = max(1, min(8, -(-launch_context // ONE_PASS_TOKENS_PER_WAVE)))
-        return AttentionPlan(True, capacity32, 1, waves)
+        tokens = wide_tokens_per_wave(launch_context)
+        waves = max(1, min(8, -(-launch_context // tokens)))
+        return AttentionPlan(True, capacity32, 1, waves, tokens)
     if (attention_path == "one_pass" or launch_context <= NARROW_ONE_PASS_CONTEXT
             or (workgroups >= NARROW_ONE_PASS_MIN_WORKGROUPS and launch_context <= 2048)):
         return AttentionPlan(True, capacity32, 1, NARROW_WAVES, NARROW_TOKENS_PER_WAVE)

@@ -269,7 +269,10 @@ def test_attention_plan() -> None:
     assert narrow_split_size_for(32768, 1, 4) == 2048  # at most 16 splits per row
     assert narrow_split_size_for(4000, 1, 4) == 256
     assert attention_plan(4096, 64, 4, 4096).waves_per_head == 8
-    assert attention_plan(1024, 64, 4, 1024).waves_per_head == 2
+    mid = attention_plan(1024, 64, 4, 1024)  # ~4 wavefronts per row below 1.5k
+    assert (mid.waves_per_head, mid.tokens_per_wave) == (4, 256)
+    assert attention_plan(512, 64, 4, 512).tokens_per_wave == 128
+    assert attention_plan(100, 64, 4, 128).flags == 0  # one wavefront
     assert attention_plan(32768, 64, 4, 32768).waves_per_head == 8
     forced = attention_plan(2048, 72, 4, 2048, "split_kv")
     assert (forced.one_pass, forced.split_size, forced.waves_per_head) == (False, 576, 1)
