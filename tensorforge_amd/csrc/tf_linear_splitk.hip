@@ -30,6 +30,8 @@
 // 500-505).
 #include "tf_common.hpp"
 
+#include <atomic>
+
 namespace tf {
 namespace {
 
@@ -468,11 +470,19 @@ void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_st
   const int32_t k_per_wave = ((steps + 3) / 4) * 32;
   const size_t lds =
       static_cast<size_t>(4) * (16 * MT + (SWIGLU ? 32 : 16)) * KC * sizeof(T);
-  if (lds > 64 * 1024) {  // raise the launch's dynamic LDS limit once
-    static const hipError_t raised = hipFuncSetAttribute(
-        reinterpret_cast<const void *>(&linear_kstream_kernel<T, MT, KC, SWIGLU>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    (void)raised;
+  if (lds > 64 * 1024) {
+    // Raise the kernel's dynamic LDS limit once per device (a failure shows
+    // up as a launch error).
+    constexpr int kMaxDevices = 64;
+    static std::atomic<bool> raised[kMaxDevices];
+    int device = 0;
+    if (hipGetDevice(&device) == hipSuccess && device >= 0 && device < kMaxDevices &&
+        !raised[device].load(std::memory_order_acquire)) {
+      if (hipFuncSetAttribute(
+              reinterpret_cast<const void *>(&linear_kstream_kernel<T, MT, KC, SWIGLU>),
+              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) == hipSuccess)
+        raised[device].store(true, std::memory_order_release);
+    }
   }
   hipLaunchKernelGGL((linear_kstream_kernel<T, MT, KC, SWIGLU>), dim3((n + 15) / 16), dim3(256),
                      lds, stream, static_cast<const T *>(x), x_stride, static_cast<const T *>(w),
