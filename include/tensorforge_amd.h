@@ -26,6 +26,8 @@
  *                            (the decode step's cache write) and
  *                            runtime/prefill.py:99-115 (prefill's)
  *   tf_rms_norm              tensorforge/kernels/triton_ops.py:179-205
+ *   tf_embedding_rms_norm    token feedback + embedding + first input norm
+ *                            (runtime/decode_bucket.py:427-440)
  *   tf_residual_rms_norm     tensorforge/kernels/triton_ops.py:208-243
  *   tf_swiglu                tensorforge/kernels/triton_ops.py:246-260
  *   tf_linear_rows           the nn.Linear projections of the decode step
@@ -266,6 +268,24 @@ int32_t tf_rope_kv_append(
     const int32_t *active_mask, int32_t batch, int32_t query_heads,
     int32_t kv_heads, int32_t head_dim, int32_t num_blocks, int32_t block_size,
     int32_t dtype, void *stream);
+
+/*
+ * The decode step's input rows and the first layer's RMSNorm in one launch:
+ * row b takes token id = token_state[source_lanes[b]] when source_lanes[b]
+ * >= 0 (the token its lane sampled last step) and host_tokens[b] otherwise
+ * (int64 arrays; lane and token indices are clamped to token_state_len and
+ * vocab), copies embedding[id] (a [vocab, columns] table) to x_output[b] and
+ * writes RMSNorm(x) with `weight` to norm_output[b] -- bit for bit the
+ * gather followed by tf_rms_norm.  Replaces the token feedback, embedding
+ * lookup and first input norm of the decode step
+ * (tensorforge/runtime/decode_bucket.py:427-440; the norm
+ * tensorforge/kernels/triton_ops.py:179-205).
+ */
+int32_t tf_embedding_rms_norm(const int64_t *token_state, int64_t token_state_len,
+                              const int64_t *source_lanes, const int64_t *host_tokens,
+                              const void *embedding, int64_t vocab, const void *weight,
+                              void *x_output, void *norm_output, int64_t rows, int32_t columns,
+                              float eps, int32_t dtype, void *stream);
 
 /*
  * Row-wise RMSNorm over [rows, columns]: y = x * rsqrt(mean(x^2) + eps) * w,

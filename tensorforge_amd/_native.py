@@ -90,6 +90,8 @@ SIGNATURES: dict[str, tuple[Any, ...]] = {
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p,  # batch .. block size, dtype, stream
     ),
     "tf_rms_norm": (_p, _p, _p, _i64, _i32, _f32, _i32, _p),
+    "tf_embedding_rms_norm": (_p, _i64, _p, _p, _p, _i64, _p, _p, _p, _i64, _i32, _f32, _i32,
+                              _p),
     "tf_residual_rms_norm": (_p, _p, _p, _p, _p, _i64, _i32, _f32, _i32, _p),
     "tf_residual_rms_norm_partials": (_p, _i32, _p, _p, _p, _p, _i64, _i32, _f32, _i32, _p),
     "tf_swiglu": (_p, _p, _p, _i64, _i32, _p),

@@ -45,25 +45,46 @@ __device__ __forceinline__ float block_sum(float v, float *scratch) {
   return total;
 }
 
+// Token ids of a decode step's rows: row b reads state[source[b]] when
+// source[b] >= 0 (the token its lane sampled last step) and host[b]
+// otherwise; ids are clamped to the table.
+struct GatherRows {
+  const int64_t *state = nullptr;
+  int64_t state_len = 0;
+  const int64_t *source = nullptr;
+  const int64_t *host = nullptr;
+  int64_t vocab = 0;
+};
+
 // One workgroup per row.  RESIDUAL selects the fused residual variant.
 // PARTIALS (with RESIDUAL) reads no `inputs`:
 // element j of the row is round(sum_s partials[s][row][j]) over `splits`
 // dense fp32 [rows, columns] planes, the rounded result of a split-K
-// projection (tf_linear_partials) whose sum is fused here.
-template <typename T, int VEC, bool RESIDUAL, bool PARTIALS>
+// projection (tf_linear_partials) whose sum is fused here.  GATHER (plain
+// norm) reads row id(b) of `inputs` -- an embedding table -- and also stores
+// that row to `residual_output`.
+template <typename T, int VEC, bool RESIDUAL, bool PARTIALS, bool GATHER = false>
 __global__ void __launch_bounds__(1024)
 rms_norm_kernel(const T *__restrict__ inputs, const T *__restrict__ residual,
                 const T *__restrict__ weight, T *__restrict__ residual_output,
                 T *__restrict__ output, int32_t columns, float eps,
-                const float *__restrict__ partials, int32_t splits, int64_t plane) {
+                const float *__restrict__ partials, int32_t splits, int64_t plane,
+                GatherRows gather) {
   __shared__ float scratch[16];
   using V = Vec<T, VEC>;
   const int64_t row = blockIdx.x;
   const int32_t nvec = columns / VEC;
-  const V *x = reinterpret_cast<const V *>(inputs + (PARTIALS ? 0 : row * columns));
+  int64_t in_row = row;
+  if constexpr (GATHER) {
+    const int64_t src = gather.source[row];
+    int64_t id = src >= 0 ? gather.state[src < gather.state_len ? src : gather.state_len - 1]
+                          : gather.host[row];
+    in_row = id < 0 ? 0 : (id >= gather.vocab ? gather.vocab - 1 : id);
+  }
+  const V *x = reinterpret_cast<const V *>(inputs + (PARTIALS ? 0 : in_row * columns));
   const float *prow = PARTIALS ? partials + row * columns : nullptr;
   const V *r = reinterpret_cast<const V *>(residual + (RESIDUAL ? row * columns : 0));
-  V *ro = reinterpret_cast<V *>(residual_output + (RESIDUAL ? row * columns : 0));
+  V *ro = reinterpret_cast<V *>(residual_output + (RESIDUAL || GATHER ? row * columns : 0));
   V *y = reinterpret_cast<V *>(output + row * columns);
   const V *w = reinterpret_cast<const V *>(weight);
 
@@ -112,6 +133,7 @@ rms_norm_kernel(const T *__restrict__ inputs, const T *__restrict__ residual,
         for (int e = 0; e < VEC; ++e) xv.v[e] = from_float<T>(sum[e]);
       } else {
         xv = x[idx];
+        if constexpr (GATHER) ro[idx] = xv;
       }
       V rv;
       if constexpr (RESIDUAL) rv = r[idx];
@@ -185,7 +207,8 @@ swiglu_rows_kernel(const T *__restrict__ gate_up, int64_t in_stride, T *__restri
 template <typename T, int VEC, bool RESIDUAL>
 void launch_norm(const void *inputs, const void *residual, const void *weight,
                  void *residual_output, void *output, int64_t rows, int32_t columns,
-                 float eps, const float *partials, int32_t splits, hipStream_t stream) {
+                 float eps, const float *partials, int32_t splits, hipStream_t stream,
+                 const GatherRows *gather) {
   constexpr int kMaxVecs = max_vecs<VEC>();
   const int32_t nvec = columns / VEC;
   // Two vectors per lane where possible (one when the inputs are summed
@@ -197,37 +220,45 @@ void launch_norm(const void *inputs, const void *residual, const void *weight,
   if (threads < 64) threads = 64;
   if (threads > 1024) threads = 1024;
   const int64_t plane = rows * static_cast<int64_t>(columns);
-  if (RESIDUAL && partials)
+  if (!RESIDUAL && gather)
+    hipLaunchKernelGGL((rms_norm_kernel<T, VEC, false, false, true>), dim3(static_cast<unsigned>(rows)),
+                       dim3(threads), 0, stream, static_cast<const T *>(inputs),
+                       static_cast<const T *>(residual), static_cast<const T *>(weight),
+                       static_cast<T *>(residual_output), static_cast<T *>(output), columns, eps,
+                       nullptr, 0, plane, *gather);
+  else if (RESIDUAL && partials)
     hipLaunchKernelGGL((rms_norm_kernel<T, VEC, RESIDUAL, RESIDUAL>), dim3(static_cast<unsigned>(rows)),
                        dim3(threads), 0, stream, static_cast<const T *>(inputs),
                        static_cast<const T *>(residual), static_cast<const T *>(weight),
                        static_cast<T *>(residual_output), static_cast<T *>(output), columns, eps,
-                       partials, splits, plane);
+                       partials, splits, plane, GatherRows{});
   else
     hipLaunchKernelGGL((rms_norm_kernel<T, VEC, RESIDUAL, false>), dim3(static_cast<unsigned>(rows)),
                        dim3(threads), 0, stream, static_cast<const T *>(inputs),
                        static_cast<const T *>(residual), static_cast<const T *>(weight),
                        static_cast<T *>(residual_output), static_cast<T *>(output), columns, eps,
-                       nullptr, 0, plane);
+                       nullptr, 0, plane, GatherRows{});
 }
 
 template <typename T, bool RESIDUAL>
 int32_t dispatch_norm(const void *inputs, const void *residual, const void *weight,
                       void *residual_output, void *output, int64_t rows, int32_t columns,
-                      float eps, const float *partials, int32_t splits, hipStream_t stream) {
+                      float eps, const float *partials, int32_t splits, hipStream_t stream,
+                      const GatherRows *gather) {
   constexpr int kVec = 16 / sizeof(T);
   uintptr_t align = reinterpret_cast<uintptr_t>(partials ? partials : inputs) |
                     reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(output);
   if (RESIDUAL)
     align |= reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(residual_output);
+  if (gather) align |= reinterpret_cast<uintptr_t>(residual_output);
   const bool vectorised = columns % kVec == 0 && align % 16 == 0 &&
                           columns / kVec <= 1024 * max_vecs<kVec>();
   if (vectorised) {
     launch_norm<T, kVec, RESIDUAL>(inputs, residual, weight, residual_output, output, rows,
-                                   columns, eps, partials, splits, stream);
+                                   columns, eps, partials, splits, stream, gather);
   } else if (columns <= 1024 * max_vecs<1>()) {
     launch_norm<T, 1, RESIDUAL>(inputs, residual, weight, residual_output, output, rows,
-                                columns, eps, partials, splits, stream);
+                                columns, eps, partials, splits, stream, gather);
   } else {
     return fail(TF_ERROR_UNSUPPORTED, "RMSNorm row does not fit the register cache");
   }
@@ -238,7 +269,7 @@ template <bool RESIDUAL>
 int32_t norm_entry(const void *inputs, const void *residual, const void *weight,
                    void *residual_output, void *output, int64_t rows, int32_t columns,
                    float eps, int32_t dtype, void *stream, const float *partials = nullptr,
-                   int32_t splits = 0) {
+                   int32_t splits = 0, const GatherRows *gather = nullptr) {
   clear_error();
   if (!valid_dtype(dtype)) return fail(TF_ERROR_INVALID_ARGUMENT, "unsupported dtype code");
   if (rows < 0 || columns <= 0 || columns > 16384)
@@ -246,20 +277,20 @@ int32_t norm_entry(const void *inputs, const void *residual, const void *weight,
   if (rows > 0x7fffffff) return fail(TF_ERROR_UNSUPPORTED, "too many rows for one launch");
   if (!(eps > 0.f)) return fail(TF_ERROR_INVALID_ARGUMENT, "eps must be positive");
   if (!(partials ? static_cast<const void *>(partials) : inputs) || !weight || !output ||
-      (RESIDUAL && (!residual || !residual_output)))
+      (RESIDUAL && (!residual || !residual_output)) || (gather && !residual_output))
     return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
   if (rows == 0) return TF_SUCCESS;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case TF_DTYPE_FLOAT32:
       return dispatch_norm<float, RESIDUAL>(inputs, residual, weight, residual_output, output,
-                                            rows, columns, eps, partials, splits, s);
+                                            rows, columns, eps, partials, splits, s, gather);
     case TF_DTYPE_FLOAT16:
       return dispatch_norm<_Float16, RESIDUAL>(inputs, residual, weight, residual_output,
-                                               output, rows, columns, eps, partials, splits, s);
+                                               output, rows, columns, eps, partials, splits, s, gather);
     default:
       return dispatch_norm<__bf16, RESIDUAL>(inputs, residual, weight, residual_output, output,
-                                             rows, columns, eps, partials, splits, s);
+                                             rows, columns, eps, partials, splits, s, gather);
   }
 }
 
@@ -321,6 +352,28 @@ extern "C" int32_t tf_rms_norm(const void *inputs, const void *weight, void *out
                                void *stream) {
   return tf::norm_entry<false>(inputs, nullptr, weight, nullptr, output, rows, columns, eps,
                                dtype, stream);
+}
+
+extern "C" int32_t tf_embedding_rms_norm(const int64_t *token_state, int64_t token_state_len,
+                                         const int64_t *source_lanes, const int64_t *host_tokens,
+                                         const void *embedding, int64_t vocab, const void *weight,
+                                         void *x_output, void *norm_output, int64_t rows,
+                                         int32_t columns, float eps, int32_t dtype,
+                                         void *stream) {
+  using namespace tf;
+  clear_error();
+  if (rows > 0 && (!token_state || !source_lanes || !host_tokens))
+    return fail(TF_ERROR_INVALID_ARGUMENT, "null token pointer");
+  if (rows > 0 && (token_state_len < 1 || vocab < 1))
+    return fail(TF_ERROR_INVALID_ARGUMENT, "token state and vocabulary must be non-empty");
+  GatherRows gather;
+  gather.state = token_state;
+  gather.state_len = token_state_len;
+  gather.source = source_lanes;
+  gather.host = host_tokens;
+  gather.vocab = vocab;
+  return norm_entry<false>(embedding, nullptr, weight, x_output, norm_output, rows, columns, eps,
+                           dtype, stream, nullptr, 0, &gather);
 }
 
 extern "C" int32_t tf_residual_rms_norm(const void *inputs, const void *residual,

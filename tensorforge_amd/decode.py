@@ -43,6 +43,7 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from tensorforge_amd import _native
 from tensorforge_amd.cache import AppendReservation, PagedKVCache
 from tensorforge_amd.kernels import (
+    embedding_rms_norm,
     PagedAttentionWorkspace,
     linear_kstream,
     linear_rows,
@@ -262,6 +263,7 @@ class DecodeGraphBucket:
         self.query = torch.empty((b, hq, d), dtype=dtype, device=device)
         self.attention_output = torch.empty((b, hq, d), dtype=dtype, device=device)
         self.norm_output = torch.empty((b, config.hidden_size), dtype=dtype, device=device)
+        self.embedding_output = torch.empty((b, config.hidden_size), dtype=dtype, device=device)
         self.swiglu_output = torch.empty((b, config.intermediate_size), dtype=dtype,
                                          device=device)
         self.logits = torch.empty((b, config.vocab_size), dtype=dtype, device=device)
@@ -413,11 +415,11 @@ class DecodeGraphBucket:
         # a caller may have fixed globally.
         previous = set_attention_split_size(None)
         try:
-            fed = self.token_state.index_select(0, self.source_lanes.clamp(min=0))
-            input_ids = torch.where(self.source_lanes >= 0, fed, self.host_tokens)
-            x = F.embedding(input_ids, self.weights.embedding)
-            residual = x
-            h = rms_norm(x, self.weights.layers[0].input_norm, eps, output=self.norm_output)
+            # Token feedback, embedding and the first input norm in one launch.
+            residual, h = embedding_rms_norm(
+                self.token_state, self.source_lanes, self.host_tokens, self.weights.embedding,
+                self.weights.layers[0].input_norm, eps, x_output=self.embedding_output,
+                norm_output=self.norm_output)
             for index, layer in enumerate(self.weights.layers):
                 qkv = _project(h, layer.qkv)
                 key_cache = self.cache.key_cache[index]

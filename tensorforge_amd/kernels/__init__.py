@@ -26,6 +26,7 @@ from tensorforge_amd.kernels.linear import (
 from tensorforge_amd.kernels.ops import (
     autotune_cache_size,
     is_hip_available,
+    embedding_rms_norm,
     residual_rms_norm,
     rms_norm,
     selected_autotune_config,
@@ -49,6 +50,7 @@ __all__ = [
     "paged_gqa_decode_attention",
     "paged_kv_write_slots",
     "paged_kv_write_token",
+    "embedding_rms_norm",
     "residual_rms_norm",
     "rms_norm",
     "rope_paged_kv_append",

@@ -97,6 +97,53 @@ def _aligned(*tensors: Tensor) -> bool:
     return all(tensor.data_ptr() % 16 == 0 for tensor in tensors)
 
 
+def embedding_rms_norm(
+    token_state: Tensor,
+    source_lanes: Tensor,
+    host_tokens: Tensor,
+    embedding: Tensor,
+    weight: Tensor,
+    eps: float,
+    *,
+    x_output: Tensor,
+    norm_output: Tensor,
+) -> tuple[Tensor, Tensor]:
+    """A decode step's input rows and first RMSNorm in one launch: row b
+    embeds ``token_state[source_lanes[b]]`` when ``source_lanes[b] >= 0``
+    and ``host_tokens[b]`` otherwise (int64; indices clamped to the arrays),
+    writing the embedding row to ``x_output`` and its RMSNorm to
+    ``norm_output`` -- bit-identical to ``F.embedding`` of those ids followed
+    by :func:`rms_norm` (reference: runtime/decode_bucket.py:427-440,
+    triton_ops.py:179-205)."""
+
+    _require_library()
+    rows = source_lanes.shape[0]
+    vocab, columns = embedding.shape
+    for name, t in (("token_state", token_state), ("source_lanes", source_lanes),
+                    ("host_tokens", host_tokens)):
+        if t.dtype != torch.int64 or not t.is_cuda or not t.is_contiguous() or t.ndim != 1:
+            raise ValueError(f"{name} must be a contiguous 1-D int64 CUDA tensor")
+    if host_tokens.shape[0] != rows or token_state.shape[0] < 1:
+        raise ValueError("host_tokens must have one entry per row and token_state at least one")
+    if eps <= 0:
+        raise ValueError("eps must be positive")
+    _validate_common(embedding, weight)
+    for name, t in (("x_output", x_output), ("norm_output", norm_output)):
+        if (t.shape != (rows, columns) or t.dtype != embedding.dtype or not t.is_contiguous()
+                or t.device != embedding.device):
+            raise ValueError(f"{name} must be a contiguous [rows, hidden] tensor like the table")
+    _native.check(
+        _native.library().tf_embedding_rms_norm(
+            token_state.data_ptr(), token_state.shape[0], source_lanes.data_ptr(),
+            host_tokens.data_ptr(), embedding.data_ptr(), vocab, weight.data_ptr(),
+            x_output.data_ptr(), norm_output.data_ptr(), rows, columns, eps,
+            _native.dtype_code(embedding.dtype), _native.current_stream(embedding.device),
+        ),
+        "embedding_rms_norm",
+    )
+    return x_output, norm_output
+
+
 def rms_norm(
     inputs: Tensor,
     weight: Tensor,

@@ -220,3 +220,36 @@ def test_residual_rms_norm_partials_equals_the_unfused_pair(device, dtype, rows,
     torch.testing.assert_close(got_norm.float(), want_norm.float(), rtol=ulp, atol=1e-6)
     with pytest.raises(ValueError, match="partials"):
         residual_rms_norm_partials(partials[:, :, 1:], residual, weight, 1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("hidden", "vocab"), [(2048, 32000), (256, 1024), (200, 50)])
+def test_embedding_rms_norm_equals_gather_then_norm(device, dtype, hidden, vocab):
+    """Token feedback + embedding + RMSNorm in one launch, bit-identical to
+    index_select / where / F.embedding followed by rms_norm; lanes fed back
+    (source >= 0) and host-given, out-of-range ids clamped."""
+
+    import torch.nn.functional as F
+
+    from tensorforge_amd.kernels import embedding_rms_norm, rms_norm
+
+    generator = torch.Generator().manual_seed(hidden + vocab)
+    rows = 12
+    table = torch.randn(vocab, hidden, generator=generator).to(dtype).to(device)
+    weight = (1 + 0.1 * torch.randn(hidden, generator=generator)).to(dtype).to(device)
+    state = torch.randint(0, vocab, (16,), generator=generator).to(device)
+    source = torch.tensor([3, -1, 0, 15, -1, 7, -1, 2, 2, -1, 9, -1], device=device)
+    host = torch.randint(0, vocab, (rows,), generator=generator).to(device)
+    host[5] = vocab + 7  # unused (fed lane)
+    x = torch.full((rows, hidden), float("nan"), dtype=dtype, device=device)
+    h = torch.full_like(x, float("nan"))
+    embedding_rms_norm(state, source, host, table, weight, 1e-5, x_output=x, norm_output=h)
+    ids = torch.where(source >= 0, state.index_select(0, source.clamp(min=0)), host)
+    want_x = F.embedding(ids, table)
+    want_h = rms_norm(want_x, weight, 1e-5)
+    assert torch.equal(x.view(torch.int16), want_x.view(torch.int16))
+    assert torch.equal(h.view(torch.int16), want_h.view(torch.int16))
+    # A host id past the table reads its last row.
+    host[1] = vocab + 3
+    embedding_rms_norm(state, source, host, table, weight, 1e-5, x_output=x, norm_output=h)
+    assert torch.equal(x[1].view(torch.int16), table[vocab - 1].view(torch.int16))
