@@ -97,7 +97,7 @@ enum tf_attention_variant {
 /* Message describing the last failure on the calling thread ("" if none). */
 const char *tf_last_error(void);
 
-/* Version of this ABI; bumped on any signature change. */
+/* Version of this ABI; bumped on any signature change or added entry point. */
 int32_t tf_abi_version(void);
 
 /* Which kernel family tf_paged_gqa_decode uses for these parameters
