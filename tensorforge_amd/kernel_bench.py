@@ -17,7 +17,13 @@
 * ceiling -- what bounds the config-2 attention call: the graph launch gap,
   a fit of time against bytes over uniform-length batches (fixed cost per
   call and marginal rate), config 2 on random and on contiguous pages, and
-  one compute unit's rate with 1..8 wavefronts per kv head.
+  one compute unit's rate with 1..8 wavefronts per kv head;
+* projections -- the decode step's projections at TinyLlama shapes and 1 /
+  16 / 64 rows (weights rotated through HBM): hipBLASLt against the paths
+  the decode bucket takes (linear_kstream for qkv, linear_stream partials
+  for o / down, the K-split gate|up + SwiGLU, linear_stream for the LM
+  head), plus the attention plans of narrow calls against one wavefront per
+  256-token partition.
 
 Each case is captured as ``--calls`` launches in one HIP graph and timed by
 HIP events around one replay (a ctypes call costs the host longer than these
@@ -46,12 +52,19 @@ from tensorforge_amd.decode import (
 )
 from tensorforge_amd.kernels import (
     PagedAttentionWorkspace,
+    linear_kstream,
+    linear_rows,
+    linear_stream,
+    linear_swiglu,
     paged_gqa_decode_attention,
     residual_rms_norm,
     rms_norm,
     selected_attention_autotune_config,
+    set_attention_split_size,
     swiglu,
+    swiglu_gate_up,
 )
+from tensorforge_amd.kernels.linear import default_splits
 
 HBM_PEAK_GBS = 8000.0
 
@@ -344,11 +357,84 @@ def decode_steps(device: torch.device, model: str = "cfg1", steps: int = 64) -> 
               flush=True)
 
 
+def projections(device: torch.device, calls: int) -> list[dict]:
+    """The decode step's projections and narrow attention plans (see the
+    module docstring); times in microseconds per call."""
+
+    results = []
+    shapes = {"qkv": (2560, 2048), "o": (2048, 2048), "down": (2048, 5632),
+              "gate_up+swiglu": (11264, 2048), "lm_head": (32000, 2048)}
+    for name, (n, k) in shapes.items():
+        copies = max(2, int(600e6 // (n * k * 2)))
+        weights = [torch.randn(n, k, device=device, dtype=torch.bfloat16) * 0.02
+                   for _ in range(copies)]
+        for m in (1, 16, 64):
+            x = torch.randn(m, k, device=device, dtype=torch.bfloat16)
+            y = torch.empty(m, n, device=device, dtype=torch.bfloat16)
+            row = {"case": f"projection {name} [{m}x{k}]x[{k}x{n}]", "weight_MB": round(n * k * 2e-6, 1)}
+
+            def timed(fn) -> float:
+                return round(graph_time_us(lambda i: fn(weights[i % copies]), calls, device), 2)
+
+            if name == "gate_up+swiglu":
+                act = torch.empty(m, n // 2, device=device, dtype=torch.bfloat16)
+                row["hipblaslt+swiglu_us"] = timed(
+                    lambda w: swiglu_gate_up(torch.mm(x, w.t(), out=y), output=act))
+                row["linear_rows+swiglu_us"] = timed(
+                    lambda w: swiglu_gate_up(linear_rows(x, w, output=y), output=act))
+                row["k_split_swiglu_us"] = timed(
+                    lambda w: linear_swiglu(x, w, output=act, k_split=True))
+            else:
+                row["hipblaslt_us"] = timed(lambda w: torch.mm(x, w.t(), out=y))
+                row["linear_rows_us"] = timed(lambda w: linear_rows(x, w, output=y))
+                if name == "qkv":
+                    row["linear_kstream_us"] = timed(lambda w: linear_kstream(x, w, output=y))
+                elif name in ("o", "down"):
+                    splits = default_splits(n, k)
+                    part = torch.empty(splits, m, n, device=device)
+                    row[f"linear_stream_{splits}_slices_us"] = timed(
+                        lambda w: linear_stream(x, w, splits=splits, partials=part))
+                else:
+                    row["linear_stream_us"] = timed(lambda w: linear_stream(x, w, output=y))
+            results.append(row)
+        del weights
+        torch.cuda.empty_cache()
+
+    for batch, context in ((1, 1000), (8, 1000), (1, 4000), (8, 4000), (64, 512), (64, 1000)):
+        case = workloads.make_decode_attention_case(
+            [context] * batch, query_heads=32, kv_heads=4, head_dim=64, block_size=16,
+            dtype=torch.bfloat16, seed=batch + context)
+        gpu = case.to(device)
+        width = gpu.block_tables.shape[1]
+        workspace = PagedAttentionWorkspace.allocate(
+            batch_capacity=batch, query_heads=32, head_dim=64, max_context_length=width * 16,
+            device=device)
+        output = torch.empty_like(gpu.query)
+
+        def run(i: int) -> None:
+            paged_gqa_decode_attention(gpu.query, gpu.key_cache, gpu.value_cache,
+                                       gpu.block_tables, gpu.context_lengths, scale=case.scale,
+                                       max_context_length=width * 16, output=output,
+                                       workspace=workspace)
+
+        planned = graph_time_us(run, calls, device)
+        record = selected_attention_autotune_config()
+        previous = set_attention_split_size(256)
+        try:
+            one_wave = graph_time_us(run, calls, device)
+        finally:
+            set_attention_split_size(previous)
+        results.append({"case": f"attention {batch} rows x {context} (TinyLlama geometry)",
+                        "plan_us": round(planned, 2), "plan": record,
+                        "one_wavefront_per_256_partition_us": round(one_wave, 2)})
+    return results
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--calls", type=int, default=100)
-    parser.add_argument("--only", choices=("cfg3", "cfg4", "decode", "decode22", "ceiling"),
-                        default=None)
+    parser.add_argument("--only", choices=("cfg3", "cfg4", "decode", "decode22", "ceiling",
+                                           "projections"), default=None)
     args = parser.parse_args()
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -365,6 +451,9 @@ def main() -> int:
         decode_steps(device, "tinyllama")
     if args.only in (None, "ceiling"):
         for result in attention_ceiling(device, args.calls):
+            print(json.dumps(result), flush=True)
+    if args.only in (None, "projections"):
+        for result in projections(device, args.calls):
             print(json.dumps(result), flush=True)
     return 0
 
