@@ -1,4 +1,14 @@
-// Split-K decode linear layer on MFMA for 17..64 rows:
+// Decode-shaped linear layers on MFMA for up to 64 rows.  This file holds
+//   * tf_linear_partials / tf_linear_partials_sum -- split-K slices with
+//     operands loaded in the MFMA operand layout (below);
+//   * tf_linear_stream -- the same products (or a one-slice rounded output)
+//     with both operands staged through LDS by whole-row loads;
+//   * tf_linear_swiglu -- its form for the stacked gate|up weight with the
+//     SwiGLU in the epilogue;
+//   * tf_linear_kstream / tf_linear_kswiglu -- K split over the wavefronts
+//     of 16-column workgroups, for narrow weights and for gate|up + SwiGLU.
+//
+// Split-K form:
 //   partials[s][m][n] = sum over k in slice s of x[m][k] * w[n][k]   (fp32)
 // and the row sum y[m][n] = round(sum_s partials[s][m][n]).
 //
