@@ -6,7 +6,8 @@ model/llama.py: embedding, pre-norm blocks (RMSNorm :14-30, grouped-query
 causal attention with RoPE :33-143, SwiGLU MLP :146-158, residuals
 :161-171), final RMSNorm and the LM head.  Weights come from the same
 container the GPU path uses (tensorforge_amd.decode.DecoderWeights), read on
-the CPU in fp32.
+the CPU in fp32 (or, as a checker of long runs, on the GPU in fp32 or in
+the model's own precision).
 
 Pinning (tests/test_oracle_model.py): RoPE against its closed forms
 (identity at position 0, norm preservation, dot products depending only on
@@ -46,19 +47,37 @@ def apply_rope(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
     return x * cos + rotate_half(x) * sin
 
 
-def decoder_forward(weights, tokens: Tensor) -> Tensor:
-    """Logits [seq, vocab] (fp32) of a full causal forward over `tokens` [seq]."""
+def _rms_norm(x: Tensor, weight: Tensor, eps: float) -> Tensor:
+    """rms_norm_reference's formula (fp32 mean of squares, rsqrt, scale by
+    weight, one rounding to x's dtype) on x's own device."""
+
+    xf = x.float()
+    inv = torch.rsqrt(xf.square().mean(dim=-1, keepdim=True) + eps)
+    return (xf * inv * weight.float()).to(x.dtype)
+
+
+def decoder_forward(weights, tokens: Tensor, *, device: torch.device | str = "cpu",
+                    dtype: torch.dtype = torch.float32) -> Tensor:
+    """Logits [seq, vocab] of a full causal forward over `tokens` [seq].
+
+    By default in fp32 on the CPU.  ``device`` runs the same math on another
+    device (a checker for long sequences); ``dtype`` runs it in another
+    precision (fp16 / bf16: every operand and every intermediate rounded to
+    it, as a same-precision restatement of the model).  Logits are returned
+    in fp32 on the CPU."""
 
     config = weights.config
-    f32 = lambda t: t.detach().cpu().float()  # noqa: E731
+    device = torch.device(device)
+    f32 = lambda t: t.detach().to(device=device, dtype=dtype)  # noqa: E731
     hq, hkv, d = config.num_attention_heads, config.num_key_value_heads, config.head_dim
     group = hq // hkv
     seq = tokens.shape[0]
-    x = f32(weights.embedding)[tokens.cpu()]
+    x = f32(weights.embedding)[tokens.to(device)]
     cos, sin = rope_tables(d, config.rope_theta, torch.arange(seq))
-    causal = torch.ones(seq, seq, dtype=torch.bool).triu(1)
+    cos, sin = cos.to(device=device, dtype=dtype), sin.to(device=device, dtype=dtype)
+    causal = torch.ones(seq, seq, dtype=torch.bool, device=device).triu(1)
     for layer in weights.layers:
-        h = rms_norm_reference(x, f32(layer.input_norm), config.rms_norm_eps)
+        h = _rms_norm(x, f32(layer.input_norm), config.rms_norm_eps)
         qkv = h @ f32(layer.qkv).T
         q = qkv[:, : hq * d].view(seq, hq, d).transpose(0, 1)
         k = qkv[:, hq * d: (hq + hkv) * d].view(seq, hkv, d).transpose(0, 1)
@@ -66,16 +85,16 @@ def decoder_forward(weights, tokens: Tensor) -> Tensor:
         q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
         k = k.repeat_interleave(group, dim=0)
         v = v.repeat_interleave(group, dim=0)
-        scores = (q @ k.transpose(-1, -2)) * d**-0.5
+        scores = (q @ k.transpose(-1, -2).contiguous()) * d**-0.5
         scores = scores.masked_fill(causal, float("-inf"))
-        context = torch.softmax(scores, dim=-1) @ v  # [hq, seq, d]
+        context = torch.softmax(scores.float(), dim=-1).to(dtype) @ v  # [hq, seq, d]
         x = x + context.transpose(0, 1).reshape(seq, hq * d) @ f32(layer.o_proj).T
-        h = rms_norm_reference(x, f32(layer.post_norm), config.rms_norm_eps)
+        h = _rms_norm(x, f32(layer.post_norm), config.rms_norm_eps)
         gate = h @ f32(layer.gate).T
         up = h @ f32(layer.up).T
         x = x + (torch.nn.functional.silu(gate) * up) @ f32(layer.down).T
-    h = rms_norm_reference(x, f32(weights.final_norm), config.rms_norm_eps)
-    return h @ f32(weights.lm_head).T
+    h = _rms_norm(x, f32(weights.final_norm), config.rms_norm_eps)
+    return (h @ f32(weights.lm_head).T).float().cpu()
 
 
 def decode_step_reference(weights, keys: list[Tensor], values: list[Tensor], tokens: Tensor,

@@ -651,8 +651,8 @@ paged_decode_mfma_kernel(AttnParams p) {
         const uint32_t t_off =
             LINES ? (tt < ntok ? static_cast<uint32_t>(tt) * token_bytes : 0u) + v_piece
                   : lane_off + 64u * ks;
-        kf[j][ks] = *reinterpret_cast<const vec8 *>(kbytes + tile_off + t_off);
-        vf[j][ks] = *reinterpret_cast<const vec8 *>(vbytes + tile_off + t_off);
+        kf[j][ks] = load_stream16<vec8>(kbytes + tile_off + t_off);
+        vf[j][ks] = load_stream16<vec8>(vbytes + tile_off + t_off);
       }
     }
   };
@@ -1186,8 +1186,8 @@ paged_decode_stream_kernel(AttnParams p) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const uint32_t o = lane_off + (ntok > 0 ? h * D * sizeof(T) : 0) + 64 * ks;
-        st.k[h][ks] = *reinterpret_cast<const vec8 *>(kbytes + tile_off + o);
-        st.v[h][ks] = *reinterpret_cast<const vec8 *>(vbytes + tile_off + o);
+        st.k[h][ks] = load_stream16<vec8>(kbytes + tile_off + o);
+        st.v[h][ks] = load_stream16<vec8>(vbytes + tile_off + o);
       }
   };
 

@@ -32,7 +32,9 @@ initialize_weights (layers.py:174-176).
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+import time
+from contextlib import suppress
+from dataclasses import asdict, dataclass, field
 
 import numpy as np
 import torch
@@ -41,6 +43,7 @@ from torch.nn import functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from tensorforge_amd import _native
+from tensorforge_amd.batch import BatchExecutionResult
 from tensorforge_amd.cache import AppendReservation, PagedKVCache
 from tensorforge_amd.kernels import (
     embedding_rms_norm,
@@ -212,12 +215,17 @@ class DecodeGraphBucket:
     """
 
     def __init__(self, weights: DecoderWeights, cache: PagedKVCache, *, batch_capacity: int,
-                 context_capacity: int, token_state: Tensor | None = None) -> None:
+                 context_capacity: int, token_state: Tensor | None = None, graph: bool = True,
+                 metrics: _MutableMetrics | None = None) -> None:
         config = weights.config
         self.weights = weights
         self.cache = cache
         self.batch_capacity = batch_capacity
         self.context_capacity = context_capacity
+        # graph=False runs every step eagerly (the executor's fallback for
+        # steps no bucket holds); the step's work is the same.
+        self.graph = graph
+        self._metrics = metrics
         device = cache.config.device
         dtype = cache.config.dtype
         width = cache.config.max_blocks_per_sequence
@@ -383,10 +391,18 @@ class DecodeGraphBucket:
         self._copy_recorded[k] = True
 
     def execute(self) -> Tensor:
-        """Run the step (capturing the graph on first use); returns the
-        device tensor of greedy next tokens, one per lane."""
+        """Run the step (capturing the graph on first use, or eagerly when
+        the bucket has no graph); returns the device tensor of greedy next
+        tokens, one per lane."""
 
+        metrics = self._metrics
+        if not self.graph:
+            self._forward()
+            if metrics is not None:
+                metrics.eager_calls += 1
+            return self.next_tokens
         if self._graph is None:
+            begin = time.perf_counter()
             stream = torch.cuda.current_stream(self.device)
             # The eager warm-up (library handles and plans) samples into
             # token_state; restore it so the replay reads the previous step's
@@ -399,9 +415,19 @@ class DecodeGraphBucket:
             stream.wait_stream(side)
             self.token_state.copy_(saved)
             torch.cuda.synchronize(self.device)
+            warm = time.perf_counter()
             self._graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self._graph):
                 self._forward()
+            if metrics is not None:
+                metrics.capture_count += 1
+                metrics.capture_warmup_time_ms += (warm - begin) * 1e3
+                metrics.capture_time_ms += (time.perf_counter() - begin) * 1e3
+                metrics.graph_misses += 1
+        elif metrics is not None:
+            metrics.graph_hits += 1
+        if metrics is not None:
+            metrics.graph_calls += 1
         self._graph.replay()
         return self.next_tokens
 
@@ -505,88 +531,151 @@ def _causal_attention(q: Tensor, k: Tensor, v: Tensor, scale: float) -> Tensor:
     return context[0].transpose(0, 1).reshape(seq, hq * d)
 
 
-def prefill_batch(weights: DecoderWeights, cache: PagedKVCache,
-                  prompts: dict[str, list[int]]) -> dict[str, tuple[int, Tensor]]:
-    """Prefill several fresh prompts together: {request_id: (greedy next
-    token, last-position logits)}.
+def _validate_prompt(weights: DecoderWeights, cache: PagedKVCache, request_id: str,
+                     prompt) -> None:
+    """Host-side checks of one prompt before any reservation or device work
+    (runtime/prefill.py:175-185): an id outside the vocabulary would index
+    the embedding table out of range on the device."""
 
-    The reference pads the prompts into one [batch, longest] causal batch
-    and writes each request's K/V with its own write_layer per layer
-    (runtime/prefill.py:37-149).  Here the prompts' tokens are packed into
-    one [total, H] stream with no padding: every projection is one GEMM over
-    all tokens, and one rope_paged_kv_append launch per layer rotates q and k
-    of every token and writes k, v straight into the pages each token's
-    position maps to.  Attention is one packed causal launch per layer over
-    all prompts (prefill_attention; torch's fused causal SDPA per prompt for
-    geometries that kernel does not serve).  All reservations commit
-    together, or roll back together on an error.
-    """
+    if len(prompt) == 0:
+        raise ValueError("prompt must contain at least one token")
+    ids = np.asarray(prompt, dtype=np.int64)
+    if ids.ndim != 1 or bool(((ids < 0) | (ids >= weights.config.vocab_size)).any()):
+        raise ValueError("prompt token is outside the model vocabulary")
+    if cache.sequence_layout(request_id).context_length != 0:
+        raise ValueError("prefill ingests fresh sequences only")
+    if len(prompt) > weights.rope_cos.shape[0]:
+        raise ValueError("prompt exceeds the model's RoPE table")
 
-    if not prompts:
-        raise ValueError("prefill_batch requires at least one prompt")
+
+def _prefill_packed(weights: DecoderWeights, cache: PagedKVCache, prompts: dict[str, list[int]],
+                    ) -> Tensor:
+    """Run the packed prefill of reserved, validated prompts; last-position
+    logits [len(prompts), vocab] in prompt order.  Writes every layer's
+    pages; commit or rollback is the caller's."""
+
     config = weights.config
     hq, hkv, d = config.num_attention_heads, config.num_key_value_heads, config.head_dim
     device = cache.config.device
     block_size = cache.config.block_size
+    request_ids = list(prompts)
+    lengths = [len(prompts[r]) for r in request_ids]
+    bounds = np.concatenate(([0], np.cumsum(lengths)))
+    total = int(bounds[-1])
+    longs = np.empty((2, total), dtype=np.int64)   # token ids, positions
+    ints = np.ones((3, total), dtype=np.int32)     # pages, offsets, active
+    for i, request_id in enumerate(request_ids):
+        lo, hi = bounds[i], bounds[i + 1]
+        positions = np.arange(hi - lo, dtype=np.int64)
+        pages = np.asarray(cache.page_list(request_id)[0], dtype=np.int32)
+        longs[0, lo:hi] = prompts[request_id]
+        longs[1, lo:hi] = positions
+        ints[0, lo:hi] = pages[positions // block_size]
+        ints[1, lo:hi] = positions % block_size
+    longs_dev = torch.from_numpy(longs).to(device)
+    ints_dev = torch.from_numpy(ints).to(device)
+    packed_attention = prefill_attention_supported(weights.embedding.dtype, hq, hkv, d)
+    if packed_attention:
+        tiles = torch.from_numpy(prefill_tiles(lengths)).to(device)
+    tokens, positions_dev = longs_dev[0], longs_dev[1]
+    eps = config.rms_norm_eps
+    residual = F.embedding(tokens, weights.embedding)
+    h = rms_norm(residual, weights.layers[0].input_norm, eps)
+    q = torch.empty((total, hq, d), dtype=residual.dtype, device=device)
+    k = torch.empty((total, hkv, d), dtype=residual.dtype, device=device)
+    context = torch.empty((total, hq * d), dtype=residual.dtype, device=device)
+    for index, layer in enumerate(weights.layers):
+        qkv = F.linear(h, layer.qkv)
+        rope_paged_kv_append(qkv, positions_dev, weights.rope_cos, weights.rope_sin,
+                             cache.key_cache[index], cache.value_cache[index], ints_dev[0],
+                             ints_dev[1], ints_dev[2], query_heads=hq, query_output=q,
+                             key_output=k)
+        if packed_attention:  # every prompt's causal attention in one launch
+            prefill_attention(q.view(total, hq * d), k.view(total, hkv * d),
+                              qkv[:, (hq + hkv) * d:], tiles, query_heads=hq,
+                              kv_heads=hkv, scale=d ** -0.5, output=context)
+        else:
+            v = qkv[:, (hq + hkv) * d:].view(total, hkv, d)
+            for i in range(len(request_ids)):
+                lo, hi = int(bounds[i]), int(bounds[i + 1])
+                context[lo:hi] = _causal_attention(q[lo:hi], k[lo:hi], v[lo:hi], d ** -0.5)
+        attn = F.linear(context, layer.o_proj)
+        residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps)
+        act = swiglu_gate_up(F.linear(h, layer.gate_up))
+        next_norm = (weights.layers[index + 1].input_norm
+                     if index + 1 < len(weights.layers) else weights.final_norm)
+        residual, h = residual_rms_norm(F.linear(act, layer.down), residual, next_norm, eps)
+    last = torch.from_numpy(bounds[1:] - 1).to(device)
+    return F.linear(h.index_select(0, last), weights.lm_head)
+
+
+def prefill_requests(weights: DecoderWeights, cache: PagedKVCache,
+                     prompts: dict[str, list[int]]) -> BatchExecutionResult:
+    """Prefill fresh prompts together, each in a transaction of its own
+    (runtime/prefill.py:37-149): the last position's logits of every prompt
+    that ran, and an error message for every prompt that could not.
+
+    A prompt with an id outside the vocabulary, a sequence that is not
+    fresh or a reservation the cache cannot make fails alone, before any
+    device work; the others run.  A failure of the packed launch itself
+    rolls back every reservation and fails every request of the call.
+
+    The reference pads the prompts into one [batch, longest] causal batch
+    and writes each request's K/V with its own write_layer per layer.  Here
+    the prompts' tokens are packed into one [total, H] stream with no
+    padding: every projection is one GEMM over all tokens, and one
+    rope_paged_kv_append launch per layer rotates q and k of every token and
+    writes k, v straight into the pages each token's position maps to.
+    Attention is one packed causal launch per layer over all prompts
+    (prefill_attention; torch's fused causal SDPA per prompt for geometries
+    that kernel does not serve).
+    """
+
+    if not prompts:
+        raise ValueError("prefill requires at least one prompt")
+    errors: dict[str, str] = {}
+    reservations: dict[str, AppendReservation] = {}
+    for request_id, prompt in prompts.items():
+        try:
+            _validate_prompt(weights, cache, request_id, prompt)
+            reservations[request_id] = cache.begin_append(request_id, len(prompt))
+        except Exception as error:  # noqa: BLE001 - reported per request
+            errors[request_id] = f"{type(error).__name__}: {error}"
+    if not reservations:
+        return BatchExecutionResult(logits={}, errors=errors)
+    try:
+        logits = _prefill_packed(weights, cache, {r: list(prompts[r]) for r in reservations})
+    except Exception as error:  # noqa: BLE001 - the whole launch failed
+        message = f"{type(error).__name__}: {error}"
+        for request_id, reservation in reservations.items():
+            with suppress(RuntimeError):
+                cache.rollback(reservation)
+            errors[request_id] = message
+        return BatchExecutionResult(logits={}, errors=errors)
+    for reservation in reservations.values():
+        cache.record_all_layers_written(reservation)
+        cache.commit(reservation)
+    return BatchExecutionResult(
+        logits={request_id: logits[i] for i, request_id in enumerate(reservations)},
+        errors=errors)
+
+
+def prefill_batch(weights: DecoderWeights, cache: PagedKVCache,
+                  prompts: dict[str, list[int]]) -> dict[str, tuple[int, Tensor]]:
+    """Prefill several fresh prompts together, all or nothing: {request_id:
+    (greedy next token, last-position logits)}.  Every prompt is validated
+    on the host and every reservation made before any device work; any
+    failure rolls back the reservations made and raises."""
+
+    if not prompts:
+        raise ValueError("prefill_batch requires at least one prompt")
+    for request_id, prompt in prompts.items():
+        _validate_prompt(weights, cache, request_id, prompt)
     reservations: dict[str, AppendReservation] = {}
     try:
         for request_id, prompt in prompts.items():
-            if not prompt:
-                raise ValueError("prompt must contain at least one token")
-            if cache.sequence_layout(request_id).context_length != 0:
-                raise ValueError("prefill_batch ingests fresh sequences only")
-            if len(prompt) > weights.rope_cos.shape[0]:
-                raise ValueError("prompt exceeds the model's RoPE table")
             reservations[request_id] = cache.begin_append(request_id, len(prompt))
-        request_ids = list(prompts)
-        lengths = [len(prompts[r]) for r in request_ids]
-        bounds = np.concatenate(([0], np.cumsum(lengths)))
-        total = int(bounds[-1])
-        longs = np.empty((2, total), dtype=np.int64)   # token ids, positions
-        ints = np.ones((3, total), dtype=np.int32)     # pages, offsets, active
-        for i, request_id in enumerate(request_ids):
-            lo, hi = bounds[i], bounds[i + 1]
-            positions = np.arange(hi - lo, dtype=np.int64)
-            pages = np.asarray(cache.page_list(request_id)[0], dtype=np.int32)
-            longs[0, lo:hi] = prompts[request_id]
-            longs[1, lo:hi] = positions
-            ints[0, lo:hi] = pages[positions // block_size]
-            ints[1, lo:hi] = positions % block_size
-        longs_dev = torch.from_numpy(longs).to(device)
-        ints_dev = torch.from_numpy(ints).to(device)
-        packed_attention = prefill_attention_supported(weights.embedding.dtype, hq, hkv, d)
-        if packed_attention:
-            tiles = torch.from_numpy(prefill_tiles(lengths)).to(device)
-        tokens, positions_dev = longs_dev[0], longs_dev[1]
-        eps = config.rms_norm_eps
-        residual = F.embedding(tokens, weights.embedding)
-        h = rms_norm(residual, weights.layers[0].input_norm, eps)
-        q = torch.empty((total, hq, d), dtype=residual.dtype, device=device)
-        k = torch.empty((total, hkv, d), dtype=residual.dtype, device=device)
-        context = torch.empty((total, hq * d), dtype=residual.dtype, device=device)
-        for index, layer in enumerate(weights.layers):
-            qkv = F.linear(h, layer.qkv)
-            rope_paged_kv_append(qkv, positions_dev, weights.rope_cos, weights.rope_sin,
-                                 cache.key_cache[index], cache.value_cache[index], ints_dev[0],
-                                 ints_dev[1], ints_dev[2], query_heads=hq, query_output=q,
-                                 key_output=k)
-            if packed_attention:  # every prompt's causal attention in one launch
-                prefill_attention(q.view(total, hq * d), k.view(total, hkv * d),
-                                  qkv[:, (hq + hkv) * d:], tiles, query_heads=hq,
-                                  kv_heads=hkv, scale=d ** -0.5, output=context)
-            else:
-                v = qkv[:, (hq + hkv) * d:].view(total, hkv, d)
-                for i in range(len(request_ids)):
-                    lo, hi = int(bounds[i]), int(bounds[i + 1])
-                    context[lo:hi] = _causal_attention(q[lo:hi], k[lo:hi], v[lo:hi], d ** -0.5)
-            attn = F.linear(context, layer.o_proj)
-            residual, h = residual_rms_norm(attn, residual, layer.post_norm, eps)
-            act = swiglu_gate_up(F.linear(h, layer.gate_up))
-            next_norm = (weights.layers[index + 1].input_norm
-                         if index + 1 < len(weights.layers) else weights.final_norm)
-            residual, h = residual_rms_norm(F.linear(act, layer.down), residual, next_norm, eps)
-        last = torch.from_numpy(bounds[1:] - 1).to(device)
-        logits = F.linear(h.index_select(0, last), weights.lm_head)
+        logits = _prefill_packed(weights, cache, {r: list(p) for r, p in prompts.items()})
         first_tokens = torch.argmax(logits, dim=-1).tolist()
     except Exception:
         for reservation in reservations.values():
@@ -595,20 +684,61 @@ def prefill_batch(weights: DecoderWeights, cache: PagedKVCache,
     for reservation in reservations.values():
         cache.record_all_layers_written(reservation)
         cache.commit(reservation)
-    return {request_id: (first_tokens[i], logits[i]) for i, request_id in enumerate(request_ids)}
+    return {request_id: (first_tokens[i], logits[i]) for i, request_id in enumerate(prompts)}
 
 
 DEFAULT_BATCH_BUCKETS = (1, 2, 4, 8, 16, 32, 64)
 DEFAULT_CONTEXT_BUCKETS = (512, 1024, 2048, 4096)
 
 
+@dataclass(frozen=True, slots=True)
+class DecodeExecutionMetrics:
+    """Counters of the executor's step dispatch (the graph and fallback
+    fields of decode_bucket.py:140-154).  ``graph_misses`` counts steps
+    that captured their bucket's graph and steps that fell back to an
+    eager step because no bucket holds them; ``fallback_reasons`` counts
+    the latter by "batch_overflow", "context_overflow" or
+    "batch_and_context_overflow"."""
+
+    eager_calls: int
+    graph_calls: int
+    graph_hits: int
+    graph_misses: int
+    shape_fallbacks: int
+    eager_fallback_calls: int
+    capture_count: int
+    capture_time_ms: float
+    capture_warmup_time_ms: float
+    padded_lanes: int
+    fallback_reasons: dict[str, int]
+
+
+@dataclass(slots=True)
+class _MutableMetrics:
+    eager_calls: int = 0
+    graph_calls: int = 0
+    graph_hits: int = 0
+    graph_misses: int = 0
+    shape_fallbacks: int = 0
+    eager_fallback_calls: int = 0
+    capture_count: int = 0
+    capture_time_ms: float = 0.0
+    capture_warmup_time_ms: float = 0.0
+    padded_lanes: int = 0
+    fallback_reasons: dict[str, int] = field(default_factory=dict)
+
+
 @dataclass(slots=True)
 class DecodeTicket:
-    """One launched decode step whose sampled tokens have not been read yet."""
+    """One launched decode step whose sampled tokens have not been read yet.
+    ``request_ids`` are the requests that run in it, in lane order;
+    ``errors`` the requests of the launch that could not run, with why.
+    A launch in which no request could run has no slot (-1)."""
 
     request_ids: tuple[str, ...]
     bucket: tuple[int, int]
     slot: int
+    errors: dict[str, str] = field(default_factory=dict)
 
 
 @dataclass(frozen=True, slots=True)
@@ -616,6 +746,7 @@ class DecodeStepRecord:
     bucket: tuple[int, int]
     lanes: int
     device_ms: float
+    graph: bool = True
 
 
 class BucketedDecodeExecutor:
@@ -627,7 +758,17 @@ class BucketedDecodeExecutor:
     launched step needs no host token: its lane's sample is fed back on the
     device.  So a serving loop can launch step n+1 before reading step n's
     tokens and keep the GPU one step ahead of the host.  ``append_tokens``
-    is the reference's synchronous form (host tokens in, logits out).
+    and ``prefill_prompts`` are the reference's synchronous contract (host
+    tokens or prompts in, ``BatchExecutionResult`` of logits and per-request
+    errors out).
+
+    Failures are per request: a token outside the vocabulary, a missing
+    input token, a position past the RoPE table or a reservation the cache
+    cannot make fails that request alone, before anything is staged, and
+    the others run.  A step that no bucket holds (more requests than the
+    largest batch bucket, or a context past the largest context bucket) runs
+    eagerly on buffers sized for it, counted in ``metrics()`` with its
+    reason (decode_bucket.py:597-614).
     """
 
     _RING = 4
@@ -648,21 +789,31 @@ class BucketedDecodeExecutor:
         if self.context_buckets[-1] > cache.config.max_sequence_length:
             raise ValueError("context bucket exceeds cache sequence capacity")
         device = cache.config.device
-        lanes = self.batch_buckets[-1]
+        # One sampled-token slot per lane of any step: a step never holds
+        # more requests than the cache has sequences, fallback steps included.
+        lanes = max(self.batch_buckets[-1], cache.config.max_sequences)
         self.token_state = torch.zeros(lanes, dtype=torch.long, device=device)
         self._buckets: dict[tuple[int, int], DecodeGraphBucket] = {}
+        self._fallbacks: dict[tuple[int, int], DecodeGraphBucket] = {}
         self._last_lanes: dict[str, int] = {}
         self._readback = [torch.zeros(lanes, dtype=torch.long, pin_memory=True)
                           for _ in range(self._RING)]
         self._events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
                          torch.cuda.Event()) for _ in range(self._RING)]
         self._busy = [False] * self._RING
+        self._slot_bucket: list[DecodeGraphBucket | None] = [None] * self._RING
         self._next_slot = 0
+        self._metrics = _MutableMetrics()
         self.step_records: list[DecodeStepRecord] = []
 
     @property
     def vocab_size(self) -> int:
         return self.weights.config.vocab_size
+
+    def metrics(self) -> DecodeExecutionMetrics:
+        values = asdict(self._metrics)
+        values["fallback_reasons"] = dict(self._metrics.fallback_reasons)
+        return DecodeExecutionMetrics(**values)
 
     def create_request(self, request_id: str) -> None:
         self.cache.create_sequence(request_id)
@@ -671,28 +822,60 @@ class BucketedDecodeExecutor:
         self._last_lanes.pop(request_id, None)
         self.cache.release(request_id)
 
-    def prefill_prompts(self, prompts: dict[str, list[int]]) -> dict[str, int]:
-        """Prefill the prompts together; returns each one's greedy first token
-        (decode_bucket.py:567-570)."""
+    def prefill_prompts(self, prompts: dict[str, tuple[int, ...]]) -> BatchExecutionResult:
+        """Prefill the prompts together; the last position's logits of each
+        that ran and the errors of those that could not
+        (decode_bucket.py:567-570, runtime/prefill.py:37-149)."""
 
-        return {rid: token for rid, (token, _) in
-                prefill_batch(self.weights, self.cache, prompts).items()}
+        return prefill_requests(self.weights, self.cache, {r: list(p) for r, p in prompts.items()})
+
+    def prefill_tokens(self, prompts: dict[str, tuple[int, ...]],
+                       ) -> tuple[dict[str, int], dict[str, str]]:
+        """``prefill_prompts`` with the greedy first token of each prompt that
+        ran (one device-to-host copy) instead of its logits."""
+
+        result = self.prefill_prompts(prompts)
+        if not result.logits:
+            return {}, dict(result.errors)
+        ids = list(result.logits)
+        tokens = torch.argmax(torch.stack([result.logits[r] for r in ids]), dim=-1).tolist()
+        return dict(zip(ids, tokens)), dict(result.errors)
 
     def buffer_addresses(self) -> dict[str, dict[str, int]]:
         return {f"b{batch}-c{context}": bucket.addresses()
                 for (batch, context), bucket in self._buckets.items()}
 
-    def bucket(self, batch: int, context: int) -> DecodeGraphBucket:
+    def _capacities(self, batch: int, context: int) -> tuple[int | None, int | None]:
         batch_capacity = next((v for v in self.batch_buckets if v >= batch), None)
         context_capacity = next((v for v in self.context_buckets if v >= context), None)
+        return batch_capacity, context_capacity
+
+    def bucket(self, batch: int, context: int) -> DecodeGraphBucket:
+        batch_capacity, context_capacity = self._capacities(batch, context)
         if batch_capacity is None or context_capacity is None:
             raise ValueError(f"no decode bucket holds batch {batch} at context {context}")
         key = (batch_capacity, context_capacity)
         if key not in self._buckets:
             self._buckets[key] = DecodeGraphBucket(
                 self.weights, self.cache, batch_capacity=batch_capacity,
-                context_capacity=context_capacity, token_state=self.token_state)
+                context_capacity=context_capacity, token_state=self.token_state,
+                metrics=self._metrics)
         return self._buckets[key]
+
+    def _fallback_bucket(self, batch: int, context: int) -> DecodeGraphBucket:
+        """Eager buffers for a step no graph bucket holds: batch rounded up
+        to a multiple of 16 (within the cache's sequences), context up to
+        the cache's maximum sequence length."""
+
+        config = self.cache.config
+        capacity = min(-(-batch // 16) * 16, config.max_sequences)
+        key = (capacity, config.max_sequence_length)
+        if key not in self._fallbacks:
+            self._fallbacks[key] = DecodeGraphBucket(
+                self.weights, self.cache, batch_capacity=capacity,
+                context_capacity=config.max_sequence_length, token_state=self.token_state,
+                graph=False, metrics=self._metrics)
+        return self._fallbacks[key]
 
     def capture_all(self) -> None:
         """Capture every (batch, context) bucket now, with all lanes padded,
@@ -712,44 +895,79 @@ class BucketedDecodeExecutor:
     def launch(self, request_ids: list[str], tokens: dict[str, int] | None = None) -> DecodeTicket:
         """Append one token to each request and enqueue the step.  Requests in
         ``tokens`` take that input token; the others must have run in the
-        previously launched step, whose sample they continue from."""
+        previously launched step, whose sample they continue from.  Requests
+        that cannot run are left out of the step and listed in the ticket's
+        ``errors`` with nothing of theirs reserved."""
 
         tokens = tokens or {}
         if not request_ids:
             raise ValueError("launch requires at least one request")
-        for request_id in request_ids:
-            if request_id not in tokens and request_id not in self._last_lanes:
-                raise ValueError(f"{request_id}: no input token (not in the previous step)")
-            if request_id in tokens and not 0 <= tokens[request_id] < self.vocab_size:
-                raise ValueError(f"{request_id}: token_id is outside the model vocabulary")
         slot = self._next_slot
         if self._busy[slot]:
             raise RuntimeError("too many decode steps launched without collect()")
+        errors: dict[str, str] = {}
         reservations: dict[str, AppendReservation] = {}
-        try:
-            for request_id in request_ids:
-                reservations[request_id] = self.cache.begin_append(request_id, 1)
-            context = max(r.end_position for r in reservations.values())
-            bucket = self.bucket(len(request_ids), context)
-            bucket.prepare(list(request_ids), reservations, tokens=tokens,
-                           source_lanes=self._last_lanes)
-        except Exception:
-            for reservation in reservations.values():
+        max_position = self.weights.rope_cos.shape[0]
+        for request_id in request_ids:
+            if request_id in tokens:
+                if not 0 <= tokens[request_id] < self.vocab_size:
+                    errors[request_id] = "token_id is outside the model vocabulary"
+                    continue
+            elif request_id not in self._last_lanes:
+                errors[request_id] = "no input token (the request was not in the previous step)"
+                continue
+            try:
+                reservation = self.cache.begin_append(request_id, 1)
+            except Exception as error:  # noqa: BLE001 - reported per request
+                errors[request_id] = f"{type(error).__name__}: {error}"
+                continue
+            if reservation.start_position >= max_position:
                 self.cache.rollback(reservation)
-            raise
+                errors[request_id] = "position exceeds the model's RoPE table"
+                continue
+            reservations[request_id] = reservation
+        staged = list(reservations)
+        if not staged:
+            return DecodeTicket((), (0, 0), -1, errors)
+        context = max(r.end_position for r in reservations.values())
+        batch_capacity, context_capacity = self._capacities(len(staged), context)
+        try:
+            if batch_capacity is None or context_capacity is None:
+                reason = ("batch_and_context_overflow" if batch_capacity is None
+                          and context_capacity is None else
+                          "batch_overflow" if batch_capacity is None else "context_overflow")
+                metrics = self._metrics
+                metrics.shape_fallbacks += 1
+                metrics.eager_fallback_calls += 1
+                metrics.graph_misses += 1
+                metrics.fallback_reasons[reason] = metrics.fallback_reasons.get(reason, 0) + 1
+                bucket = self._fallback_bucket(len(staged), context)
+            else:
+                bucket = self.bucket(len(staged), context)
+            bucket.prepare(staged, reservations, tokens=tokens, source_lanes=self._last_lanes)
+        except Exception as error:  # noqa: BLE001 - nothing was launched
+            message = f"{type(error).__name__}: {error}"
+            for request_id, reservation in reservations.items():
+                self.cache.rollback(reservation)
+                errors[request_id] = message
+            return DecodeTicket((), (0, 0), -1, errors)
+        self._metrics.padded_lanes += bucket.batch_capacity - len(staged)
         begin, end, copied = self._events[slot]
         begin.record()
         try:
             bucket.execute()
-        except Exception:
+        except Exception as error:  # noqa: BLE001
             # Nothing of this step is committed; its lanes' previous samples
             # are no longer trusted as inputs either.
-            for reservation in reservations.values():
-                self.cache.rollback(reservation)
+            message = f"{type(error).__name__}: {error}"
+            for request_id, reservation in reservations.items():
+                with suppress(RuntimeError):
+                    self.cache.rollback(reservation)
+                errors[request_id] = message
             self._last_lanes = {}
-            raise
+            return DecodeTicket((), (0, 0), -1, errors)
         end.record()
-        lanes = len(request_ids)
+        lanes = len(staged)
         self._readback[slot][:lanes].copy_(self.token_state[:lanes], non_blocking=True)
         copied.record()
         # Host bookkeeping only: the step's device work is ordered before any
@@ -757,52 +975,91 @@ class BucketedDecodeExecutor:
         for reservation in reservations.values():
             self.cache.record_all_layers_written(reservation)
             self.cache.commit(reservation)
-        self._last_lanes = {request_id: lane for lane, request_id in enumerate(request_ids)}
+        self._last_lanes = {request_id: lane for lane, request_id in enumerate(staged)}
+        self._slot_bucket[slot] = bucket
         self._busy[slot] = True
         self._next_slot = (slot + 1) % self._RING
-        return DecodeTicket(tuple(request_ids), (bucket.batch_capacity, bucket.context_capacity),
-                            slot)
+        return DecodeTicket(tuple(staged), (bucket.batch_capacity, bucket.context_capacity),
+                            slot, errors)
 
     def collect(self, ticket: DecodeTicket) -> list[int]:
         """Wait for a launched step; its sampled token per request, in order."""
 
+        if ticket.slot < 0:
+            return []
         if not self._busy[ticket.slot]:
             raise RuntimeError("decode ticket was already collected")
         begin, end, copied = self._events[ticket.slot]
         copied.synchronize()
         lanes = len(ticket.request_ids)
         sampled = self._readback[ticket.slot][:lanes].tolist()
-        self.step_records.append(DecodeStepRecord(ticket.bucket, lanes, begin.elapsed_time(end)))
+        bucket = self._slot_bucket[ticket.slot]
+        self.step_records.append(DecodeStepRecord(ticket.bucket, lanes, begin.elapsed_time(end),
+                                                  bucket is not None and bucket.graph))
         self._busy[ticket.slot] = False
         return sampled
 
-    def append_tokens(self, tokens: dict[str, int]) -> dict[str, Tensor]:
-        """The reference's synchronous step: logits per request
-        (decode_bucket.py:582-666); views into the bucket's logits buffer,
-        valid until the next step."""
+    def logits_of(self, ticket: DecodeTicket) -> dict[str, Tensor]:
+        """The collected step's logits per request: views into its bucket's
+        logits buffer, valid until the bucket runs again."""
 
+        if ticket.slot < 0:
+            return {}
+        bucket = self._slot_bucket[ticket.slot]
+        return {request_id: bucket.logits[lane] for lane, request_id in enumerate(ticket.request_ids)}
+
+    def append_tokens(self, tokens: dict[str, int]) -> BatchExecutionResult:
+        """The reference's synchronous step (decode_bucket.py:582-666): logits
+        of every request that ran (views into the bucket's logits buffer,
+        valid until the next step) and the errors of those that could not."""
+
+        if not tokens:
+            raise ValueError("append_tokens requires at least one request")
         ticket = self.launch(list(tokens), tokens)
         self.collect(ticket)
-        bucket = self._buckets[ticket.bucket]
-        return {request_id: bucket.logits[lane] for lane, request_id in enumerate(tokens)}
+        return BatchExecutionResult(logits=self.logits_of(ticket), errors=dict(ticket.errors))
 
 
 def greedy_decode(executor: BucketedDecodeExecutor, prompts: dict[str, list[int]],
-                  steps: int) -> dict[str, list[int]]:
+                  steps: int, *, logits: dict[str, list[Tensor]] | None = None,
+                  ) -> dict[str, list[int]]:
     """Prefill each prompt, then decode ``steps - 1`` more greedy tokens for
     all of them together, keeping one step in flight: step n+1 is launched
-    (its inputs fed back on the device) before step n's tokens are read."""
+    (its inputs fed back on the device) before step n's tokens are read.
+    Raises on the first request that fails.
+
+    With ``logits`` (a dict to fill) every step is read back before the next
+    is launched -- the inputs are still fed back on the device -- and the
+    fp32 logits row behind each sampled token is appended per request."""
 
     outputs: dict[str, list[int]] = {}
     for request_id, prompt in prompts.items():
         executor.create_request(request_id)
-    first = executor.prefill_prompts(prompts)
+    if logits is None:
+        first, errors = executor.prefill_tokens(prompts)
+    else:
+        result = executor.prefill_prompts(prompts)
+        errors = dict(result.errors)
+        first = {}
+        for request_id, row in result.logits.items():
+            logits[request_id] = [row.float().cpu()]
+            first[request_id] = int(torch.argmax(row))
+    if errors:
+        raise RuntimeError(f"prefill failed: {errors}")
     for request_id in prompts:
         outputs[request_id] = [first[request_id]]
     order = list(prompts)
     pending: DecodeTicket | None = None
     for step in range(steps - 1):
         ticket = executor.launch(order, first if step == 0 else None)
+        if ticket.errors:
+            raise RuntimeError(f"decode step failed: {ticket.errors}")
+        if logits is not None:
+            for request_id, token in zip(order, executor.collect(ticket)):
+                outputs[request_id].append(token)
+            for request_id, row in executor.logits_of(ticket).items():
+                logits[request_id].append(row.float().cpu())
+            continue
         if pending is not None:
             for request_id, token in zip(order, executor.collect(pending)):
                 outputs[request_id].append(token)
@@ -811,4 +1068,3 @@ def greedy_decode(executor: BucketedDecodeExecutor, prompts: dict[str, list[int]
         for request_id, token in zip(order, executor.collect(pending)):
             outputs[request_id].append(token)
     return outputs
-

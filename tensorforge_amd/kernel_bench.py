@@ -313,7 +313,9 @@ def measure_decode_step(weights: DecoderWeights, batch: int, context: int, *,
         executor.create_request(rid)
     prompts = {rid: torch.randint(0, config.vocab_size, (n,), generator=generator).tolist()
                for rid, n in zip(rids, prompt_lengths)}
-    tokens = executor.prefill_prompts(prompts)
+    tokens, errors = executor.prefill_tokens(prompts)
+    if errors:
+        raise RuntimeError(f"prefill failed: {errors}")
     budget = context - prompt_length
     warm = min(4, budget // 4)
     timed = min(steps, budget - warm - 1)

@@ -414,11 +414,13 @@ def paged_gqa_decode_attention(
             ),
             "paged_gqa_decode_attention",
         )
+        # The reference's record, key for key (triton_attention.py:475-479;
+        # its test compares it with ==); launch details go to
+        # selected_attention_launch().
         _LAST_ATTENTION_CONFIG = {
             "path": "split_kv",
             "split_size": split_size,
             "num_splits": num_splits,
-            "waves_per_head": plan.waves_per_head if kernel == "mfma" else 1,
         }
     else:
         # One partition spanning the whole table: every present token of a
@@ -460,10 +462,10 @@ def paged_gqa_decode_attention(
             "path": "one_pass",
             "kernel": kernel,
             "workgroup": "sequence x kv_head",
-            "waves_per_head": plan.waves_per_head if kernel == "mfma" else 1,
         }
     _LAST_ATTENTION_LAUNCH = {
         "kernel": kernel,
+        "waves_per_head": plan.waves_per_head if kernel == "mfma" else 1,
         "grid": (batch * kv_heads, num_splits),
         "in_kernel_merge": bool(use_split_kv and counters_ptr is not None),
         "group_size": group,

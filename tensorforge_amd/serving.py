@@ -69,6 +69,7 @@ class RequestTrace:
     token_ns: list[int] = field(default_factory=list)
     generated: list[int] = field(default_factory=list)
     completed_ns: int | None = None
+    error: str | None = None  # set when the request failed (it still completes)
 
 
 def synthetic_requests(count: int = 512, *, rate: float = 20.0, vocab_size: int = 32000,
@@ -92,14 +93,27 @@ def synthetic_requests(count: int = 512, *, rate: float = 20.0, vocab_size: int 
 
 
 class ContinuousServer:
-    """Admission, prefill and pipelined decode over one executor."""
+    """Admission, prefill and pipelined decode over one executor.
+
+    A request the executor cannot serve -- its prefill or one of its decode
+    steps reports an error (an exhausted cache, an invalid token) -- fails
+    alone: it is completed with the error recorded and its sequence
+    released, and the other requests carry on (the reference fails only
+    that request, scheduler/continuous.py:284-299).
+    """
 
     def __init__(self, executor: BucketedDecodeExecutor, *, max_batch: int = 64,
-                 max_prefill_tokens: int = 8192, progress_s: float = 5.0) -> None:
+                 max_prefill_tokens: int = 8192, progress_s: float = 5.0,
+                 logits: dict[str, list] | None = None) -> None:
+        """``logits`` (a dict to fill, for checkers): every step is read back
+        before the next is launched and the fp32 logits row behind each
+        sampled token is appended per request; the schedule is unchanged."""
+
         self.executor = executor
         self.max_batch = max_batch
         self.max_prefill_tokens = max_prefill_tokens
         self.progress_s = progress_s
+        self.logits = logits
 
     def run(self, requests: list[RequestSpec]) -> list[RequestTrace]:
         executor = self.executor
@@ -115,10 +129,13 @@ class ContinuousServer:
         done = 0
         last_report = t0
 
-        def finish(request_id: str, now: int) -> None:
+        def finish(request_id: str, now: int, error: str | None = None) -> None:
             nonlocal done
-            traces[request_id].completed_ns = now
-            running.remove(request_id)
+            trace = traces[request_id]
+            trace.completed_ns = now
+            trace.error = error
+            if request_id in running:
+                running.remove(request_id)
             executor.release_request(request_id)
             done += 1
 
@@ -147,8 +164,18 @@ class ContinuousServer:
                 budget -= len(spec.prompt)
             host_tokens: dict[str, int] = {}
             if admitted:
-                first = executor.prefill_prompts(admitted)
+                if self.logits is None:
+                    first, failed = executor.prefill_tokens(admitted)
+                else:
+                    result = executor.prefill_prompts(admitted)
+                    failed = dict(result.errors)
+                    first = {}
+                    for request_id, row in result.logits.items():
+                        self.logits[request_id] = [row.float().cpu()]
+                        first[request_id] = int(torch.argmax(row))
                 stamp = clock()
+                for request_id, message in failed.items():
+                    finish(request_id, stamp, message)
                 for request_id, token in first.items():
                     trace = traces[request_id]
                     trace.generated.append(token)
@@ -164,12 +191,34 @@ class ContinuousServer:
             if order:
                 ticket = executor.launch(order, {r: host_tokens[r] for r in order
                                                  if r in host_tokens})
-                for request_id in order:
+                for request_id in ticket.request_ids:
                     launched[request_id] += 1
+                for request_id, message in ticket.errors.items():
+                    finish(request_id, clock(), message)
+                if ticket.slot < 0:
+                    ticket = None
+            if self.logits is not None and ticket is not None:
+                # Read this step back before the next launch, with its logits.
+                if in_flight is not None:
+                    raise RuntimeError("a recorded run keeps no step in flight")
+                in_flight, ticket = ticket, None
+                sampled = executor.collect(in_flight)
+                for request_id, row in executor.logits_of(in_flight).items():
+                    self.logits[request_id].append(row.float().cpu())
+                stamp = clock()
+                for request_id, token in zip(in_flight.request_ids, sampled):
+                    trace = traces[request_id]
+                    trace.generated.append(token)
+                    trace.token_ns.append(stamp)
+                    if len(trace.generated) >= trace.max_new_tokens:
+                        finish(request_id, stamp)
+                in_flight = None
             if in_flight is not None:
                 sampled = executor.collect(in_flight)
                 stamp = clock()
                 for request_id, token in zip(in_flight.request_ids, sampled):
+                    if request_id not in running:
+                        continue  # failed in the step launched since
                     trace = traces[request_id]
                     trace.generated.append(token)
                     trace.token_ns.append(stamp)
@@ -199,13 +248,15 @@ def summarize(traces: list[RequestTrace], executor: BucketedDecodeExecutor) -> d
     """The reference's serving metrics (metrics/statistics.py:40-98) plus
     the decode-only rate and per-bucket step time."""
 
+    failed = [t for t in traces if t.error is not None]
+    served = [t for t in traces if t.error is None]
     generated = sum(len(t.generated) for t in traces)
     first_arrival = min(t.arrival_ns for t in traces)
     last_completion = max(t.completed_ns for t in traces)
-    ttft = [(t.token_ns[0] - t.arrival_ns) / 1e6 for t in traces]
+    ttft = [(t.token_ns[0] - t.arrival_ns) / 1e6 for t in served if t.token_ns]
     tpot = [(t.completed_ns - t.token_ns[0]) / (len(t.generated) - 1) / 1e6
-            for t in traces if len(t.generated) > 1]
-    latency = [(t.completed_ns - t.arrival_ns) / 1e6 for t in traces]
+            for t in served if len(t.generated) > 1]
+    latency = [(t.completed_ns - t.arrival_ns) / 1e6 for t in served]
     records = executor.step_records
     lanes = sum(r.lanes for r in records)
     device_ms = sum(r.device_ms for r in records)
@@ -217,6 +268,7 @@ def summarize(traces: list[RequestTrace], executor: BucketedDecodeExecutor) -> d
         "decode_tokens_per_second": round(lanes / (device_ms / 1e3), 1) if device_ms else None,
         "generated_tokens": generated,
         "requests": len(traces),
+        "failed_requests": len(failed),
         "decode_steps": len(records),
         "mean_lanes_per_step": round(lanes / max(len(records), 1), 2),
         "ttft_ms": _percentiles(ttft),

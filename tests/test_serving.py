@@ -36,7 +36,13 @@ class StubExecutor:
 
     vocab_size = VOCAB
 
-    def __init__(self) -> None:
+    def __init__(self, fail_prefill: set[str] | None = None,
+                 fail_step: dict[str, int] | None = None) -> None:
+        # Requests whose prefill reports an error, and requests whose n-th
+        # decode launch reports one (the executor's per-request errors).
+        self.fail_prefill = set(fail_prefill or ())
+        self.fail_step = dict(fail_step or {})
+        self.launches: dict[str, int] = {}
         self.live: set[str] = set()
         self.max_live = 0
         self.created: list[str] = []
@@ -56,32 +62,44 @@ class StubExecutor:
         self.live.remove(request_id)
         self._previous.pop(request_id, None)
 
-    def prefill_prompts(self, prompts: dict[str, list[int]]) -> dict[str, int]:
+    def prefill_tokens(self, prompts: dict[str, list[int]]) -> tuple[dict[str, int], dict[str, str]]:
         assert set(prompts) <= self.live
-        return {rid: len(prompt) % VOCAB for rid, prompt in prompts.items()}
+        errors = {rid: "CacheExhaustedError: no pages" for rid in prompts if rid in self.fail_prefill}
+        return ({rid: len(prompt) % VOCAB for rid, prompt in prompts.items() if rid not in errors},
+                errors)
 
     def launch(self, request_ids: list[str], tokens: dict[str, int] | None = None) -> DecodeTicket:
         tokens = tokens or {}
         inputs = {}
+        errors = {}
         for rid in request_ids:
             assert rid in self.live, f"{rid} launched after release"
+            self.launches[rid] = self.launches.get(rid, 0) + 1
+            if self.fail_step.get(rid) == self.launches[rid]:
+                errors[rid] = "CacheExhaustedError: no pages"
+                continue
             if rid in tokens:
                 inputs[rid] = tokens[rid]
             else:
                 assert rid in self._previous, f"{rid} has no token to continue from"
                 inputs[rid] = self._previous[rid]
+        if not inputs:
+            return DecodeTicket((), (0, 0), -1, errors)
         assert len(self._pending) < 3, "too many steps in flight"
         sampled = {rid: next_token(token) for rid, token in inputs.items()}
         self._previous = dict(sampled)
         slot = self._next
         self._next += 1
         self._pending[slot] = _Launched(sampled)
-        self.steps.append(tuple(request_ids))
-        bucket = 1 << max(0, (len(request_ids) - 1).bit_length())
-        self.step_records.append(DecodeStepRecord((bucket, 512), len(request_ids), 1.0))
-        return DecodeTicket(tuple(request_ids), (bucket, 512), slot)
+        staged = tuple(inputs)
+        self.steps.append(staged)
+        bucket = 1 << max(0, (len(staged) - 1).bit_length())
+        self.step_records.append(DecodeStepRecord((bucket, 512), len(staged), 1.0))
+        return DecodeTicket(staged, (bucket, 512), slot, errors)
 
     def collect(self, ticket: DecodeTicket) -> list[int]:
+        if ticket.slot < 0:
+            return []
         launched = self._pending.pop(ticket.slot)
         return [launched.tokens[rid] for rid in ticket.request_ids]
 
@@ -121,13 +139,13 @@ def test_burst_respects_the_batch_limit_and_generates_every_token() -> None:
 def test_prefill_budget_limits_admission_per_iteration() -> None:
     executor = StubExecutor()
     calls: list[int] = []
-    original = executor.prefill_prompts
+    original = executor.prefill_tokens
 
     def counting(prompts):
         calls.append(len(prompts))
         return original(prompts)
 
-    executor.prefill_prompts = counting
+    executor.prefill_tokens = counting
     requests = _requests([100, 100, 100, 40, 40], [3, 3, 3, 3, 3])
     ContinuousServer(executor, max_batch=8, max_prefill_tokens=150, progress_s=0).run(requests)
     # 100 alone (a second 100 exceeds the rest of the budget), then 100,
@@ -161,3 +179,36 @@ def test_synthetic_requests_match_the_workload() -> None:
     assert all(0 <= t < 32000 for r in requests[:20] for t in r.prompt)
     burst = synthetic_requests(8, burst=True)
     assert all(r.arrival_s == 0.0 for r in burst)
+
+
+def test_a_failed_decode_step_fails_only_its_request() -> None:
+    """An executor error for one request mid-run (an exhausted cache at its
+    third decode launch) completes that request with the error and releases
+    it; every other request still gets all of its tokens
+    (scheduler/continuous.py:284-299)."""
+
+    executor = StubExecutor(fail_step={"r2": 3})
+    requests = _requests([5, 9, 3, 12, 7], [6, 6, 6, 6, 6])
+    traces = ContinuousServer(executor, max_batch=8, progress_s=0).run(requests)
+    assert not executor.live  # every sequence released, the failed one too
+    for spec, trace in zip(requests, traces):
+        if spec.request_id == "r2":
+            assert trace.error is not None and "CacheExhausted" in trace.error
+            # prefill's token and the first two decode steps' samples, at most
+            assert 1 <= len(trace.generated) <= 3
+            assert trace.generated == _expected(3, len(trace.generated))
+        else:
+            assert trace.error is None
+            assert trace.generated == _expected(len(spec.prompt), spec.max_new_tokens)
+    summary = summarize(traces, executor)
+    assert summary["failed_requests"] == 1 and summary["requests"] == 5
+
+
+def test_a_failed_prefill_fails_only_its_request() -> None:
+    executor = StubExecutor(fail_prefill={"r1"})
+    requests = _requests([5, 9, 3], [4, 4, 4])
+    traces = ContinuousServer(executor, max_batch=8, progress_s=0).run(requests)
+    assert not executor.live
+    assert traces[1].error is not None and traces[1].generated == []
+    assert traces[0].generated == _expected(5, 4) and traces[2].generated == _expected(3, 4)
+    assert "r1" not in {rid for step in executor.steps for rid in step}
