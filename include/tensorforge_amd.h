@@ -169,6 +169,30 @@ int32_t tf_paged_gqa_decode_rope_append(
     int32_t flags, void *stream);
 
 /*
+ * tf_paged_gqa_decode without a caller workspace: no partial buffers and no
+ * counters are passed, and nothing is allocated.  No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Split partials (num_splits > 1: batch * query_heads *
+ * num_splits rows of next_pow2(head_dim) + 2 floats) live in a fixed
+ * device array of TF_NOALLOC_SCRATCH_BYTES that each GPU holds until the
+ * process ends; larger requests fail with TF_ERROR_INVALID_ARGUMENT.  The
+ * split stage writes every partial the merge reads, so the array needs no
+ * clearing.  All calls on one GPU share that array: calls that overlap in
+ * time on one GPU race.  The STREAM flag (which needs counters) is
+ * rejected; other arguments are as in tf_paged_gqa_decode, whose kernels it
+ * runs, with the same results.
+ */
+#define TF_NOALLOC_SCRATCH_BYTES (8LL << 20)
+int32_t tf_paged_gqa_decode_noalloc(
+    const void *query, const void *key_cache, const void *value_cache,
+    const int32_t *block_tables, const int32_t *context_lengths, void *output,
+    int32_t batch, int32_t query_heads, int32_t kv_heads, int32_t head_dim,
+    int32_t num_blocks, int32_t block_size, int32_t table_width,
+    int32_t split_size, int32_t num_splits, float scale, int32_t dtype,
+    int32_t flags, void *stream);
+
+/*
  * First stage of tf_paged_gqa_decode alone (num_splits >= 1): writes the
  * partials of every non-empty split.  Partial max values are base-2
  * logarithms of the unnormalised scores (score * scale * log2(e)).

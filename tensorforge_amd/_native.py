@@ -28,6 +28,7 @@ TF_ATTENTION_WAVES_PER_CU_SHIFT = 8
 TF_ATTENTION_DEPTH_SHIFT = 16
 TF_ATTENTION_HEADS_PER_WG_SHIFT = 20
 TF_ATTENTION_TOKENS_PER_WAVE_SHIFT = 24
+TF_NOALLOC_SCRATCH_BYTES = 8 << 20
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: TF_DTYPE_FLOAT32,
@@ -48,6 +49,12 @@ SIGNATURES: dict[str, tuple[Any, ...]] = {
     "tf_paged_gqa_decode": (
         _p, _p, _p, _p, _p, _p,  # query, key/value cache, tables, lengths, output
         _p, _p, _p, _p, _i64, _i32,  # partials, counters, capacity, row stride
+        _i32, _i32, _i32, _i32,  # batch, query heads, kv heads, head dim
+        _i32, _i32, _i32,  # num blocks, block size, table width
+        _i32, _i32, _f32, _i32, _i32, _p,  # split size, splits, scale, dtype, flags, stream
+    ),
+    "tf_paged_gqa_decode_noalloc": (
+        _p, _p, _p, _p, _p, _p,  # query, key/value cache, tables, lengths, output
         _i32, _i32, _i32, _i32,  # batch, query heads, kv heads, head dim
         _i32, _i32, _i32,  # num blocks, block size, table width
         _i32, _i32, _f32, _i32, _i32, _p,  # split size, splits, scale, dtype, flags, stream

@@ -49,6 +49,8 @@
 //   split kernel      triton_attention.py:173-266 (partials :260-266)
 //   reduce kernel     triton_attention.py:268-316 (LSE merge :288-316)
 //   oracle            kernels/reference.py:46-93
+#include <mutex>
+
 #include "tf_common.hpp"
 
 namespace tf {
@@ -2155,4 +2157,102 @@ extern "C" int32_t tf_paged_gqa_decode_merge(
   return launch_merge(partial_max, partial_sum, partial_accumulator, context_lengths, output,
                       batch, query_heads, head_dim, split_size, num_splits, partial_row_stride,
                       clamp, dtype, static_cast<hipStream_t>(stream));
+}
+
+// ===========================================================================
+// tf_paged_gqa_decode_noalloc: the same call with no caller workspace
+// ===========================================================================
+// For callers that cannot allocate device memory (code under HIP graph
+// capture, tight serving loops, harnesses that forbid hipMalloc).  The
+// split partials live in `scratch`, a fixed array of this library that every
+// GPU holds in its own memory until the process ends.  In host code the
+// array's name is only a stand-in: the device address comes from
+// hipGetSymbolAddress, taken once per device (with that device current) on
+// the first call there, and only that address is passed to kernels.  The
+// split kernel writes every partial the merge reads (empty splits are never
+// read), so nothing in `scratch` has to start at zero; arrival counters are
+// not used (no in-kernel merge, no STREAM flag).  Every call on a GPU shares
+// that GPU's array: calls that overlap in time on one GPU race.
+
+static __device__ __align__(256) unsigned char scratch[TF_NOALLOC_SCRATCH_BYTES];
+
+namespace tf {
+namespace {
+
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_lock;
+void *g_scratch_address[kScratchMaxDevices] = {};
+
+// Device address of `scratch` on the current device.
+int32_t scratch_address(void **out) {
+  int device = -1;
+  const hipError_t got = hipGetDevice(&device);
+  if (got != hipSuccess || device < 0 || device >= kScratchMaxDevices) {
+    set_error("no usable current HIP device for the attention scratch (%s)",
+              hipGetErrorString(got));
+    return TF_ERROR_LAUNCH;
+  }
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch_address[device] == nullptr) {
+    void *address = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || address == nullptr) {
+      set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                hipGetErrorString(err));
+      return TF_ERROR_LAUNCH;
+    }
+    g_scratch_address[device] = address;
+  }
+  *out = g_scratch_address[device];
+  return TF_SUCCESS;
+}
+
+}  // namespace
+}  // namespace tf
+
+extern "C" int32_t tf_paged_gqa_decode_noalloc(
+    const void *query, const void *key_cache, const void *value_cache,
+    const int32_t *block_tables, const int32_t *context_lengths, void *output, int32_t batch,
+    int32_t query_heads, int32_t kv_heads, int32_t head_dim, int32_t num_blocks,
+    int32_t block_size, int32_t table_width, int32_t split_size, int32_t num_splits, float scale,
+    int32_t dtype, int32_t flags, void *stream) {
+  using namespace tf;
+  clear_error();
+  if (flags & TF_ATTENTION_FLAG_STREAM)
+    return fail(TF_ERROR_UNSUPPORTED,
+                "the no-allocation attention call has no arrival counters (no STREAM flag)");
+  if (batch < 0 || query_heads <= 0 || head_dim <= 0 || head_dim > 256 || num_splits <= 0)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "attention dimensions out of range");
+  // Partials as the workspace lays them out: accumulator rows of
+  // next_pow2(head_dim) floats, then the maxima, then the sums.
+  int32_t stride = 1;
+  while (stride < head_dim) stride <<= 1;
+  const int64_t rows =
+      num_splits > 1 ? static_cast<int64_t>(batch) * query_heads * num_splits : 0;
+  const int64_t bytes = rows * (stride + 2) * static_cast<int64_t>(sizeof(float));
+  if (bytes > TF_NOALLOC_SCRATCH_BYTES) {
+    set_error("split partials of %lld rows need %lld bytes; the no-allocation scratch holds "
+              "%lld (use fewer splits or tf_paged_gqa_decode with a workspace)",
+              static_cast<long long>(rows), static_cast<long long>(bytes),
+              static_cast<long long>(TF_NOALLOC_SCRATCH_BYTES));
+    return TF_ERROR_INVALID_ARGUMENT;
+  }
+  if (batch > 0 && !output) return fail(TF_ERROR_INVALID_ARGUMENT, "null output pointer");
+  void *base = nullptr;
+  if (int32_t st = scratch_address(&base)) return st;
+  float *partial_acc = static_cast<float *>(base);
+  float *partial_max = partial_acc + rows * stride;
+  float *partial_sum = partial_max + rows;
+  AttnParams p;
+  if (int32_t st = make_params(p, query, key_cache, value_cache, block_tables, context_lengths,
+                               output, partial_max, partial_sum, partial_acc, nullptr, rows,
+                               stride, batch, query_heads, kv_heads, head_dim, num_blocks,
+                               block_size, table_width, split_size, num_splits, scale, dtype))
+    return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int32_t st = launch_split_stage(p, dtype, flags, s)) return st;
+  if (num_splits == 1) return TF_SUCCESS;
+  return launch_merge(partial_max, partial_sum, partial_acc, context_lengths, output, batch,
+                      query_heads, head_dim, split_size, num_splits, stride, p.max_tokens, dtype,
+                      s);
 }

@@ -86,7 +86,7 @@ def test_header_constants_match_the_python_binding() -> None:
 
 
 def test_abi_version_and_variant_selection(lib) -> None:
-    assert lib.tf_abi_version() == 9
+    assert lib.tf_abi_version() == 10
     variant = lib.tf_paged_gqa_decode_variant
     bf16, f16, f32 = (_native.TF_DTYPE_BFLOAT16, _native.TF_DTYPE_FLOAT16,
                       _native.TF_DTYPE_FLOAT32)
@@ -356,3 +356,19 @@ def test_bench_refuses_more_than_one_gpu() -> None:
     assert result.returncode == 2
     message = json.loads(result.stdout.strip().splitlines()[-1])
     assert "one GPU" in message["error"] and message["n_gpus"] == 2
+
+
+def test_noalloc_attention_rejects_what_its_scratch_cannot_hold(lib) -> None:
+    """The size checks of tf_paged_gqa_decode_noalloc come before any HIP
+    call: 4 rows x 32 heads x 2048 splits of (64 + 2) floats exceed the
+    8 MiB array, and the STREAM flag needs counters the call does not have."""
+
+    bf16 = _native.TF_DTYPE_BFLOAT16
+    call = lib.tf_paged_gqa_decode_noalloc
+    status = call(None, None, None, None, None, None, 4, 32, 4, 64, 10, 16, 64, 32, 2048,
+                  0.125, bf16, 0, None)
+    assert status == 1 and b"no-allocation scratch holds 8388608" in lib.tf_last_error()
+    status = call(None, None, None, None, None, None, 4, 32, 4, 64, 10, 16, 64, 32, 2, 0.125,
+                  bf16, _native.TF_ATTENTION_FLAG_STREAM, None)
+    assert status == 2 and b"no arrival counters" in lib.tf_last_error()
+    assert _native.TF_NOALLOC_SCRATCH_BYTES == 8 << 20
