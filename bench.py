@@ -89,6 +89,84 @@ def copy_calibration(mib: int) -> int:
     return 0
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the baseline labels."""
+
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def read_ceiling(nbytes: int) -> dict:
+    """What this GPU streams from HBM, measured in this process: the library's
+    read probe (contiguous slices, 16-byte nontemporal loads) over 1 GiB and
+    over the attention call's own byte count, each rotated over regions the
+    256 MB Infinity Cache cannot hold, the best of a few launch shapes (swept
+    on MI355X: 512 x 4 waves for 1 GiB, 4096 x 16 waves for ~80 MB); and the
+    reference's method, a torch copy_ of 256 MiB counted as read + write
+    (benchmark/kernel_benchmark.py:176-192)."""
+
+    from tensorforge_amd import _native
+
+    lib = _native.library()
+    device = torch.device("cuda", 0)
+    buffer = torch.ones(3 << 28, dtype=torch.int32, device=device)  # 3 GiB
+    sink = torch.zeros(1, dtype=torch.int32, device=device)
+    total = buffer.numel() * 4
+
+    def timed(size: int, shape: tuple[int, int, int]) -> float:
+        size -= size % 16
+        regions = max(2, min(12, total // size))
+        stride = (total // regions) // 256 * 256
+        reps = 24 if size < (256 << 20) else 8
+        stream = torch.cuda.Stream(device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(reps):
+                _native.check(lib.tf_hbm_read_probe(
+                    buffer.data_ptr() + (i % regions) * stride, size, *shape, sink.data_ptr(),
+                    stream.cuda_stream), "read probe")
+        graph.replay()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            begin = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            begin.record()
+            graph.replay()
+            end.record()
+            end.synchronize()
+            best = min(best, begin.elapsed_time(end) / reps)
+        return size / (best * 1e-3) / 1e9
+
+    one_gib = max(timed(1 << 30, shape) for shape in ((512, 4, 4), (256, 8, 4), (4096, 4, 8)))
+    same = max(timed(nbytes, shape) for shape in ((4096, 16, 4), (8192, 8, 8), (2048, 16, 4)))
+    source = buffer[: (256 << 20) // 4]
+    destination = torch.empty_like(source)
+    for _ in range(3):
+        destination.copy_(source)
+    torch.cuda.synchronize()
+    begin = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    begin.record()
+    for _ in range(10):
+        destination.copy_(source)
+    end.record()
+    end.synchronize()
+    copy = 2 * source.numel() * 4 / (begin.elapsed_time(end) / 10 * 1e-3) / 1e9
+    del buffer, source, destination
+    torch.cuda.empty_cache()
+    return {"read_1GiB": round(one_gib, 1), "read_same_bytes": round(same, 1),
+            "copy_256MiB": round(copy, 1), "unit": "GB/s",
+            "method": "tf_hbm_read_probe graph replays (best launch shape), 1 GiB and the "
+                      "call's byte count, regions rotated past the MALL; torch copy_ of 256 MiB "
+                      "counted as 2 x bytes (the reference's ceiling)"}
+
+
 def cpu_baseline(case, rows: list[int], seconds: float) -> dict:
     """Time the CPU oracle (fp32 torch on the host cores) on ``rows``."""
 
@@ -119,7 +197,7 @@ def cpu_baseline(case, rows: list[int], seconds: float) -> dict:
         "sample": (
             f"CPU oracle paged_gqa_decode_reference (fp32 torch {torch.__version__}) on "
             f"{len(rows)} of the 64 active rows (sum ctx {sum(lengths)}), p50 of "
-            f"{len(samples)} reps = {p50 * 1e3:.2f} ms; {platform.processor() or platform.machine()}"
+            f"{len(samples)} reps = {p50 * 1e3:.2f} ms; {cpu_model()}"
         ),
     }
 
@@ -199,7 +277,7 @@ def decode_step_cpu_baseline(weights, contexts: list[int], seconds: float) -> di
         "sample": (
             f"oracle decode_step_reference (fp32 torch {torch.__version__}), 22 layers, "
             f"{batch} of the 64 rows (contexts {contexts}), p50 of {len(samples)} steps = "
-            f"{p50 * 1e3:.1f} ms; {platform.processor() or platform.machine()}"
+            f"{p50 * 1e3:.1f} ms; {cpu_model()}"
         ),
     }
 
@@ -271,7 +349,7 @@ def kernels_line(calls: int, seconds_per_case: float) -> dict:
                                  "kind": "port"}
     return {"metric": "config 3 and 4 kernels, graph-timed, CPU oracle beside each",
             "unit": "GB/s", "cases": cases + [attention],
-            "cpu": platform.processor() or platform.machine()}
+            "cpu": cpu_model()}
 
 
 def main() -> int:
@@ -455,9 +533,18 @@ def main() -> int:
     nbytes = decode_attention_bytes(lengths, query_heads, kv_heads, head_dim, block_size, 2)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     achieved = nbytes / (split_ms * 1e-3) / 1e9
+    # Counter traffic is reported only when the committed profile was taken of
+    # this very launch (kernel, plan and load form); otherwise null.
+    launch_signature = (f"{'mfma' if variant == _native.TF_ATTENTION_MFMA else 'generic'}"
+                        f"|{'one_pass' if one_pass else 'split_kv'}|waves={plan.waves_per_head}"
+                        f"|tokens_per_wave={plan.tokens_per_wave}|split={split_size}"
+                        f"|merge={args.merge}|abi={lib.tf_abi_version()}")
     traffic = None
-    if TRAFFIC_FILE.exists() and one_pass:  # the profile covers the default one-pass plan
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    if TRAFFIC_FILE.exists():
+        profiled = json.loads(TRAFFIC_FILE.read_text())
+        if profiled.get("launch") == launch_signature:
+            traffic = profiled.get("hbm_bytes_per_launch")
+    ceiling = read_ceiling(nbytes)
 
     result = {
         "metric": METRIC,
@@ -501,6 +588,10 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "launch": launch_signature,
+            "ceiling": ceiling,
+            "frac_of_ceiling": round(achieved / ceiling["read_1GiB"], 4),
+            "frac_of_same_size_read": round(achieved / ceiling["read_same_bytes"], 4),
             "kernel": "paged_decode_mfma_kernel"
             + (" (one pass, the whole call)" if one_pass
                else " (split stage with in-kernel merge)" if fused else " (split stage)"),

@@ -43,6 +43,10 @@
  *   tf_linear_swiglu         the MLP's gate|up projection with its SwiGLU
  *                            (model/layers.py:144-158)
  *   tf_prefill_attention     prefill's causal attention (runtime/prefill.py:84-88, 109-118)
+ *   tf_hbm_read_probe        measurement only: the read-rate ceiling the attention
+ *                            roofline is compared with (the reference measures
+ *                            its ceiling with a device copy,
+ *                            tensorforge/benchmark/kernel_benchmark.py:176-192)
  */
 #ifndef TENSORFORGE_AMD_H_
 #define TENSORFORGE_AMD_H_
@@ -86,9 +90,18 @@ enum tf_attention_variant {
  *   bits 16-19  streaming kernel: tiles in flight per wavefront (2..4)
  *   bits 20-23  grid kernel: kv heads per workgroup (must divide kv_heads)
  *   bits 24-30  grid kernel: tokens per wavefront / 64; a row then uses
- *               ceil(its tokens / that) of the head's wavefronts (0: all) */
+ *               ceil(its tokens / that) of the head's wavefronts (0: all)
+ * PAGES (one-pass calls of tf_paged_gqa_decode: bf16/fp16, head_dim
+ * 32/64/128, group <= 16, 16-token pages, kv_heads <= 8 with
+ * kv_heads * head_dim * 2 <= 1024, batch <= 2048) streams the batch's pages
+ * in equal contiguous ranges, one workgroup (a wavefront per kv head) per
+ * range: bits 8-15 give workgroups per compute unit (default 1), bits 16-19
+ * pages in flight per workgroup (2..4, default 3).  It needs split_counters
+ * and partial buffers of at least 2 x workgroups x query_heads rows: rows
+ * split over several ranges are merged in the same launch. */
 #define TF_ATTENTION_FLAG_FORCE_GENERIC 1
 #define TF_ATTENTION_FLAG_STREAM 4
+#define TF_ATTENTION_FLAG_PAGES 8
 #define TF_ATTENTION_WAVES_PER_CU_SHIFT 8
 #define TF_ATTENTION_DEPTH_SHIFT 16
 #define TF_ATTENTION_HEADS_PER_WG_SHIFT 20
@@ -475,6 +488,17 @@ int32_t tf_prefill_attention(const void *q, int64_t q_row_stride, const void *k,
                              int32_t query_heads, int32_t kv_heads, int32_t head_dim,
                              float scale, int32_t heads_per_wave, int32_t dtype,
                              void *stream);
+
+/*
+ * Measurement only: stream `bytes` (a positive multiple of 16) of the
+ * 16-byte aligned `buffer` from HBM with 16-byte nontemporal loads.
+ * `workgroups` workgroups of `waves` (1..16) wavefronts each read one
+ * contiguous slice, `loads` (2, 4 or 8) loads in flight per lane.  `sink` is
+ * one uint32 the kernel may write (so the loads are kept).  Timing it gives
+ * the attainable read rate the attention kernels are compared with.
+ */
+int32_t tf_hbm_read_probe(const void *buffer, int64_t bytes, int32_t workgroups,
+                          int32_t waves, int32_t loads, uint32_t *sink, void *stream);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,7 @@ TF_ATTENTION_GENERIC = 0
 TF_ATTENTION_MFMA = 1
 TF_ATTENTION_FLAG_FORCE_GENERIC = 1
 TF_ATTENTION_FLAG_STREAM = 4
+TF_ATTENTION_FLAG_PAGES = 8
 TF_ATTENTION_WAVES_PER_CU_SHIFT = 8
 TF_ATTENTION_DEPTH_SHIFT = 16
 TF_ATTENTION_HEADS_PER_WG_SHIFT = 20
@@ -44,6 +45,7 @@ _f32 = ctypes.c_float
 # name -> argument types, in header order.
 SIGNATURES: dict[str, tuple[Any, ...]] = {
     "tf_last_error": (),
+    "tf_hbm_read_probe": (_p, _i64, _i32, _i32, _i32, _p, _p),
     "tf_abi_version": (),
     "tf_paged_gqa_decode_variant": (_i32, _i32, _i32, _i32, _i32),
     "tf_paged_gqa_decode": (

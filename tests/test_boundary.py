@@ -75,6 +75,7 @@ def test_library_exports_every_declared_symbol(lib) -> None:
 def test_header_constants_match_the_python_binding() -> None:
     text = HEADER.read_text()
     for name in ("TF_ATTENTION_FLAG_FORCE_GENERIC", "TF_ATTENTION_FLAG_STREAM",
+                 "TF_ATTENTION_FLAG_PAGES",
                  "TF_ATTENTION_WAVES_PER_CU_SHIFT", "TF_ATTENTION_DEPTH_SHIFT",
                  "TF_ATTENTION_HEADS_PER_WG_SHIFT", "TF_ATTENTION_TOKENS_PER_WAVE_SHIFT"):
         match = re.search(rf"#define {name} (\d+)", text)
