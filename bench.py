@@ -101,14 +101,21 @@ def cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
-def read_ceiling(nbytes: int) -> dict:
+def read_ceiling(nbytes: int, gather: dict | None = None) -> dict:
     """What this GPU streams from HBM, measured in this process: the library's
     read probe (contiguous slices, 16-byte nontemporal loads) over 1 GiB and
     over the attention call's own byte count, each rotated over regions the
     256 MB Infinity Cache cannot hold, the best of a few launch shapes (swept
     on MI355X: 512 x 4 waves for 1 GiB, 4096 x 16 waves for ~80 MB); and the
     reference's method, a torch copy_ of 256 MiB counted as read + write
-    (benchmark/kernel_benchmark.py:176-192)."""
+    (benchmark/kernel_benchmark.py:176-192).
+
+    With ``gather`` (``pools``: the rotated (key, value) caches, ``pages``:
+    the call's physical pages in row order on the device, ``page_bytes``,
+    ``num_blocks``), also the library's page-gather probe over exactly
+    those pages -- the call's own scattered-page reads and nothing else,
+    best of a few launch shapes -- reported as its time and as the call's
+    algorithmic bytes over that time."""
 
     from tensorforge_amd import _native
 
@@ -160,11 +167,65 @@ def read_ceiling(nbytes: int) -> dict:
     copy = 2 * source.numel() * 4 / (begin.elapsed_time(end) / 10 * 1e-3) / 1e9
     del buffer, source, destination
     torch.cuda.empty_cache()
-    return {"read_1GiB": round(one_gib, 1), "read_same_bytes": round(same, 1),
-            "copy_256MiB": round(copy, 1), "unit": "GB/s",
-            "method": "tf_hbm_read_probe graph replays (best launch shape), 1 GiB and the "
-                      "call's byte count, regions rotated past the MALL; torch copy_ of 256 MiB "
-                      "counted as 2 x bytes (the reference's ceiling)"}
+    result = {"read_1GiB": round(one_gib, 1), "read_same_bytes": round(same, 1),
+              "copy_256MiB": round(copy, 1), "unit": "GB/s",
+              "method": "tf_hbm_read_probe graph replays (best launch shape), 1 GiB and the "
+                        "call's byte count, regions rotated past the MALL; torch copy_ of 256 MiB "
+                        "counted as 2 x bytes (the reference's ceiling)"}
+    if gather is not None:
+        gather_us = page_gather_us(**gather)
+        result["gather_call_pages_us"] = round(gather_us, 3)
+        result["gather_call_pages"] = round(nbytes / (gather_us * 1e-6) / 1e9, 1)
+        result["gather_method"] = ("tf_hbm_page_gather_probe over the call's own pages (whole "
+                                   "pages, rotated pools, best of 3 launch shapes): the call's "
+                                   "algorithmic bytes / the probe's time")
+    return result
+
+
+def page_gather_us(pools: list, pages: torch.Tensor, page_bytes: int, num_blocks: int) -> float:
+    """Graph-timed microseconds of reading ``pages`` of every pool's K and V
+    caches once (one pool per launch, rotated), the best of a few launch
+    shapes (swept on MI355X at config 2: 256 x 8 waves best, 13.8 us)."""
+
+    from tensorforge_amd import _native
+
+    lib = _native.library()
+    device = pages.device
+    sink = torch.zeros(1, dtype=torch.int32, device=device)
+    best = float("inf")
+    for workgroups, waves in ((256, 8), (512, 8), (1024, 8)):
+        reps = 6 * len(pools)
+        stream = torch.cuda.Stream(device)
+        stream.wait_stream(torch.cuda.current_stream(device))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(reps):
+                key_cache, value_cache = pools[i % len(pools)]
+                _native.check(lib.tf_hbm_page_gather_probe(
+                    key_cache.data_ptr(), value_cache.data_ptr(), pages.data_ptr(),
+                    pages.numel(), page_bytes, num_blocks, workgroups, waves, sink.data_ptr(),
+                    stream.cuda_stream), "page gather probe")
+        torch.cuda.current_stream(device).wait_stream(stream)
+        graph.replay()
+        torch.cuda.synchronize()
+        for _ in range(3):
+            begin = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            begin.record()
+            graph.replay()
+            end.record()
+            end.synchronize()
+            best = min(best, begin.elapsed_time(end) * 1e3 / reps)
+    return best
+
+
+def call_pages(block_tables: torch.Tensor, lengths: list[int], block_size: int) -> torch.Tensor:
+    """The physical pages an attention call reads, in row order (host side)."""
+
+    pages = []
+    for row, ctx in enumerate(lengths):
+        pages.extend(int(page) for page in block_tables[row, : (ctx + block_size - 1) // block_size])
+    return torch.tensor(pages, dtype=torch.int32)
 
 
 def cpu_baseline(case, rows: list[int], seconds: float) -> dict:
@@ -544,7 +605,11 @@ def main() -> int:
         profiled = json.loads(TRAFFIC_FILE.read_text())
         if profiled.get("launch") == launch_signature:
             traffic = profiled.get("hbm_bytes_per_launch")
-    ceiling = read_ceiling(nbytes)
+    num_blocks = gpu.key_cache.shape[0]
+    page_bytes = gpu.key_cache[0].numel() * gpu.key_cache.element_size()
+    ceiling = read_ceiling(nbytes, gather={
+        "pools": pools, "pages": call_pages(case.block_tables, lengths, block_size).to(device),
+        "page_bytes": page_bytes, "num_blocks": num_blocks})
 
     result = {
         "metric": METRIC,
@@ -592,6 +657,7 @@ def main() -> int:
             "ceiling": ceiling,
             "frac_of_ceiling": round(achieved / ceiling["read_1GiB"], 4),
             "frac_of_same_size_read": round(achieved / ceiling["read_same_bytes"], 4),
+            "frac_of_page_gather": round(achieved / ceiling["gather_call_pages"], 4),
             "kernel": "paged_decode_mfma_kernel"
             + (" (one pass, the whole call)" if one_pass
                else " (split stage with in-kernel merge)" if fused else " (split stage)"),

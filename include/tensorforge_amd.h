@@ -47,6 +47,9 @@
  *                            roofline is compared with (the reference measures
  *                            its ceiling with a device copy,
  *                            tensorforge/benchmark/kernel_benchmark.py:176-192)
+ *   tf_hbm_page_gather_probe measurement only: the rate of reading one attention
+ *                            call's K/V pages and nothing else (no counterpart
+ *                            in the reference)
  */
 #ifndef TENSORFORGE_AMD_H_
 #define TENSORFORGE_AMD_H_
@@ -499,6 +502,21 @@ int32_t tf_prefill_attention(const void *q, int64_t q_row_stride, const void *k,
  */
 int32_t tf_hbm_read_probe(const void *buffer, int64_t bytes, int32_t workgroups,
                           int32_t waves, int32_t loads, uint32_t *sink, void *stream);
+
+/*
+ * Measurement only: read every byte of the K and V pages listed in `pages`
+ * (npages physical page ids; ids outside [0, num_blocks) are skipped), each
+ * page `page_bytes` (a positive multiple of 1024) in both caches, with
+ * 16-byte nontemporal loads: `workgroups` workgroups of `waves` (1..16)
+ * wavefronts, each wavefront an equal contiguous range of the list.  No
+ * compute and no output besides the `sink` word.  Timing it over the page
+ * list of an attention call gives the attainable rate of that call's own
+ * scattered-page access pattern.  No counterpart in the reference.
+ */
+int32_t tf_hbm_page_gather_probe(const void *key_cache, const void *value_cache,
+                                 const int32_t *pages, int32_t npages, int64_t page_bytes,
+                                 int32_t num_blocks, int32_t workgroups, int32_t waves,
+                                 uint32_t *sink, void *stream);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,7 @@ _f32 = ctypes.c_float
 SIGNATURES: dict[str, tuple[Any, ...]] = {
     "tf_last_error": (),
     "tf_hbm_read_probe": (_p, _i64, _i32, _i32, _i32, _p, _p),
+    "tf_hbm_page_gather_probe": (_p, _p, _p, _i32, _i64, _i32, _i32, _i32, _p, _p),
     "tf_abi_version": (),
     "tf_paged_gqa_decode_variant": (_i32, _i32, _i32, _i32, _i32),
     "tf_paged_gqa_decode": (

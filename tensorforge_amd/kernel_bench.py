@@ -189,7 +189,13 @@ def attention_ceiling(device: torch.device, calls: int) -> list[dict]:
     * config 2 itself with its random pages and with the same rows on
       contiguous pages (page locality);
     * 16 rows x 2048 (64 compute units busy) with 1..8 wavefronts per kv
-      head through the C ABI: one compute unit's ceiling at low load.
+      head through the C ABI: one compute unit's ceiling at low load;
+    * the read probe with one workgroup (one compute unit alone) at 4..16
+      wavefronts and 4 or 8 loads in flight per lane: a compute unit's read
+      rate against the bytes it keeps in flight;
+    * the page-gather probe over config 2's own pages (every byte of each
+      K and V page, no compute) at several launch shapes: the attainable
+      rate of the call's scattered-page reads.
     Every case rotates 6 copies of its page pool (the MALL cannot hold them).
     """
 
@@ -278,6 +284,47 @@ def attention_ceiling(device: torch.device, calls: int) -> list[dict]:
         result["GB/s_per_compute_unit_beyond_fixed"] = round(
             result["algorithmic_bytes"] / 64 / (result["us_per_call"] - fixed_us) / 1e3, 1)
         results.append(result)
+
+    lib = _native.library()
+    sink = torch.zeros(1, dtype=torch.int32, device=device)
+    region = 8 << 20
+    regions = 40  # 320 MiB rotated: no region is served from the MALL
+    buffer = torch.ones(regions * region // 4, dtype=torch.int32, device=device)
+    for waves, loads in ((4, 4), (8, 4), (8, 8), (16, 4), (16, 8)):
+        def read_one_unit(i: int, waves=waves, loads=loads) -> None:
+            _native.check(lib.tf_hbm_read_probe(
+                buffer.data_ptr() + (i % regions) * region, region, 1, waves, loads,
+                sink.data_ptr(), _native.current_stream(device)), "read probe")
+
+        us = graph_time_us(read_one_unit, 20, device)
+        results.append({"case": f"read probe, one compute unit, {waves} wavefronts x {loads} "
+                                f"loads ({waves * loads} KB in flight)",
+                        "us_per_call": round(us, 2), "GB/s": round(region / us / 1e3, 1)})
+    del buffer
+    torch.cuda.empty_cache()
+
+    gpu = config2.to(device)
+    pools = [(gpu.key_cache, gpu.value_cache)] + [
+        (gpu.key_cache.clone(), gpu.value_cache.clone()) for _ in range(5)]
+    page_list = []
+    for row, ctx in enumerate(config2.lengths):
+        page_list.extend(int(p) for p in config2.block_tables[row, : (ctx + 15) // 16])
+    pages = torch.tensor(page_list, dtype=torch.int32, device=device)
+    page_bytes = gpu.key_cache[0].numel() * gpu.key_cache.element_size()
+    nbytes2 = workloads.decode_attention_bytes(config2.lengths, 32, 4, 64, 16, 2)
+    for workgroups, waves in ((256, 4), (256, 8), (512, 8), (1024, 8), (2048, 4)):
+        def gather(i: int, workgroups=workgroups, waves=waves) -> None:
+            key_cache, value_cache = pools[i % len(pools)]
+            _native.check(lib.tf_hbm_page_gather_probe(
+                key_cache.data_ptr(), value_cache.data_ptr(), pages.data_ptr(), pages.numel(),
+                page_bytes, gpu.key_cache.shape[0], workgroups, waves, sink.data_ptr(),
+                _native.current_stream(device)), "page gather probe")
+
+        us = graph_time_us(gather, calls, device)
+        results.append({"case": f"page gather of config 2's {pages.numel()} pages, "
+                                f"{workgroups} x {waves} wavefronts",
+                        "us_per_call": round(us, 3),
+                        "call_bytes_GB/s": round(nbytes2 / us / 1e3, 1)})
     return results
 
 

@@ -373,3 +373,24 @@ def test_noalloc_attention_rejects_what_its_scratch_cannot_hold(lib) -> None:
                   bf16, _native.TF_ATTENTION_FLAG_STREAM, None)
     assert status == 2 and b"no arrival counters" in lib.tf_last_error()
     assert _native.TF_NOALLOC_SCRATCH_BYTES == 8 << 20
+
+
+def test_measurement_probes_reject_bad_arguments_before_launch(lib) -> None:
+    """The read and page-gather probes validate sizes, shapes and pointers on
+    the host: nothing reaches the device (no GPU here)."""
+
+    sink = ctypes.c_uint32(0)
+    read = lib.tf_hbm_read_probe
+    assert read(None, 1 << 20, 256, 4, 4, ctypes.byref(sink), None) == 1          # no buffer
+    assert read(ctypes.c_void_p(16), 100, 256, 4, 4, ctypes.byref(sink), None) == 1  # not x16
+    assert read(ctypes.c_void_p(16), 1 << 20, 256, 17, 4, ctypes.byref(sink), None) == 1
+    gather = lib.tf_hbm_page_gather_probe
+    page = ctypes.c_void_p(256)
+    assert gather(page, page, page, 10, 1000, 64, 256, 8, ctypes.byref(sink), None) == 1  # % 1024
+    assert gather(page, page, page, 10, 8192, 0, 256, 8, ctypes.byref(sink), None) == 1   # blocks
+    assert gather(page, page, None, 10, 8192, 64, 256, 8, ctypes.byref(sink), None) == 1  # list
+    assert gather(page, ctypes.c_void_p(8), page, 10, 8192, 64, 256, 8, ctypes.byref(sink),
+                  None) == 1                                                           # aligned
+    assert b"page gather probe" in lib.tf_last_error()
+    # an empty page list is a no-op that launches nothing
+    assert gather(None, None, None, 0, 8192, 64, 256, 8, ctypes.byref(sink), None) == 0
