@@ -101,10 +101,15 @@ enum tf_attention_variant {
  * range: bits 8-15 give workgroups per compute unit (default 1), bits 16-19
  * pages in flight per workgroup (2..4, default 3).  It needs split_counters
  * and partial buffers of at least 2 x workgroups x query_heads rows: rows
- * split over several ranges are merged in the same launch. */
+ * split over several ranges are merged in the same launch.
+ * VALU (the MFMA grid kernel's calls, head_dim 64, no RoPE) computes the
+ * score and P.V products on the VALU -- packed two-element dot products
+ * (v_dot2_f32_bf16 / _f16) and fp32 FMAs -- with the same grid, loads and
+ * LDS staging: the comparison form for the MFMA products. */
 #define TF_ATTENTION_FLAG_FORCE_GENERIC 1
 #define TF_ATTENTION_FLAG_STREAM 4
 #define TF_ATTENTION_FLAG_PAGES 8
+#define TF_ATTENTION_FLAG_VALU 16
 #define TF_ATTENTION_WAVES_PER_CU_SHIFT 8
 #define TF_ATTENTION_DEPTH_SHIFT 16
 #define TF_ATTENTION_HEADS_PER_WG_SHIFT 20

@@ -450,6 +450,41 @@ __host__ __device__ constexpr int mfma_lds_bytes(int head_dim, int waves) {
 constexpr float kRescaleThreshold = 8.f;
 constexpr int kSegmentTiles = 64;  // page-window capacity: 64 tiles = 1024 tokens
 
+// c + a . b over 8 elements with the packed two-element dot product
+// (v_dot2_f32_bf16 / v_dot2_f32_f16: fp32 products and accumulation) -- the
+// VALU form of the score product.
+template <typename T>
+__device__ __forceinline__ float dot8(T __attribute__((ext_vector_type(8))) a,
+                                      T __attribute__((ext_vector_type(8))) b, float c);
+
+template <>
+__device__ __forceinline__ float dot8<__bf16>(__bf16 __attribute__((ext_vector_type(8))) a,
+                                              __bf16 __attribute__((ext_vector_type(8))) b,
+                                              float c) {
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 0, 1),
+                                      __builtin_shufflevector(b, b, 0, 1), c, false);
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 2, 3),
+                                      __builtin_shufflevector(b, b, 2, 3), c, false);
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 4, 5),
+                                      __builtin_shufflevector(b, b, 4, 5), c, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 6, 7),
+                                         __builtin_shufflevector(b, b, 6, 7), c, false);
+}
+
+template <>
+__device__ __forceinline__ float dot8<_Float16>(_Float16 __attribute__((ext_vector_type(8))) a,
+                                                _Float16 __attribute__((ext_vector_type(8))) b,
+                                                float c) {
+  c = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 0, 1),
+                             __builtin_shufflevector(b, b, 0, 1), c, false);
+  c = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 2, 3),
+                             __builtin_shufflevector(b, b, 2, 3), c, false);
+  c = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 4, 5),
+                             __builtin_shufflevector(b, b, 4, 5), c, false);
+  return __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 6, 7),
+                                __builtin_shufflevector(b, b, 6, 7), c, false);
+}
+
 // Wave-level layout of one 32-token chunk (tiles j = 0, 1 of 16 tokens):
 //   loads    LINES: lane holds bytes [16 (lane % (D/8)), +16) of the K / V
 //            slice of token 16j + lane / (D/8) + (512/D) ks (whole token
@@ -466,7 +501,7 @@ constexpr int kSegmentTiles = 64;  // page-window capacity: 64 tiles = 1024 toke
 //            V[4q4 + e][16n + i] for e = 0..3.
 // Requires block_size % 16 == 0 and split_size % 32 == 0 (a tile never
 // straddles a page), so each tile's page is wave-uniform.
-template <typename T, int D, int NW, bool ROPE, bool LINES>
+template <typename T, int D, int NW, bool ROPE, bool LINES, bool VALU = false>
 __global__ void __launch_bounds__(NW * 64)
 paged_decode_mfma_kernel(AttnParams p) {
   using M = Mfma<T>;
@@ -561,6 +596,17 @@ paged_decode_mfma_kernel(AttnParams p) {
     }
   }
   if constexpr (!ROPE) page_win = load_window(0);
+  // VALU form: the whole query row of head l16 (zeros for l16 >= group).
+  vec8 qv[VALU ? D / 8 : 1];
+  if constexpr (VALU) {
+    const bool own = l16 < p.group;
+    const T *qrow = static_cast<const T *>(p.query) +
+                    (static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(kvh) * p.group +
+                     (own ? l16 : 0)) * D;
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c)
+      qv[c] = own ? *reinterpret_cast<const vec8 *>(qrow + 8 * c) : vec8{};
+  }
 
   if (s0 >= ctx) {
     if (split == 0) zero_rows<T>(p, b, grp * HPW * p.group, HPW * p.group);
@@ -672,22 +718,41 @@ paged_decode_mfma_kernel(AttnParams p) {
         for (int ks = 0; ks < KS; ++ks)
           *reinterpret_cast<vec8 *>(vt + (16 * j + v_tok + kVTokens * ks) * kRow + v_piece) = kf[j][ks];
       __asm__ volatile("" ::: "memory");
+      if constexpr (!VALU) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            kf[j][ks] =
+                *reinterpret_cast<const vec8 *>(vt + (16 * j + l16) * kRow + (32 * ks + 8 * q4) * 2);
+        __asm__ volatile("" ::: "memory");
+      }
+    }
+    float sc[8];  // raw q.k of token 16j + 4q4 + r, head l16
+    if constexpr (VALU) {
+      // Packed two-element dot products of the whole query row against the
+      // staged K rows of the lane's 8 tokens (v_dot2_f32_{bf16,f16}).
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          kf[j][ks] =
-              *reinterpret_cast<const vec8 *>(vt + (16 * j + l16) * kRow + (32 * ks + 8 * q4) * 2);
+        for (int r = 0; r < 4; ++r) {
+          const unsigned char *krow = vt + (16 * j + 4 * q4 + r) * kRow;
+          float dot = 0.f;
+#pragma unroll
+          for (int c = 0; c < D / 8; ++c)
+            dot = dot8<T>(qv[c], *reinterpret_cast<const vec8 *>(krow + 16 * c), dot);
+          sc[4 * j + r] = dot;
+        }
       __asm__ volatile("" ::: "memory");
-    }
-    float sc[8];  // raw q.k of token 16j + 4q4 + r, head l16
+    } else {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 2; ++j) {
+        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) s = M::mma(kf[j][ks], qf[ks], s);
+        for (int ks = 0; ks < KS; ++ks) s = M::mma(kf[j][ks], qf[ks], s);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[4 * j + r] = s[r];
+        for (int r = 0; r < 4; ++r) sc[4 * j + r] = s[r];
+      }
     }
     if ((valid[0] & valid[1]) != 0xffffu) {  // uniform: partial chunk
 #pragma unroll
@@ -744,14 +809,42 @@ paged_decode_mfma_kernel(AttnParams p) {
             vt + (LINES ? (16 * j + v_tok + kVTokens * ks) * kRow + v_piece
                         : (16 * j + l16) * kRow + (32 * ks + 8 * q4) * 2)) = vf[j][ks];
     __asm__ volatile("" ::: "memory");
-    const unsigned char *rd = vt + (4 * q4 + (l16 >> 2)) * kRow + (l16 & 3) * 8;
+    if constexpr (VALU) {
+      // P of head l16 for all 32 tokens through the wavefront's LDS slice
+      // (the weights rounded to T, as the MFMA form feeds them), then
+      // acc[n][r] += p[t] * V[t][16n + 4q4 + r] with fp32 FMAs.
+      float *pb = reinterpret_cast<float *>(lds + mfma_lds_bytes(D, blockDim.x >> 6)) +
+                  wave * 16 * kChunk + l16 * kChunk;
+      *reinterpret_cast<f32x4 *>(pb + 4 * q4) =
+          f32x4{to_float(pf[0]), to_float(pf[1]), to_float(pf[2]), to_float(pf[3])};
+      *reinterpret_cast<f32x4 *>(pb + 16 + 4 * q4) =
+          f32x4{to_float(pf[4]), to_float(pf[5]), to_float(pf[6]), to_float(pf[7])};
+      __asm__ volatile("" ::: "memory");
 #pragma unroll
-    for (int n = 0; n < NB; ++n) {
-      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(rd + 32 * n));
-      const i16x4 hi =
-          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(rd + 16 * kRow + 32 * n));
-      const i16x8 a16 = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[n] = M::mma(__builtin_bit_cast(vec8, a16), pf, acc[n]);
+      for (int t4 = 0; t4 < kChunk; t4 += 4) {
+        const f32x4 pt = *reinterpret_cast<const f32x4 *>(pb + t4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const unsigned char *vrow = vt + (t4 + e) * kRow + 8 * q4;
+#pragma unroll
+          for (int n = 0; n < NB; ++n) {
+            typedef T t4v __attribute__((ext_vector_type(4)));
+            const t4v v = *reinterpret_cast<const t4v *>(vrow + 32 * n);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[n][r] = __builtin_fmaf(pt[e], to_float(v[r]), acc[n][r]);
+          }
+        }
+      }
+    } else {
+      const unsigned char *rd = vt + (4 * q4 + (l16 >> 2)) * kRow + (l16 & 3) * 8;
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(rd + 32 * n));
+        const i16x4 hi =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(rd + 16 * kRow + 32 * n));
+        const i16x8 a16 = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        acc[n] = M::mma(__builtin_bit_cast(vec8, a16), pf, acc[n]);
+      }
     }
     __asm__ volatile("" ::: "memory");
   };
@@ -2324,6 +2417,18 @@ void launch_mfma_form(const AttnParams &p, dim3 grid, hipStream_t stream) {
                        dim3(waves * 64), lds, stream, p);
 }
 
+// The VALU form of the one-pass / split kernel (TF_ATTENTION_FLAG_VALU): the
+// same grid, loads and LDS staging (whole token rows, K staged token-major),
+// with the score and P.V products on the VALU; head_dim 64 without RoPE.
+template <typename T>
+void launch_valu(const AttnParams &p, dim3 grid, hipStream_t stream) {
+  const int waves = p.heads_per_wg * p.waves_per_head;
+  const size_t lds = static_cast<size_t>(mfma_lds_bytes(64, waves)) +
+                     static_cast<size_t>(waves) * 16 * kChunk * sizeof(float);
+  hipLaunchKernelGGL((paged_decode_mfma_kernel<T, 64, kMfmaWaves, false, true, true>), grid,
+                     dim3(waves * 64), lds, stream, p);
+}
+
 template <typename T, int D>
 void launch_mfma(const AttnParams &p, dim3 grid, hipStream_t stream) {
   if (p.rope_qkv)
@@ -2522,6 +2627,15 @@ int32_t launch_split_stage(const AttnParams &p, int32_t dtype, int32_t flags, hi
     mfma_geometry(q, flags);
     const dim3 mgrid(static_cast<unsigned>(p.batch) * static_cast<unsigned>(p.kv_heads / q.heads_per_wg),
                      static_cast<unsigned>(p.num_splits));
+    if (flags & TF_ATTENTION_FLAG_VALU) {
+      if (p.head_dim != 64 || p.rope_qkv != nullptr)
+        return fail(TF_ERROR_UNSUPPORTED, "the VALU attention form supports head_dim 64 without RoPE");
+      if (dtype == TF_DTYPE_BFLOAT16)
+        launch_valu<__bf16>(q, mgrid, stream);
+      else
+        launch_valu<_Float16>(q, mgrid, stream);
+      return check_launch("paged_gqa_decode (valu)");
+    }
     if (dtype == TF_DTYPE_BFLOAT16)
       launch_mfma_dim<__bf16>(q, mgrid, stream);
     else

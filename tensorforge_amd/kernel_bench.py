@@ -16,8 +16,11 @@
   launch/collect loop;
 * ceiling -- what bounds the config-2 attention call: the graph launch gap,
   a fit of time against bytes over uniform-length batches (fixed cost per
-  call and marginal rate), config 2 on random and on contiguous pages, and
-  one compute unit's rate with 1..8 wavefronts per kv head;
+  call and marginal rate), config 2 on random and on contiguous pages, one
+  compute unit's rate with 1..8 wavefronts per kv head and with the read
+  probe alone, and the page-gather probe over config 2's own pages;
+* valu (only with ``--only valu``) -- the attention kernel's products on
+  MFMA against its VALU form, at config 2's lengths with group 8 and 4;
 * projections -- the decode step's projections at TinyLlama shapes and 1 /
   16 / 64 rows (weights rotated through HBM): hipBLASLt against the paths
   the decode bucket takes (linear_kstream for qkv, linear_stream partials
@@ -328,6 +331,62 @@ def attention_ceiling(device: torch.device, calls: int) -> list[dict]:
     return results
 
 
+def valu_comparison(device: torch.device, calls: int) -> list[dict]:
+    """The attention products on MFMA against the VALU form of the same grid
+    kernel (TF_ATTENTION_FLAG_VALU: packed bf16 dot products for the scores,
+    fp32 FMAs for P.V; same loads, LDS staging, softmax and epilogue), at
+    config 2's lengths with group 8 (32/4 heads) and group 4 (16/4 heads,
+    the same K/V bytes), bf16, through the C ABI with the entry point's
+    one-pass plan (4 wavefronts per kv head, 576 tokens each) and with one
+    wavefront per (row, kv head).  6 rotated page pools."""
+
+    from tensorforge_amd import _native
+
+    lib = _native.library()
+    results = []
+    config2 = workloads.tinyllama_decode_case(seed=0, dtype=torch.bfloat16)
+    plans = {
+        "one pass, 4 wavefronts per kv head": (
+            (1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
+            | (4 << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
+            | ((576 // 64) << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT)),
+        "one pass, 1 wavefront per kv head": 0,
+    }
+    for query_heads in (32, 16):
+        case = workloads.make_decode_attention_case(
+            config2.lengths, query_heads=query_heads, kv_heads=4, head_dim=64, block_size=16,
+            dtype=torch.bfloat16, seed=0)
+        gpu = case.to(device)
+        pools = [(gpu.key_cache, gpu.value_cache)] + [
+            (gpu.key_cache.clone(), gpu.value_cache.clone()) for _ in range(5)]
+        output = torch.empty_like(gpu.query)
+        batch = gpu.query.shape[0]
+        num_blocks, block_size, kv_heads, head_dim = gpu.key_cache.shape
+        width = gpu.block_tables.shape[1]
+        nbytes = workloads.decode_attention_bytes(case.lengths, query_heads, kv_heads, head_dim,
+                                                  block_size, 2)
+        for plan, plan_flags in plans.items():
+            row = {"case": f"group {query_heads // kv_heads}, {plan}"}
+            for form, form_flags in (("mfma", 0), ("valu", _native.TF_ATTENTION_FLAG_VALU)):
+                def run(i: int, flags=plan_flags | form_flags) -> None:
+                    key_cache, value_cache = pools[i % len(pools)]
+                    _native.check(lib.tf_paged_gqa_decode(
+                        gpu.query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+                        gpu.block_tables.data_ptr(), gpu.context_lengths.data_ptr(),
+                        output.data_ptr(), None, None, None, None, 0, head_dim, batch,
+                        query_heads, kv_heads, head_dim, num_blocks, block_size, width,
+                        (width * block_size + 31) // 32 * 32, 1, case.scale,
+                        _native.dtype_code(gpu.query.dtype), flags,
+                        _native.current_stream(device)), "tf_paged_gqa_decode")
+
+                us = graph_time_us(run, calls, device)
+                row[f"{form}_us"] = round(us, 3)
+                row[f"{form}_GB/s"] = round(nbytes / us / 1e3, 1)
+            row["valu_over_mfma"] = round(row["valu_us"] / row["mfma_us"], 3)
+            results.append(row)
+    return results
+
+
 def measure_decode_step(weights: DecoderWeights, batch: int, context: int, *,
                         steps: int = 64, seed: int = 0,
                         prompt_lengths: list[int] | None = None) -> dict:
@@ -482,7 +541,7 @@ def projections(device: torch.device, calls: int) -> list[dict]:
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--calls", type=int, default=100)
-    parser.add_argument("--only", choices=("cfg3", "cfg4", "decode", "decode22", "ceiling",
+    parser.add_argument("--only", choices=("cfg3", "cfg4", "decode", "decode22", "ceiling", "valu",
                                            "projections"), default=None)
     args = parser.parse_args()
     if not torch.cuda.is_available():
@@ -498,6 +557,9 @@ def main() -> int:
         decode_steps(device, "cfg1")
     if args.only in (None, "decode22"):
         decode_steps(device, "tinyllama")
+    if args.only == "valu":
+        for result in valu_comparison(device, args.calls):
+            print(json.dumps(result), flush=True)
     if args.only in (None, "ceiling"):
         for result in attention_ceiling(device, args.calls):
             print(json.dumps(result), flush=True)
