@@ -67,6 +67,7 @@ from tensorforge_amd.kernels import (
     swiglu,
     swiglu_gate_up,
 )
+from tensorforge_amd.kernels.attention import attention_plan
 from tensorforge_amd.kernels.linear import default_splits
 
 HBM_PEAK_GBS = 8000.0
@@ -156,25 +157,71 @@ def config4(device: torch.device, calls: int) -> list[dict]:
     return results
 
 
-def config3(device: torch.device, calls: int) -> dict:
+def config3(device: torch.device, calls: int) -> list[dict]:
+    """Config 3 (4 rows of 8k..32k at Llama-3-8B geometry) four ways: the
+    entry point's tuned plan (partition size chosen per call, merge launch);
+    the BASELINE's form, 512-token partitions and a separate log-sum-exp
+    merge launch (the entry point with the partition size fixed at 512, as
+    the reference's split_size argument fixes it); and both partition sizes
+    with the in-kernel merge instead (the C ABI with the workspace's arrival
+    counters: the last partition of each (row, kv head) merges)."""
+
+    from tensorforge_amd import _native
+
     case = workloads.llama3_long_context_case(seed=0)
     pools = [case.to(device) for _ in range(2)]  # 2 x 671 MB: the MALL cannot hold them
     batch, query_heads, head_dim = case.query.shape
+    num_blocks, block_size, kv_heads, _ = case.key_cache.shape
+    width = case.block_tables.shape[1]
     workspace = PagedAttentionWorkspace.allocate(
         batch_capacity=batch, query_heads=query_heads, head_dim=head_dim,
         max_context_length=32768, device=device)
     output = torch.empty_like(pools[0].query)
+    nbytes = workloads.decode_attention_bytes(case.lengths, query_heads, kv_heads, head_dim,
+                                              block_size, 2)
+    name = "paged_gqa_decode cfg3 (4 x 8k..32k, 32/8 heads, D128, bf16)"
+    results = []
 
-    def run(i: int) -> None:
+    def entry(i: int) -> None:
         gpu = pools[i % 2]
         paged_gqa_decode_attention(gpu.query, gpu.key_cache, gpu.value_cache, gpu.block_tables,
                                    gpu.context_lengths, scale=case.scale,
                                    max_context_length=32768, output=output, workspace=workspace)
 
-    us = graph_time_us(run, calls, device)
-    nbytes = workloads.decode_attention_bytes(case.lengths, query_heads, 8, head_dim, 16, 2)
-    return report("paged_gqa_decode cfg3 (4 x 8k..32k, 32/8 heads, D128, bf16)", us, nbytes,
-                  record=selected_attention_autotune_config())
+    us = graph_time_us(entry, calls, device)
+    tuned = dict(selected_attention_autotune_config() or {})
+    results.append(report(f"{name}, tuned plan, merge launch", us, nbytes, record=tuned))
+
+    previous = set_attention_split_size(512)
+    try:
+        us = graph_time_us(entry, calls, device)
+        results.append(report(f"{name}, 512-token partitions, merge launch (BASELINE form)", us,
+                              nbytes, record=dict(selected_attention_autotune_config() or {})))
+    finally:
+        set_attention_split_size(previous)
+
+    capacity = workspace.partial_max.numel()
+    tuned_plan = attention_plan(32768, batch, kv_heads, 32768)
+    for split, flags in ((512, 0), (tuned_plan.split_size, tuned_plan.flags)):
+        splits = -(-32768 // split)
+
+        def fused(i: int, split=split, splits=splits, flags=flags) -> None:
+            gpu = pools[i % 2]
+            _native.check(_native.library().tf_paged_gqa_decode(
+                gpu.query.data_ptr(), gpu.key_cache.data_ptr(), gpu.value_cache.data_ptr(),
+                gpu.block_tables.data_ptr(), gpu.context_lengths.data_ptr(), output.data_ptr(),
+                workspace.partial_max.data_ptr(), workspace.partial_sum.data_ptr(),
+                workspace.partial_accumulator.data_ptr(), workspace.split_counters.data_ptr(),
+                capacity, workspace.partial_accumulator.shape[1], batch, query_heads, kv_heads,
+                head_dim, num_blocks, block_size, width, split, splits, case.scale,
+                _native.dtype_code(case.query.dtype), flags, _native.current_stream(device)),
+                "tf_paged_gqa_decode (in-kernel merge)")
+
+        us = graph_time_us(fused, calls, device)
+        waves = tuned_plan.waves_per_head if flags else 1
+        results.append(report(f"{name}, {split}-token partitions, {waves} wavefront(s) each, "
+                              f"in-kernel merge", us, nbytes))
+    return results
 
 
 def attention_ceiling(device: torch.device, calls: int) -> list[dict]:
@@ -552,7 +599,8 @@ def main() -> int:
         for result in config4(device, args.calls):
             print(json.dumps(result), flush=True)
     if args.only in (None, "cfg3"):
-        print(json.dumps(config3(device, max(10, args.calls // 4))), flush=True)
+        for result in config3(device, max(10, args.calls // 4)):
+            print(json.dumps(result), flush=True)
     if args.only in (None, "decode"):
         decode_steps(device, "cfg1")
     if args.only in (None, "decode22"):
