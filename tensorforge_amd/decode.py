@@ -14,9 +14,12 @@ sequences runs as ONE captured HIP graph.  Per layer:
 * ``residual_rms_norm`` of (attention output, residual);
 * one fused gate|up projection, ``swiglu_gate_up``, the down projection.
 
-The gfx950 kernels of this package do the norm, cache and attention work,
-and the small projections at up to 16 rows; the other GEMMs are library
-GEMMs (torch -> hipBLASLt).  Every per-step input
+The gfx950 kernels of this package do the norm, cache and attention work
+and the projections (``_project`` and the bucket's o / down / gate|up
+launches: the K-split weight stream for qkv and for gate|up with its
+SwiGLU, LDS-staged slice sums for o and down, the weight stream for the LM
+head up to 32 rows); only the LM head of larger buckets is a library GEMM
+(torch -> hipBLASLt).  Every per-step input
 lives in one device "control" slab, filled from one pinned host slab with
 one asynchronous copy per step.  So the graph's addresses never change,
 and a step needs no host synchronisation beyond reading back the sampled
