@@ -94,21 +94,12 @@ enum tf_attention_variant {
  *   bits 20-23  grid kernel: kv heads per workgroup (must divide kv_heads)
  *   bits 24-30  grid kernel: tokens per wavefront / 64; a row then uses
  *               ceil(its tokens / that) of the head's wavefronts (0: all)
- * PAGES (one-pass calls of tf_paged_gqa_decode: bf16/fp16, head_dim
- * 32/64/128, group <= 16, 16-token pages, kv_heads <= 8 with
- * kv_heads * head_dim * 2 <= 1024, batch <= 2048) streams the batch's pages
- * in equal contiguous ranges, one workgroup (a wavefront per kv head) per
- * range: bits 8-15 give workgroups per compute unit (default 1), bits 16-19
- * pages in flight per workgroup (2..4, default 3).  It needs split_counters
- * and partial buffers of at least 2 x workgroups x query_heads rows: rows
- * split over several ranges are merged in the same launch.
  * VALU (the MFMA grid kernel's calls, head_dim 64, no RoPE) computes the
  * score and P.V products on the VALU -- packed two-element dot products
  * (v_dot2_f32_bf16 / _f16) and fp32 FMAs -- with the same grid, loads and
  * LDS staging: the comparison form for the MFMA products. */
 #define TF_ATTENTION_FLAG_FORCE_GENERIC 1
 #define TF_ATTENTION_FLAG_STREAM 4
-#define TF_ATTENTION_FLAG_PAGES 8
 #define TF_ATTENTION_FLAG_VALU 16
 #define TF_ATTENTION_WAVES_PER_CU_SHIFT 8
 #define TF_ATTENTION_DEPTH_SHIFT 16

@@ -24,7 +24,6 @@ TF_ATTENTION_GENERIC = 0
 TF_ATTENTION_MFMA = 1
 TF_ATTENTION_FLAG_FORCE_GENERIC = 1
 TF_ATTENTION_FLAG_STREAM = 4
-TF_ATTENTION_FLAG_PAGES = 8
 TF_ATTENTION_FLAG_VALU = 16
 TF_ATTENTION_WAVES_PER_CU_SHIFT = 8
 TF_ATTENTION_DEPTH_SHIFT = 16

@@ -49,7 +49,6 @@
 //   split kernel      triton_attention.py:173-266 (partials :260-266)
 //   reduce kernel     triton_attention.py:268-316 (LSE merge :288-316)
 //   oracle            kernels/reference.py:46-93
-#include <atomic>
 #include <mutex>
 
 #include "tf_common.hpp"
@@ -1848,559 +1847,6 @@ void mfma_geometry(AttnParams &p, int32_t flags) {
   p.tokens_per_wave = ((flags >> TF_ATTENTION_TOKENS_PER_WAVE_SHIFT) & 0x7f) * 64;
 }
 
-// ===========================================================================
-// Page-stream kernel (TF_ATTENTION_FLAG_PAGES): equal page ranges per workgroup
-// ===========================================================================
-// The batch's 16-token pages are listed in row order (row b owns
-// ceil(ctx_b / 16) of them, the exclusive prefix of those counts giving each
-// row's first page) and workgroup k of N streams the contiguous range
-// [floor(k P / N), floor((k + 1) P / N)) of the P pages, so every workgroup
-// reads the same bytes whatever the row lengths -- ragged rows cannot leave
-// compute units idle.  The workgroup has one wavefront per kv head.  All its
-// threads load each page whole: the 16 token rows of K and of V with every kv
-// head (contiguous 16-byte nontemporal loads, a whole cache line per four
-// lanes), plus the query rows of the page's row (L2 hits after the first
-// page of a row), DEPTH pages ahead into registers.  The page is then staged
-// in LDS (two buffers, one barrier per page) and each wavefront computes its
-// kv head's query group from it: scores with v_mfma_f32_16x16x32 (K rows as
-// the A operand, the query group padded to 16 columns as B), the online
-// softmax on the accumulator layout (a lane owns one query head), and P.V
-// with v_mfma_f32_16x16x16 (V^T read transposed from LDS with
-// ds_read_b64_tr_b16, P already in the B layout).
-//
-// A row wholly inside one range is finished there.  A row split over
-// several ranges leaves one partial (max, sum, unnormalised accumulator) per
-// piece in workspace slot 2 k + side of its range k -- side 0 for the row a
-// range starts in, 1 for the row it ends in -- stored with agent-scope
-// atomic stores after the range's pages are done; the piece then counts
-// itself in at split_counters[row * kv_heads + kv head] and the last of the
-// row's pieces merges them by log-sum-exp and resets the counter.
-constexpr int kPageTokens = 16;
-constexpr int kPageRowPad = 32;       // LDS token-row padding (bank spread)
-constexpr int kPageMaxRowBytes = 1024;  // kv_heads * head_dim * 2 the kernel stages
-constexpr int kPageMaxRows = 2048;    // rows whose page prefix fits LDS
-constexpr int kPageMaxWaves = 8;
-
-// LDS layout of the page-stream kernel for `threads` threads.
-struct PageLds {
-  int32_t prefix;    // (batch + 1) ints: first page of each row, then P
-  int32_t list;      // 3 x threads ints: physical page, row, tokens of a segment's pages
-  int32_t stage;     // 2 buffers x (K rows, V rows, query rows)
-  int32_t stage_bytes;
-  int32_t kv_bytes;  // one tensor's rows in a buffer
-  int32_t pitch;     // bytes per staged token row
-  int32_t q_pitch;   // bytes per staged query row
-  int32_t total;
-};
-
-__host__ __device__ inline PageLds page_lds(int32_t batch, int32_t threads, int32_t query_heads,
-                                            int32_t kv_heads, int32_t head_dim) {
-  PageLds l;
-  l.prefix = 0;
-  l.list = ((batch + 1) * 4 + 15) / 16 * 16;
-  l.stage = l.list + 3 * threads * 4;
-  l.pitch = kv_heads * head_dim * 2 + kPageRowPad;
-  l.q_pitch = head_dim * 2 + 16;
-  l.kv_bytes = kPageTokens * l.pitch;
-  l.stage_bytes = 2 * l.kv_bytes + (query_heads + 1) * l.q_pitch;  // + a spare query slot
-  l.total = l.stage + 2 * l.stage_bytes;
-  return l;
-}
-
-// Range holding global page g of P pages split over N <= P ranges.
-__device__ __forceinline__ int32_t page_range_of(int64_t g, int64_t P, int64_t N) {
-  return static_cast<int32_t>(((g + 1) * N - 1) / P);
-}
-
-// LDS-only barrier: the workgroup's LDS writes are done and visible; global
-// loads in flight are not waited for (a __syncthreads would drain them).
-__device__ __forceinline__ void lds_barrier() {
-  __asm__ volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0) only
-  __builtin_amdgcn_s_barrier();
-  __asm__ volatile("" ::: "memory");
-}
-
-// Merge of the pieces [f, l] of row b for kv head kvh by one wavefront:
-// log-sum-exp over the pieces' (max, sum, accumulator) partials, written as
-// the output rows of the head's G query heads.  Maxima and sums of every
-// (head, piece) are loaded at once (one per lane), the first batch of
-// accumulator loads right behind them; the normalised weights pass through
-// the wavefront's LDS scratch (`capacity` floats).
-template <typename T, int D>
-__device__ void merge_page_pieces(const AttnParams &p, int32_t b, int32_t kvh, int32_t f,
-                                  int32_t l, bool first_at_side1, float *scratch,
-                                  int32_t capacity) {
-  const int lane = threadIdx.x & 63;
-  const int32_t G = p.group;
-  const int32_t pieces = l - f + 1;
-  const int32_t pairs = G * pieces;
-  const int items = G * D;
-  // Partial row of (piece j, head g).
-  auto row_of = [&](int32_t j, int32_t g) -> int64_t {
-    const int32_t slot = 2 * (f + j) + ((j == 0 && first_at_side1) ? 1 : 0);
-    return static_cast<int64_t>(slot) * p.query_heads + static_cast<int64_t>(kvh) * G + g;
-  };
-  if (2 * pairs > capacity) {
-    // Scratch too small (very many pieces): one item at a time.
-    for (int idx = lane; idx < items; idx += 64) {
-      const int g = idx / D;
-      const int d = idx - g * D;
-      float gmax = kNegInf, num = 0.f, den = 0.f;
-      for (int32_t j = 0; j < pieces; ++j) {
-        const int64_t r = row_of(j, g);
-        const float m = __hip_atomic_load(p.partial_max + r, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-        const float s = __hip_atomic_load(p.partial_sum + r, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-        const float a = __hip_atomic_load(p.partial_acc + r * p.partial_stride + d,
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (m == kNegInf) continue;
-        if (m > gmax) {
-          const float c = fast_exp2(gmax - m);
-          num *= c;
-          den *= c;
-          gmax = m;
-        }
-        const float e = fast_exp2(m - gmax);
-        den += e * s;
-        num += e * a;
-      }
-      output_row<T>(p, b, kvh * G + g)[d] = from_float<T>(den > 0.f ? num / den : 0.f);
-    }
-    return;
-  }
-  float *wm = scratch;          // [G][pieces] maxima, then weights
-  float *wl = scratch + pairs;  // [G][pieces] sums
-  constexpr int kItems = 8, kBatch = 8;
-  float v[kItems][kBatch];
-  auto load_acc = [&](int k0, int32_t j0) {
-#pragma unroll
-    for (int i = 0; i < kItems; ++i) {
-      const int idx = min(lane + 64 * (k0 + i), items - 1);
-      const int g = idx / D;
-      const int d = idx - g * D;
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j)
-        v[i][j] = __hip_atomic_load(
-            p.partial_acc + row_of(min(j0 + j, pieces - 1), g) * p.partial_stride + d,
-            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  };
-  for (int32_t q0 = 0; q0 < pairs; q0 += 4 * 64) {
-    float mv[4], lv[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int32_t q = min(q0 + t * 64 + lane, pairs - 1);
-      const int32_t g = q / pieces;
-      const int64_t r = row_of(q - g * pieces, g);
-      mv[t] = __hip_atomic_load(p.partial_max + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      lv[t] = __hip_atomic_load(p.partial_sum + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (q0 == 0) load_acc(0, 0);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int32_t q = q0 + t * 64 + lane;
-      if (q < pairs) {
-        wm[q] = mv[t];
-        wl[q] = lv[t];
-      }
-    }
-  }
-  __asm__ volatile("" ::: "memory");
-  if (lane < G) {
-    float mmax = kNegInf;
-    for (int32_t j = 0; j < pieces; ++j) mmax = fmaxf(mmax, wm[lane * pieces + j]);
-    float den = 0.f;
-    if (mmax != kNegInf)
-      for (int32_t j = 0; j < pieces; ++j)
-        den += wl[lane * pieces + j] * fast_exp2(wm[lane * pieces + j] - mmax);
-    const float inv = den > 0.f ? 1.f / den : 0.f;
-    for (int32_t j = 0; j < pieces; ++j) {
-      const float m = wm[lane * pieces + j];
-      wm[lane * pieces + j] = m == kNegInf ? 0.f : fast_exp2(m - mmax) * inv;
-    }
-  }
-  __asm__ volatile("" ::: "memory");
-  for (int k0 = 0; k0 * 64 < items; k0 += kItems) {
-    float num[kItems];
-#pragma unroll
-    for (int i = 0; i < kItems; ++i) num[i] = 0.f;
-    for (int32_t j0 = 0; j0 < pieces; j0 += kBatch) {
-      if (k0 > 0 || j0 > 0) load_acc(k0, j0);
-#pragma unroll
-      for (int i = 0; i < kItems; ++i) {
-        const int idx = min(lane + 64 * (k0 + i), items - 1);
-        const int g = idx / D;
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j)
-          if (j0 + j < pieces) num[i] += wm[g * pieces + j0 + j] * v[i][j];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kItems; ++i) {
-      const int idx = lane + 64 * (k0 + i);
-      if (idx < items) {
-        const int g = idx / D;
-        output_row<T>(p, b, kvh * G + g)[idx - g * D] = from_float<T>(num[i]);
-      }
-    }
-  }
-}
-
-template <typename T, int D, int DEPTH, int QP>
-__global__ void __launch_bounds__(64 * kPageMaxWaves)
-paged_decode_pages_kernel(AttnParams p) {
-  using M = Mfma<T>;
-  using vec8 = typename M::vec8;
-  constexpr int KS = D / 32;   // k-steps of the score product
-  constexpr int NB = D / 16;   // 16-dim blocks of the output
-  constexpr int KV = D / 32;   // 16-byte pieces of K (and of V) per thread per page
-  // QP = ceil(group * D / 512): 16-byte query pieces per thread per page.
-  extern __shared__ __attribute__((aligned(16))) unsigned char page_smem[];
-  const int32_t threads = blockDim.x;
-  const int32_t tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int32_t kvh = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l16 = lane & 15;
-  const int q4 = lane >> 4;
-  const int32_t B = p.batch;
-  const int32_t G = p.group;
-  const int64_t N = gridDim.x;
-  const int32_t k = blockIdx.x;
-  const PageLds layout = page_lds(B, threads, p.query_heads, p.kv_heads, D);
-  int32_t *prefix = reinterpret_cast<int32_t *>(page_smem + layout.prefix);
-  int32_t *lst_phys = reinterpret_cast<int32_t *>(page_smem + layout.list);
-  int32_t *lst_row = lst_phys + threads;
-  int32_t *lst_ntok = lst_row + threads;
-  unsigned char *stage = page_smem + layout.stage;
-  const int32_t row_bytes = p.kv_heads * D * static_cast<int32_t>(sizeof(T));
-  const int32_t pieces_per_row = row_bytes / 16;
-  const int64_t page_bytes = static_cast<int64_t>(kPageTokens) * row_bytes;
-  const int32_t q_pieces = p.query_heads * D / 8;
-  const int32_t q_row_pieces = D / 8;
-
-  // ---- 1. Each row's first page: exclusive prefix of ceil(ctx / 16) -------
-  const int32_t per_thread = (B + threads - 1) / threads;
-  int32_t local = 0;
-  for (int32_t r = tid * per_thread; r < min(B, (tid + 1) * per_thread); ++r)
-    local += (clamp_context(p, r) + kPageTokens - 1) / kPageTokens;
-  int32_t incl = local;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int32_t v = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += v;
-  }
-  if (lane == 63) lst_row[kvh] = incl;  // wavefront totals (list area, reused below)
-  lds_barrier();
-  int32_t base = 0, total = 0;
-  for (int32_t w = 0; w < threads / 64; ++w) {
-    const int32_t t = lst_row[w];
-    base += w < kvh ? t : 0;
-    total += t;
-  }
-  int32_t run = base + incl - local;
-  for (int32_t r = tid * per_thread; r < min(B, (tid + 1) * per_thread); ++r) {
-    prefix[r] = run;
-    run += (clamp_context(p, r) + kPageTokens - 1) / kPageTokens;
-  }
-  if (tid == 0) prefix[B] = total;
-  lds_barrier();
-
-  // Rows of length zero: zeros, written by workgroup (row mod grid).
-  for (int32_t r = k; r < B; r += static_cast<int32_t>(N)) {
-    if (prefix[r + 1] != prefix[r]) continue;
-    T *out = output_row<T>(p, r, 0);
-    for (int32_t i = tid; i < p.query_heads * D; i += threads) out[i] = from_float<T>(0.f);
-  }
-  // The pages are split over min(grid, P) ranges, so no range is empty and
-  // the ranges of a row's pieces are consecutive; surplus workgroups idle.
-  const int64_t P = total;
-  if (k >= P) return;
-  const int64_t RN = N < P ? N : P;
-  const int64_t lo = static_cast<int64_t>(k) * P / RN;
-  const int64_t hi = static_cast<int64_t>(k + 1) * P / RN;
-
-  // ---- 2. Stream the range ------------------------------------------------
-  const unsigned char *kbytes = static_cast<const unsigned char *>(p.key_cache);
-  const unsigned char *vbytes = static_cast<const unsigned char *>(p.value_cache);
-  const unsigned char *qbytes = static_cast<const unsigned char *>(p.query);
-  int32_t cur = -1;  // row of the wavefront's running state
-  float m_run = kNegInf, l_run = 0.f;
-  f32x4 acc[NB];
-#pragma unroll
-  for (int n = 0; n < NB; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // The piece of a split row the range starts in (side 0), kept in registers
-  // until the range is done: a store now would be counted with the page
-  // loads behind it and hold up their waits.
-  int32_t saved_row = -1;
-  float saved_m = kNegInf, saved_l = 0.f;
-  f32x4 saved_acc[NB];
-#pragma unroll
-  for (int n = 0; n < NB; ++n) saved_acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Finish `row` for this wavefront's kv head: a row wholly inside the
-  // range is written to the output; the range's first row, if split, is
-  // kept for the end.
-  auto flush = [&](int32_t row) {
-    float lt = l_run + __shfl_xor(l_run, 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
-    if (prefix[row] >= lo && prefix[row + 1] <= hi) {
-      if (l16 < G) {
-        const float inv = lt > 0.f ? 1.f / lt : 0.f;
-        T *out = output_row<T>(p, row, kvh * G + l16);
-#pragma unroll
-        for (int n = 0; n < NB; ++n) {
-          typedef T t4 __attribute__((ext_vector_type(4)));
-          const t4 v = {from_float<T>(acc[n][0] * inv), from_float<T>(acc[n][1] * inv),
-                        from_float<T>(acc[n][2] * inv), from_float<T>(acc[n][3] * inv)};
-          *reinterpret_cast<t4 *>(out + 16 * n + 4 * q4) = v;
-        }
-      }
-      return;
-    }
-    saved_row = row;
-    saved_m = m_run;
-    saved_l = lt;
-#pragma unroll
-    for (int n = 0; n < NB; ++n) saved_acc[n] = acc[n];
-  };
-
-  // The partial of a split row's piece in slot 2 k + side, after the page
-  // loop (the stage buffers are then free): the accumulator tile passes
-  // through the wavefront's LDS slice so each store instruction writes
-  // consecutive floats of a partial row.
-  auto store_partial = [&](int side, float m, float lt, const f32x4 (&a)[NB], float *tile) {
-    const int64_t prow0 = static_cast<int64_t>(2 * k + side) * p.query_heads + kvh * G;
-    if (l16 < G) {
-#pragma unroll
-      for (int n = 0; n < NB; ++n)
-        *reinterpret_cast<f32x4 *>(tile + l16 * D + 16 * n + 4 * q4) = a[n];
-      if (q4 == 0) {
-        __hip_atomic_store(p.partial_max + prow0 + l16, m, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.partial_sum + prow0 + l16, lt, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    __asm__ volatile("" ::: "memory");
-    for (int idx = lane; idx < G * D; idx += 64) {
-      const int g = idx / D;
-      __hip_atomic_store(p.partial_acc + (prow0 + g) * p.partial_stride + (idx - g * D),
-                         tile[idx], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __asm__ volatile("" ::: "memory");
-  };
-
-  for (int64_t seg0 = lo; seg0 < hi; seg0 += threads) {
-    const int32_t seg_len = static_cast<int32_t>(min(static_cast<int64_t>(threads), hi - seg0));
-    // Page list of the segment: thread t resolves page seg0 + t.
-    if (tid < seg_len) {
-      const int64_t g = seg0 + tid;
-      int32_t a = 0, z = B;  // prefix[a] <= g < prefix[z]
-      while (z - a > 1) {
-        const int32_t mid = (a + z) >> 1;
-        if (prefix[mid] <= g) a = mid;
-        else z = mid;
-      }
-      const int32_t j = static_cast<int32_t>(g - prefix[a]);
-      const int32_t ctx = clamp_context(p, a);
-      int32_t ntok = min(kPageTokens, ctx - kPageTokens * j);
-      int32_t page = p.block_tables[static_cast<int64_t>(a) * p.table_width + j];
-      if (page < 0 || page >= p.num_blocks) {
-        page = 0;
-        ntok = 0;
-      }
-      lst_phys[tid] = page;
-      lst_row[tid] = a;
-      lst_ntok[tid] = ntok;
-    }
-    lds_barrier();
-
-    u32x4 rk[DEPTH][KV], rv[DEPTH][KV], rq[DEPTH][QP];
-    // Loads of segment page i into ring slot d (pages past the segment, and
-    // pages without tokens, read one stand-in line).
-    auto issue = [&](int d, int32_t i) {
-      const bool real = i < seg_len;
-      const int32_t ntok = real ? lst_ntok[i] : 0;
-      const int32_t row = real ? lst_row[i] : 0;
-      const int64_t kv_off = ntok > 0 ? static_cast<int64_t>(lst_phys[i]) * page_bytes : 0;
-      const int64_t q_off = static_cast<int64_t>(row) * p.query_heads * D * sizeof(T);
-#pragma unroll
-      for (int j = 0; j < KV; ++j) {
-        const int64_t o = ntok > 0 ? kv_off + 16 * (tid + j * threads) : 0;
-        rk[d][j] = load_stream16<u32x4>(kbytes + o);
-        rv[d][j] = load_stream16<u32x4>(vbytes + o);
-      }
-      // Every query load is issued (surplus threads repeat piece 0), so the
-      // wait counts of the loop stay static.
-#pragma unroll
-      for (int j = 0; j < QP; ++j) {
-        const int32_t piece = tid + j * threads;
-        rq[d][j] = *reinterpret_cast<const u32x4 *>(
-            qbytes + q_off + 16 * (real && piece < q_pieces ? piece : 0));
-      }
-    };
-    // Stage ring slot d (page i) into LDS buffer `buf`; V rows of absent
-    // tokens are written as zeros so that 0 * (stand-in) cannot reach the
-    // sum.  Branch-free: threads past the query rows write a spare slot.
-    auto stage_page = [&](int d, int32_t i, int buf) {
-      unsigned char *sk = stage + buf * layout.stage_bytes;
-      unsigned char *sv = sk + layout.kv_bytes;
-      unsigned char *sq = sv + layout.kv_bytes;
-      const int32_t ntok = lst_ntok[i];
-#pragma unroll
-      for (int j = 0; j < KV; ++j) {
-        const int32_t piece = tid + j * threads;
-        const int32_t t = piece / pieces_per_row;
-        const int32_t at = t * layout.pitch + (piece - t * pieces_per_row) * 16;
-        const uint32_t keep = t < ntok ? 0xffffffffu : 0u;
-        *reinterpret_cast<u32x4 *>(sk + at) = rk[d][j];
-        *reinterpret_cast<u32x4 *>(sv + at) = rv[d][j] & keep;
-      }
-#pragma unroll
-      for (int j = 0; j < QP; ++j) {
-        const int32_t piece = tid + j * threads;
-        const int32_t h = piece / q_row_pieces;
-        const int32_t at = piece < q_pieces
-                               ? h * layout.q_pitch + (piece - h * q_row_pieces) * 16
-                               : p.query_heads * layout.q_pitch;  // spare slot
-        *reinterpret_cast<u32x4 *>(sq + at) = rq[d][j];
-      }
-    };
-    // This wavefront's kv head over staged page i.
-    auto compute = [&](int32_t i, int buf) {
-      const int32_t row = __builtin_amdgcn_readfirstlane(lst_row[i]);
-      const int32_t ntok = __builtin_amdgcn_readfirstlane(lst_ntok[i]);
-      if (row != cur) {
-        if (cur >= 0) flush(cur);
-        cur = row;
-        m_run = kNegInf;
-        l_run = 0.f;
-#pragma unroll
-        for (int n = 0; n < NB; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-      if (ntok <= 0) return;  // page outside the cache: no tokens
-      const unsigned char *sk = stage + buf * layout.stage_bytes;
-      const unsigned char *sv = sk + layout.kv_bytes;
-      const unsigned char *sq = sv + layout.kv_bytes;
-      const int32_t head_off = kvh * D * static_cast<int32_t>(sizeof(T));
-      vec8 kf[KS], qf[KS];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        kf[ks] = *reinterpret_cast<const vec8 *>(sk + l16 * layout.pitch + head_off +
-                                                 (32 * ks + 8 * q4) * 2);
-        qf[ks] = l16 < G ? *reinterpret_cast<const vec8 *>(sq + (kvh * G + l16) * layout.q_pitch +
-                                                          (32 * ks + 8 * q4) * 2)
-                         : vec8{};
-      }
-      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) s = M::mma(kf[ks], qf[ks], s);
-      // The MFMA result is read only after 16 wait states.  The compiler's
-      // own hazard padding was found missing on a branch taken right after
-      // the MFMA (the scores then read stale registers), so the padding is
-      // explicit here, on the result's registers, and the masking below is
-      // branch-free.
-      __asm__ volatile("s_nop 7\n\ts_nop 7" : "+v"(s));
-      // Lane (l16, q4) holds S[token 4 q4 + r][query head l16].
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s[r] = 4 * q4 + r < ntok ? s[r] : kNegInf;
-      float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])) * p.scale_log2;
-      if (__ballot(mx > m_run + kRescaleThreshold) != 0) {
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = m_run == kNegInf ? 0.f : fast_exp2(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int n = 0; n < NB; ++n) acc[n] *= alpha;
-      }
-      i16x4 pf;
-      float psum = 0.f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pr = fast_exp2(__builtin_fmaf(s[r], p.scale_log2, -m_run));
-        psum += pr;
-        pf[r] = __builtin_bit_cast(short, from_float<T>(pr));
-      }
-      l_run += psum;
-      const unsigned char *rd = sv + (4 * q4 + (l16 >> 2)) * layout.pitch + head_off + (l16 & 3) * 8;
-#pragma unroll
-      for (int n = 0; n < NB; ++n) {
-        const i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(rd + 32 * n));
-        acc[n] = Mfma16<T>::mma(a, pf, acc[n]);
-      }
-    };
-
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) issue(d, d);
-    // Every stage of the unrolled body runs (past the segment it stages and
-    // computes nothing), so the body's wait counts are the same each trip.
-    for (int32_t i0 = 0; i0 < seg_len; i0 += DEPTH) {
-#pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
-        const int32_t i = i0 + d;
-        const bool real = i < seg_len;
-        if (real) stage_page(d, i, i & 1);
-        issue(d, i + DEPTH);
-        lds_barrier();
-        if (real) compute(i, i & 1);
-      }
-    }
-    lds_barrier();  // the list and stage buffers may be rewritten
-  }
-  // ---- 3. Split rows: store the pieces, count in; the last piece merges ----
-  // Stage buffers are free once every wavefront is past its last page; each
-  // wavefront takes a private slice of them as store and merge scratch.
-  const int32_t capacity = 2 * layout.stage_bytes / 4 / (threads / 64);
-  float *scratch = reinterpret_cast<float *>(stage) + kvh * capacity;
-  int32_t pending[2] = {-1, -1};  // split rows of the pieces this wavefront stored, by side
-  if (saved_row >= 0) {
-    store_partial(0, saved_m, saved_l, saved_acc, scratch);
-    pending[0] = saved_row;
-  }
-  if (cur >= 0) {
-    if (prefix[cur] >= lo && prefix[cur + 1] <= hi) {
-      flush(cur);
-    } else {
-      float lt = l_run + __shfl_xor(l_run, 16, 64);
-      lt += __shfl_xor(lt, 32, 64);
-      const int side = prefix[cur] <= lo ? 0 : 1;
-      store_partial(side, m_run, lt, acc, scratch);
-      pending[side] = cur;
-    }
-  }
-  if (pending[0] < 0 && pending[1] < 0) return;
-  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's partial stores have completed
-  int32_t last[2] = {0, 0};
-  if (lane == 0) {
-#pragma unroll
-    for (int side = 0; side < 2; ++side) {
-      const int32_t row = pending[side];
-      if (row < 0) continue;
-      const int32_t f = page_range_of(prefix[row], P, RN);
-      const int32_t l = page_range_of(prefix[row + 1] - 1, P, RN);
-      int32_t *slot = p.split_counters + static_cast<int64_t>(row) * p.kv_heads + kvh;
-      const int32_t prev = __hip_atomic_fetch_add(slot, 1, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-      last[side] = prev == l - f;
-      if (last[side]) __hip_atomic_store(slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-#pragma unroll
-  for (int side = 0; side < 2; ++side) {
-    const int32_t row = pending[side];
-    if (row < 0 || __builtin_amdgcn_readfirstlane(last[side]) == 0) continue;
-    const int64_t first = prefix[row];
-    const int32_t f = page_range_of(first, P, RN);
-    const int32_t l = page_range_of(prefix[row + 1] - 1, P, RN);
-    const bool first_at_side1 = first != static_cast<int64_t>(f) * P / RN;
-    merge_page_pieces<T, D>(p, row, kvh, f, l, first_at_side1, scratch, capacity);
-  }
-}
-
 // Whole-row loads (LINES) when several wavefronts stream one kv head: there
 // a compute unit's load issue rate bounds the longest rows.  One wavefront
 // per (row, kv head, split) is latency-bound and keeps the operand-layout
@@ -2664,93 +2110,6 @@ int32_t launch_split_stage(const AttnParams &p, int32_t dtype, int32_t flags, hi
 }
 
 
-// ---- page-stream launch ----------------------------------------------------
-template <typename T, int D, int DEPTH, int QP>
-void launch_pages(const AttnParams &p, int32_t nwg, hipStream_t stream) {
-  const int32_t threads = 64 * p.kv_heads;
-  const size_t lds = static_cast<size_t>(page_lds(p.batch, threads, p.query_heads, p.kv_heads, D).total);
-  if (lds > 64 * 1024) {
-    // Raise the kernel's dynamic LDS limit once per device.
-    constexpr int kMaxDevices = 64;
-    static std::atomic<bool> raised[kMaxDevices];
-    int device = 0;
-    if (hipGetDevice(&device) == hipSuccess && device >= 0 && device < kMaxDevices &&
-        !raised[device].load(std::memory_order_acquire)) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void *>(&paged_decode_pages_kernel<T, D, DEPTH, QP>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              static_cast<int>(lds)) == hipSuccess)
-        raised[device].store(true, std::memory_order_release);
-    }
-  }
-  hipLaunchKernelGGL((paged_decode_pages_kernel<T, D, DEPTH, QP>), dim3(nwg), dim3(threads), lds,
-                     stream, p);
-}
-
-template <typename T, int D, int QP>
-void launch_pages_qp(const AttnParams &p, int32_t nwg, int32_t depth, hipStream_t stream) {
-  if (depth == 2)
-    launch_pages<T, D, 2, QP>(p, nwg, stream);
-  else if (depth == 4)
-    launch_pages<T, D, 4, QP>(p, nwg, stream);
-  else
-    launch_pages<T, D, 3, QP>(p, nwg, stream);
-}
-
-// Query pieces per thread: ceil(group * D / 512) (the workgroup's threads
-// are 64 x kv_heads, the query rows group * kv_heads * D / 8 pieces).
-template <typename T, int D>
-void launch_pages_depth(const AttnParams &p, int32_t nwg, int32_t depth, hipStream_t stream) {
-  const int32_t qp = (p.group * D + 511) / 512;
-  if (qp <= 1)
-    launch_pages_qp<T, D, 1>(p, nwg, depth, stream);
-  else if (qp == 2)
-    launch_pages_qp<T, D, 2>(p, nwg, depth, stream);
-  else
-    launch_pages_qp<T, D, 4>(p, nwg, depth, stream);
-}
-
-// The page-stream form of a one-pass call: p from make_params, the caller's
-// partial buffers and counters.  Workgroups: flag bits 8-15 per compute unit
-// (default 1); pages in flight per workgroup: bits 16-19 (2..4, default 3).
-int32_t launch_pages_call(AttnParams p, int32_t *split_counters, int64_t partial_capacity,
-                          int32_t dtype, int32_t flags, hipStream_t stream) {
-  const int32_t D = p.head_dim;
-  if (choose_variant(dtype, D, p.group, p.block_size, 0) != TF_ATTENTION_MFMA ||
-      p.block_size != kPageTokens || p.kv_heads > kPageMaxWaves ||
-      p.kv_heads * D * 2 > kPageMaxRowBytes || p.batch > kPageMaxRows)
-    return fail(TF_ERROR_UNSUPPORTED,
-                "page-stream attention needs bf16/fp16, head_dim 32/64/128, group <= 16, "
-                "16-token pages, kv_heads <= 8 with kv_heads * head_dim * 2 <= 1024 bytes, "
-                "and batch <= 2048");
-  int32_t per_cu = (flags >> TF_ATTENTION_WAVES_PER_CU_SHIFT) & 0xff;
-  if (per_cu == 0) per_cu = 1;
-  const int32_t nwg = device_compute_units() * per_cu;
-  if (!split_counters || !p.partial_max || !p.partial_sum || !p.partial_acc ||
-      p.partial_stride < D ||
-      partial_capacity < 2 * static_cast<int64_t>(nwg) * p.query_heads)
-    return fail(TF_ERROR_INVALID_ARGUMENT,
-                "page-stream attention needs split counters and partial buffers of at least "
-                "2 x workgroups x query_heads rows");
-  if (p.batch == 0) return TF_SUCCESS;
-  p.split_counters = split_counters;
-  const int32_t depth = (flags >> TF_ATTENTION_DEPTH_SHIFT) & 0xf;
-  switch (D) {
-    case 32:
-      if (dtype == TF_DTYPE_BFLOAT16) launch_pages_depth<__bf16, 32>(p, nwg, depth, stream);
-      else launch_pages_depth<_Float16, 32>(p, nwg, depth, stream);
-      break;
-    case 64:
-      if (dtype == TF_DTYPE_BFLOAT16) launch_pages_depth<__bf16, 64>(p, nwg, depth, stream);
-      else launch_pages_depth<_Float16, 64>(p, nwg, depth, stream);
-      break;
-    default:
-      if (dtype == TF_DTYPE_BFLOAT16) launch_pages_depth<__bf16, 128>(p, nwg, depth, stream);
-      else launch_pages_depth<_Float16, 128>(p, nwg, depth, stream);
-      break;
-  }
-  return check_launch("paged_gqa_decode (pages)");
-}
-
 int32_t launch_merge(const float *partial_max, const float *partial_sum, const float *partial_acc,
                      const int32_t *context_lengths, void *output, int32_t batch,
                      int32_t query_heads, int32_t head_dim, int32_t split_size, int32_t num_splits,
@@ -2806,11 +2165,6 @@ extern "C" int32_t tf_paged_gqa_decode(
                               num_splits, scale, dtype))
     return s;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (flags & TF_ATTENTION_FLAG_PAGES) {
-    if (num_splits != 1)
-      return fail(TF_ERROR_INVALID_ARGUMENT, "page-stream attention is a one-pass call");
-    return launch_pages_call(p, split_counters, partial_capacity, dtype, flags, s);
-  }
   if (int32_t st = launch_split_stage(p, dtype, flags, s)) return st;
   if (num_splits == 1 || split_counters != nullptr) return TF_SUCCESS;
   return launch_merge(partial_max, partial_sum, partial_accumulator, context_lengths, output,

@@ -75,7 +75,7 @@ def test_library_exports_every_declared_symbol(lib) -> None:
 def test_header_constants_match_the_python_binding() -> None:
     text = HEADER.read_text()
     for name in ("TF_ATTENTION_FLAG_FORCE_GENERIC", "TF_ATTENTION_FLAG_STREAM",
-                 "TF_ATTENTION_FLAG_PAGES", "TF_ATTENTION_FLAG_VALU",
+                 "TF_ATTENTION_FLAG_VALU",
                  "TF_ATTENTION_WAVES_PER_CU_SHIFT", "TF_ATTENTION_DEPTH_SHIFT",
                  "TF_ATTENTION_HEADS_PER_WG_SHIFT", "TF_ATTENTION_TOKENS_PER_WAVE_SHIFT"):
         match = re.search(rf"#define {name} (\d+)", text)
@@ -87,7 +87,7 @@ def test_header_constants_match_the_python_binding() -> None:
 
 
 def test_abi_version_and_variant_selection(lib) -> None:
-    assert lib.tf_abi_version() == 11
+    assert lib.tf_abi_version() == 12
     variant = lib.tf_paged_gqa_decode_variant
     bf16, f16, f32 = (_native.TF_DTYPE_BFLOAT16, _native.TF_DTYPE_FLOAT16,
                       _native.TF_DTYPE_FLOAT32)
