@@ -97,10 +97,22 @@ enum tf_attention_variant {
  * VALU (the MFMA grid kernel's calls, head_dim 64, no RoPE) computes the
  * score and P.V products on the VALU -- packed two-element dot products
  * (v_dot2_f32_bf16 / _f16) and fp32 FMAs -- with the same grid, loads and
- * LDS staging: the comparison form for the MFMA products. */
+ * LDS staging: the comparison form for the MFMA products.
+ * BALANCED (MFMA grid kernel, split-KV with the merge launch: num_splits >
+ * batch, batch <= 64, split_counters null) sizes the partitions from the
+ * rows' lengths on the device instead of using split_size for every row:
+ * with total = the sum of the (clamped) lengths, every row is cut into
+ * partitions of max(split_size, ceil32(ceil(total / (num_splits - batch))))
+ * tokens, at most num_splits per kv head over all rows together, and the
+ * launch is one compact grid of (kv_heads / heads per workgroup) x
+ * num_splits workgroups that take those partitions in row order.  Ragged
+ * long rows then spread over the grid evenly where fixed partitions leave
+ * most of it without work.  Partials land in slot j < ceil(len / partition)
+ * of their row, as with fixed partitions; the merge recomputes the size. */
 #define TF_ATTENTION_FLAG_FORCE_GENERIC 1
 #define TF_ATTENTION_FLAG_STREAM 4
 #define TF_ATTENTION_FLAG_VALU 16
+#define TF_ATTENTION_FLAG_BALANCED 32
 #define TF_ATTENTION_WAVES_PER_CU_SHIFT 8
 #define TF_ATTENTION_DEPTH_SHIFT 16
 #define TF_ATTENTION_HEADS_PER_WG_SHIFT 20

@@ -25,6 +25,7 @@ TF_ATTENTION_MFMA = 1
 TF_ATTENTION_FLAG_FORCE_GENERIC = 1
 TF_ATTENTION_FLAG_STREAM = 4
 TF_ATTENTION_FLAG_VALU = 16
+TF_ATTENTION_FLAG_BALANCED = 32
 TF_ATTENTION_WAVES_PER_CU_SHIFT = 8
 TF_ATTENTION_DEPTH_SHIFT = 16
 TF_ATTENTION_HEADS_PER_WG_SHIFT = 20

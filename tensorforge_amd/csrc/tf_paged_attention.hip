@@ -91,6 +91,7 @@ struct AttnParams {
   int32_t heads_per_wg;    // MFMA grid kernel: kv heads served by one workgroup
   int32_t waves_per_head;  // MFMA grid kernel: wavefronts sharing one kv head
   int32_t tokens_per_wave; // MFMA grid kernel: > 0 uses ceil(tokens / this) of them per row
+  int32_t balanced;        // MFMA grid kernel: partition size from the lengths (FLAG_BALANCED)
   float scale_log2;
   // Fused RoPE + append (MFMA grid kernel, tf_paged_gqa_decode_rope_append):
   // the query group is rotated from row b of `rope_qkv` ([q heads | k heads
@@ -113,6 +114,62 @@ __device__ __forceinline__ int32_t clamp_context(const AttnParams &p, int32_t b)
   if (ctx < 0) ctx = 0;
   if (ctx > p.max_tokens) ctx = p.max_tokens;
   return ctx;
+}
+
+// Partition size of a balanced split-KV call (TF_ATTENTION_FLAG_BALANCED),
+// the same in every workgroup and in the merge: with total = the sum of the
+// batch's clamped lengths, max(split_size, ceil32(ceil(total / (num_splits
+// - batch)))), capped at the largest length a row can have.  A nonempty
+// row of length L then needs ceil(L / size) <= L / size + 1 partitions, so
+// the rows together need at most total / size + batch <= num_splits.
+// Called by a whole wavefront (batch <= 64, num_splits > batch); lane b <
+// batch returns row b's clamped length in `len` (0 on the other lanes).
+__device__ __forceinline__ int32_t balanced_partition(const int32_t *lengths, int32_t batch,
+                                                      int32_t max_tokens, int32_t split_size,
+                                                      int32_t num_splits, int32_t &len) {
+  const int lane = threadIdx.x & 63;
+  int32_t v = lane < batch ? lengths[lane] : 0;
+  v = v < 0 ? 0 : (v > max_tokens ? max_tokens : v);
+  len = v;
+  int64_t total = v;
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) total += __shfl_xor(total, offset, 64);
+  const int64_t spare = num_splits - batch;
+  int64_t size = ((total + spare - 1) / spare + 31) / 32 * 32;
+  const int64_t longest = (static_cast<int64_t>(max_tokens) + 31) / 32 * 32;
+  if (size > longest) size = longest;
+  if (size < split_size) size = split_size;
+  return __builtin_amdgcn_readfirstlane(static_cast<int32_t>(size));
+}
+
+// Row and partition of slot `slot` of a balanced call: the rows'
+// partitions, ceil(length / size) each, are numbered in row order, and
+// slots past the last one have none (row -1).  Whole-wavefront call; the
+// results are wavefront-uniform.
+__device__ __forceinline__ void balanced_slot(const AttnParams &p, int32_t slot, int32_t &size,
+                                              int32_t &row, int32_t &part) {
+  const int lane = threadIdx.x & 63;
+  int32_t len;
+  size = balanced_partition(p.context_lengths, p.batch, p.max_tokens, p.split_size,
+                            p.num_splits, len);
+  const int32_t n = (len + size - 1) / size;
+  int32_t incl = n;  // inclusive prefix sum of the partition counts over rows (lanes)
+#pragma unroll
+  for (int offset = 1; offset < 64; offset <<= 1) {
+    const int32_t below = __shfl_up(incl, offset, 64);
+    if (lane >= offset) incl += below;
+  }
+  const int32_t excl = incl - n;
+  const unsigned long long hit = __ballot(slot >= excl && slot < incl);
+  row = -1;
+  part = 0;
+  if (hit != 0) {
+    const int r = __builtin_ctzll(hit);
+    row = r;
+    part = slot - __shfl(excl, r, 64);
+  }
+  row = __builtin_amdgcn_readfirstlane(row);
+  part = __builtin_amdgcn_readfirstlane(part);
 }
 
 // Element offset of token `t` of sequence row `table` for kv head 0, or -1
@@ -521,12 +578,24 @@ paged_decode_mfma_kernel(AttnParams p) {
   // one sub-index read the slices of the same token rows at the same time:
   // the cache row [token, kv head, head_dim] is fetched as a whole, not one
   // head slice at a time from different workgroups.
+  //
+  // Balanced calls launch one compact grid instead: blockIdx.x = slot * NG +
+  // group, the slot naming a (row, partition) by balanced_slot, and slots
+  // without a partition exit at once.
   const int32_t HPW = p.heads_per_wg;
   const int32_t WPH = p.waves_per_head;
   const int32_t NG = p.kv_heads / HPW;
-  const int32_t b = blockIdx.x / NG;
-  const int32_t grp = blockIdx.x - b * NG;
-  const int32_t split = blockIdx.y;
+  int32_t b, grp, split, split_size;
+  if (p.balanced) {
+    grp = blockIdx.x % NG;
+    balanced_slot(p, blockIdx.x / NG, split_size, b, split);
+    if (b < 0) return;  // the same on every wavefront of the workgroup
+  } else {
+    b = blockIdx.x / NG;
+    grp = blockIdx.x - b * NG;
+    split = blockIdx.y;
+    split_size = p.split_size;
+  }
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int32_t hl = wave % HPW;   // head within the group
@@ -534,7 +603,7 @@ paged_decode_mfma_kernel(AttnParams p) {
   const int32_t kvh = grp * HPW + hl;
   const int l16 = lane & 15;
   const int q4 = lane >> 4;
-  const int32_t s0 = split * p.split_size;
+  const int32_t s0 = split * split_size;
   const int32_t *table = p.block_tables + static_cast<int64_t>(b) * p.table_width;
 
   // Page ids of up to 64 tiles starting at `first` (lane i: tile first + i).
@@ -635,7 +704,7 @@ paged_decode_mfma_kernel(AttnParams p) {
     }
     __builtin_amdgcn_s_waitcnt(0);
   }
-  const int32_t s1 = min(s0 + p.split_size, ctx);
+  const int32_t s1 = min(s0 + split_size, ctx);
   // Wavefronts of the head that take chunks of this row: all WPH, or with a
   // token budget per wavefront only as many as the row's length needs (the
   // rest stay idle), so short rows do not load the memory system with
@@ -920,7 +989,7 @@ paged_decode_mfma_kernel(AttnParams p) {
   // ---- per-wavefront epilogue for kv head kvh ----------------------------
   // Lane (l16, q4) owns head l16 (if < G), dims 16n + 4q4 + r.
   const int32_t G = p.group;
-  const int32_t nvalid = (ctx + p.split_size - 1) / p.split_size;
+  const int32_t nvalid = (ctx + split_size - 1) / split_size;
   const bool counters = p.num_splits > 1 && p.split_counters != nullptr;
   const bool direct = p.num_splits == 1 || (counters && nvalid == 1);
   const bool head_ok = l16 < G;
@@ -1737,7 +1806,8 @@ merge_partials_kernel(const float *__restrict__ partial_max, const float *__rest
                       const float *__restrict__ partial_acc,
                       const int32_t *__restrict__ context_lengths, T *__restrict__ output,
                       int32_t query_heads, int32_t head_dim, int32_t split_size,
-                      int32_t num_splits, int32_t partial_stride, int32_t max_tokens) {
+                      int32_t num_splits, int32_t partial_stride, int32_t max_tokens,
+                      int32_t balanced) {
   // One wavefront per (row, query head).  Lane s holds the max and sum of
   // split s (64 splits per pass); lanes over head_dim accumulate the
   // weighted rows, kBatch splits of loads in flight.  The first batch is
@@ -1770,6 +1840,11 @@ merge_partials_kernel(const float *__restrict__ partial_max, const float *__rest
   load_batch(0);
   int32_t ctx = context_lengths[b];
   ctx = ctx < 0 ? 0 : (ctx > max_tokens ? max_tokens : ctx);
+  if (balanced) {
+    int32_t unused;
+    split_size = balanced_partition(context_lengths, static_cast<int32_t>(gridDim.y), max_tokens,
+                                    split_size, num_splits, unused);
+  }
   const int32_t nvalid = (ctx + split_size - 1) / split_size;
   // Max and sum over the valid splits (lanes beyond 64 splits in later passes).
   float gmax = kNegInf;
@@ -1965,6 +2040,7 @@ int32_t make_params(AttnParams &p, const void *query, const void *key_cache,
   p.heads_per_wg = 1;
   p.waves_per_head = 1;
   p.tokens_per_wave = 0;
+  p.balanced = 0;
   p.scale_log2 = scale * kLog2e;
   p.rope_qkv = nullptr;
   p.rope_row_stride = 0;
@@ -2045,6 +2121,15 @@ constexpr int64_t kStreamMinWaves = 64;
 
 int32_t launch_split_stage(const AttnParams &p, int32_t dtype, int32_t flags, hipStream_t stream) {
   if (p.batch == 0) return TF_SUCCESS;
+  const bool balanced = (flags & TF_ATTENTION_FLAG_BALANCED) != 0;
+  if (balanced &&
+      (choose_variant(dtype, p.head_dim, p.group, p.block_size, flags) != TF_ATTENTION_MFMA ||
+       (flags & (TF_ATTENTION_FLAG_STREAM | TF_ATTENTION_FLAG_VALU)) || p.num_splits <= p.batch ||
+       p.batch > 64 || p.split_counters != nullptr || p.split_size % 32 != 0))
+    return fail(TF_ERROR_UNSUPPORTED,
+                "balanced partitions need the MFMA grid kernel in split-KV mode with the merge "
+                "launch (no arrival counters, no STREAM or VALU flag), num_splits > batch, "
+                "batch <= 64 and split_size % 32 == 0");
   {
     const int32_t variant = choose_variant(dtype, p.head_dim, p.group, p.block_size, flags);
     const int32_t hg = stream_heads_per_group(p.kv_heads, p.head_dim, flags);
@@ -2071,8 +2156,11 @@ int32_t launch_split_stage(const AttnParams &p, int32_t dtype, int32_t flags, hi
   if (variant == TF_ATTENTION_MFMA) {
     AttnParams q = p;
     mfma_geometry(q, flags);
-    const dim3 mgrid(static_cast<unsigned>(p.batch) * static_cast<unsigned>(p.kv_heads / q.heads_per_wg),
-                     static_cast<unsigned>(p.num_splits));
+    q.balanced = balanced ? 1 : 0;
+    const unsigned groups = static_cast<unsigned>(p.kv_heads / q.heads_per_wg);
+    const dim3 mgrid = balanced ? dim3(groups * static_cast<unsigned>(p.num_splits), 1)
+                                : dim3(static_cast<unsigned>(p.batch) * groups,
+                                       static_cast<unsigned>(p.num_splits));
     if (flags & TF_ATTENTION_FLAG_VALU) {
       if (p.head_dim != 64 || p.rope_qkv != nullptr)
         return fail(TF_ERROR_UNSUPPORTED, "the VALU attention form supports head_dim 64 without RoPE");
@@ -2114,25 +2202,28 @@ int32_t launch_merge(const float *partial_max, const float *partial_sum, const f
                      const int32_t *context_lengths, void *output, int32_t batch,
                      int32_t query_heads, int32_t head_dim, int32_t split_size, int32_t num_splits,
                      int32_t partial_stride, int32_t max_tokens, int32_t dtype,
-                     hipStream_t stream) {
+                     hipStream_t stream, bool balanced = false) {
+  const int32_t bal = balanced ? 1 : 0;
   if (batch == 0) return TF_SUCCESS;
   const dim3 grid(static_cast<unsigned>(query_heads), static_cast<unsigned>(batch));
   switch (dtype) {
     case TF_DTYPE_FLOAT32:
       hipLaunchKernelGGL(merge_partials_kernel<float>, grid, dim3(64), 0, stream, partial_max,
                          partial_sum, partial_acc, context_lengths, static_cast<float *>(output),
-                         query_heads, head_dim, split_size, num_splits, partial_stride, max_tokens);
+                         query_heads, head_dim, split_size, num_splits, partial_stride, max_tokens,
+                         bal);
       break;
     case TF_DTYPE_FLOAT16:
       hipLaunchKernelGGL(merge_partials_kernel<_Float16>, grid, dim3(64), 0, stream, partial_max,
                          partial_sum, partial_acc, context_lengths,
                          static_cast<_Float16 *>(output), query_heads, head_dim, split_size,
-                         num_splits, partial_stride, max_tokens);
+                         num_splits, partial_stride, max_tokens, bal);
       break;
     default:
       hipLaunchKernelGGL(merge_partials_kernel<__bf16>, grid, dim3(64), 0, stream, partial_max,
                          partial_sum, partial_acc, context_lengths, static_cast<__bf16 *>(output),
-                         query_heads, head_dim, split_size, num_splits, partial_stride, max_tokens);
+                         query_heads, head_dim, split_size, num_splits, partial_stride, max_tokens,
+                         bal);
       break;
   }
   return check_launch("paged_gqa_decode merge");
@@ -2169,7 +2260,7 @@ extern "C" int32_t tf_paged_gqa_decode(
   if (num_splits == 1 || split_counters != nullptr) return TF_SUCCESS;
   return launch_merge(partial_max, partial_sum, partial_accumulator, context_lengths, output,
                       batch, query_heads, head_dim, split_size, num_splits, partial_row_stride,
-                      p.max_tokens, dtype, s);
+                      p.max_tokens, dtype, s, (flags & TF_ATTENTION_FLAG_BALANCED) != 0);
 }
 
 extern "C" int32_t tf_paged_gqa_decode_rope_append(
@@ -2221,7 +2312,7 @@ extern "C" int32_t tf_paged_gqa_decode_rope_append(
   if (num_splits == 1 || split_counters != nullptr) return TF_SUCCESS;
   return launch_merge(partial_max, partial_sum, partial_accumulator, context_lengths, output,
                       batch, query_heads, head_dim, split_size, num_splits, partial_row_stride,
-                      p.max_tokens, dtype, s);
+                      p.max_tokens, dtype, s, (flags & TF_ATTENTION_FLAG_BALANCED) != 0);
 }
 
 extern "C" int32_t tf_paged_gqa_decode_partials(
@@ -2237,6 +2328,10 @@ extern "C" int32_t tf_paged_gqa_decode_partials(
   if (!partial_max || !partial_sum || !partial_accumulator)
     return fail(TF_ERROR_INVALID_ARGUMENT, "partials stage needs partial buffers");
   if (num_splits < 2) return fail(TF_ERROR_INVALID_ARGUMENT, "partials stage needs num_splits >= 2");
+  if (flags & TF_ATTENTION_FLAG_BALANCED)
+    return fail(TF_ERROR_UNSUPPORTED,
+                "the partials stage takes fixed partitions (tf_paged_gqa_decode_merge has no "
+                "balanced form)");
   AttnParams p;
   if (int32_t s = make_params(p, query, key_cache, value_cache, block_tables, context_lengths,
                               nullptr, partial_max, partial_sum, partial_accumulator,
@@ -2369,5 +2464,5 @@ extern "C" int32_t tf_paged_gqa_decode_noalloc(
   if (num_splits == 1) return TF_SUCCESS;
   return launch_merge(partial_max, partial_sum, partial_acc, context_lengths, output, batch,
                       query_heads, head_dim, split_size, num_splits, stride, p.max_tokens, dtype,
-                      s);
+                      s, (flags & TF_ATTENTION_FLAG_BALANCED) != 0);
 }

@@ -63,11 +63,11 @@ from tensorforge_amd.kernels import (
     residual_rms_norm,
     rms_norm,
     selected_attention_autotune_config,
+    selected_attention_launch,
     set_attention_split_size,
     swiglu,
     swiglu_gate_up,
 )
-from tensorforge_amd.kernels.attention import attention_plan
 from tensorforge_amd.kernels.linear import default_splits
 
 HBM_PEAK_GBS = 8000.0
@@ -158,13 +158,16 @@ def config4(device: torch.device, calls: int) -> list[dict]:
 
 
 def config3(device: torch.device, calls: int) -> list[dict]:
-    """Config 3 (4 rows of 8k..32k at Llama-3-8B geometry) four ways: the
-    entry point's tuned plan (partition size chosen per call, merge launch);
-    the BASELINE's form, 512-token partitions and a separate log-sum-exp
-    merge launch (the entry point with the partition size fixed at 512, as
-    the reference's split_size argument fixes it); and both partition sizes
-    with the in-kernel merge instead (the C ABI with the workspace's arrival
-    counters: the last partition of each (row, kv head) merges)."""
+    """Config 3 (4 rows of 8k..32k at Llama-3-8B geometry) five ways: the
+    entry point's plan (balanced partitions sized on the device from the
+    rows' lengths, two wavefronts each, merge launch); the BASELINE's form,
+    512-token partitions and a separate log-sum-exp merge launch (the entry
+    point with the partition size fixed at 512, as the reference's
+    split_size argument fixes it) and the same partitions with the in-kernel
+    merge (the C ABI with the workspace's arrival counters: the last
+    partition of each (row, kv head) merges); and fixed 4096-token
+    partitions with four wavefronts each (the plan before the balanced
+    partitions) with the merge launch and with the in-kernel merge."""
 
     from tensorforge_amd import _native
 
@@ -190,7 +193,10 @@ def config3(device: torch.device, calls: int) -> list[dict]:
 
     us = graph_time_us(entry, calls, device)
     tuned = dict(selected_attention_autotune_config() or {})
-    results.append(report(f"{name}, tuned plan, merge launch", us, nbytes, record=tuned))
+    launch = selected_attention_launch() or {}
+    results.append(report(f"{name}, entry point plan (balanced partitions, "
+                          f"{launch.get('waves_per_head')} wavefronts each), merge launch", us,
+                          nbytes, record=tuned))
 
     previous = set_attention_split_size(512)
     try:
@@ -201,26 +207,32 @@ def config3(device: torch.device, calls: int) -> list[dict]:
         set_attention_split_size(previous)
 
     capacity = workspace.partial_max.numel()
-    tuned_plan = attention_plan(32768, batch, kv_heads, 32768)
-    for split, flags in ((512, 0), (tuned_plan.split_size, tuned_plan.flags)):
+    fixed_flags = ((1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
+                   | (4 << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
+                   | (1 << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
+    for split, flags, in_kernel, label in (
+            (512, 0, True, "512-token partitions, 1 wavefront each, in-kernel merge"),
+            (4096, fixed_flags, False, "fixed 4096-token partitions, 4 wavefronts each, "
+                                       "merge launch"),
+            (4096, fixed_flags, True, "fixed 4096-token partitions, 4 wavefronts each, "
+                                      "in-kernel merge")):
         splits = -(-32768 // split)
+        counters = workspace.split_counters.data_ptr() if in_kernel else None
 
-        def fused(i: int, split=split, splits=splits, flags=flags) -> None:
+        def raw(i: int, split=split, splits=splits, flags=flags, counters=counters) -> None:
             gpu = pools[i % 2]
             _native.check(_native.library().tf_paged_gqa_decode(
                 gpu.query.data_ptr(), gpu.key_cache.data_ptr(), gpu.value_cache.data_ptr(),
                 gpu.block_tables.data_ptr(), gpu.context_lengths.data_ptr(), output.data_ptr(),
                 workspace.partial_max.data_ptr(), workspace.partial_sum.data_ptr(),
-                workspace.partial_accumulator.data_ptr(), workspace.split_counters.data_ptr(),
+                workspace.partial_accumulator.data_ptr(), counters,
                 capacity, workspace.partial_accumulator.shape[1], batch, query_heads, kv_heads,
                 head_dim, num_blocks, block_size, width, split, splits, case.scale,
                 _native.dtype_code(case.query.dtype), flags, _native.current_stream(device)),
-                "tf_paged_gqa_decode (in-kernel merge)")
+                "tf_paged_gqa_decode")
 
-        us = graph_time_us(fused, calls, device)
-        waves = tuned_plan.waves_per_head if flags else 1
-        results.append(report(f"{name}, {split}-token partitions, {waves} wavefront(s) each, "
-                              f"in-kernel merge", us, nbytes))
+        us = graph_time_us(raw, calls, device)
+        results.append(report(f"{name}, {label}", us, nbytes))
     return results
 
 

@@ -12,6 +12,7 @@ torch's current stream; nothing here synchronises with the device when
 
 from __future__ import annotations
 
+import dataclasses
 from dataclasses import dataclass
 from typing import Any
 
@@ -153,6 +154,15 @@ NARROW_ONE_PASS_MIN_WORKGROUPS = 128
 NARROW_WAVES = 8
 NARROW_SPLIT_WAVES = 4
 NARROW_TOKENS_PER_WAVE = 64
+# Narrow split-KV calls of at least this context and 2..64 rows size their
+# partitions on the device from the rows' lengths (balanced_slots_for); the
+# compact grid holds one workgroup per compute unit, each partition streamed
+# by BALANCED_WAVES wavefronts (config 3 on MI355X: 64.4-64.6 us with 2,
+# 65.4-65.7 with 4, 67.7-68.2 with 6 or 8, 92.5 with 1; fixed 4096-token
+# partitions with 4: 70.8-71.9).
+BALANCED_MIN_CONTEXT = 8192
+BALANCED_WAVES = 2
+COMPUTE_UNITS = 256  # MI355X
 
 
 @dataclass(frozen=True, slots=True)
@@ -167,14 +177,20 @@ class AttentionPlan:
     num_splits: int
     waves_per_head: int
     tokens_per_wave: int = ONE_PASS_TOKENS_PER_WAVE
+    # Split-KV with partitions sized on the device from the rows' lengths
+    # (TF_ATTENTION_FLAG_BALANCED): split_size is then the smallest partition
+    # and num_splits the slots per kv head over all rows together.
+    balanced: bool = False
 
     @property
     def flags(self) -> int:
-        """The C ABI's launch flags for several wavefronts per kv head (0 for one)."""
+        """The C ABI's launch flags: several wavefronts per kv head (none for
+        one) and the balanced partitions."""
 
+        flags = _native.TF_ATTENTION_FLAG_BALANCED if self.balanced else 0
         if self.waves_per_head <= 1:
-            return 0
-        return ((1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
+            return flags
+        return (flags | (1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
                 | (self.waves_per_head << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
                 | ((self.tokens_per_wave // 64) << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
 
@@ -208,6 +224,26 @@ def narrow_split_size_for(max_context_length: int, batch: int, kv_heads: int) ->
     )
 
 
+def balanced_slots_for(max_context_length: int, batch: int, kv_heads: int) -> int:
+    """Slots per kv head of a balanced split-KV call, or 0 where the call
+    keeps fixed partitions: one slot per compute unit and kv head
+    (``COMPUTE_UNITS // kv_heads``), so the compact grid is one workgroup
+    per compute unit.  Only for 2..64 rows of at least BALANCED_MIN_CONTEXT
+    tokens, where rows of unequal length leave fixed partitions unevenly
+    spread (config 3: rows of 8k..32k in 4096-token partitions give 160 of
+    256 workgroups work); the slots must outnumber the rows (the device-side
+    partition size needs it) and fit one per 256 tokens of the context, so
+    the workspace the reference sizes for 256-token partitions holds the
+    partials ([row][query head][slot], as for fixed partitions)."""
+
+    if batch < 2 or batch > 64 or max_context_length < BALANCED_MIN_CONTEXT:
+        return 0
+    slots = COMPUTE_UNITS // max(kv_heads, 1)
+    if slots <= batch or slots > -(-max_context_length // REFERENCE_SPLIT_SIZE):
+        return 0
+    return slots
+
+
 def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capacity: int,
                    attention_path: str = "auto") -> AttentionPlan:
     """The launch of a call from host-known sizes only.
@@ -229,7 +265,10 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
     * otherwise split-KV with up to 4 wavefronts per split and the partition
       size of narrow_split_size_for (1 x 4k: 11.9 against 13.5 us; 8 x 4k:
       14.2 against 15.5; config 3, 4 x 8-32k x 8 kv heads at D 128: 74.7
-      against 78.4);
+      against 78.4), or for 2..64 rows of >= 8k the balanced partitions of
+      balanced_slots_for, sized on the device from the rows' lengths, with
+      two wavefronts each (config 3: 64.5 against 70.8-71.9 us for fixed
+      4096-token partitions);
     * a partition size fixed by the caller (set_attention_split_size) or
       ``attention_path="split_kv"``: split-KV with one wavefront per split
       and attention_split_size_for; ``"one_pass"`` forces one pass.
@@ -252,6 +291,11 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
     if (attention_path == "one_pass" or launch_context <= NARROW_ONE_PASS_CONTEXT
             or (workgroups >= NARROW_ONE_PASS_MIN_WORKGROUPS and launch_context <= 2048)):
         return AttentionPlan(True, capacity32, 1, NARROW_WAVES, NARROW_TOKENS_PER_WAVE)
+    slots = balanced_slots_for(launch_context, batch, kv_heads)
+    if slots:
+        smallest = (-(-launch_context // slots) + 63) // 64 * 64
+        return AttentionPlan(False, smallest, slots, BALANCED_WAVES, NARROW_TOKENS_PER_WAVE,
+                             balanced=True)
     narrow = narrow_split_size_for(launch_context, batch, kv_heads)
     return AttentionPlan(False, narrow, (launch_context + narrow - 1) // narrow,
                          NARROW_SPLIT_WAVES, NARROW_TOKENS_PER_WAVE)
@@ -345,6 +389,10 @@ def paged_gqa_decode_attention(
     group = query_heads // kv_heads
     variant = _native.library().tf_paged_gqa_decode_variant(dtype, head_dim, group, block_size, 0)
     kernel = "mfma" if variant == _native.TF_ATTENTION_MFMA else "generic"
+    if plan.balanced and kernel != "mfma":
+        # The generic kernel takes fixed partitions: the same slots of the
+        # smallest size still cover the context.
+        plan = dataclasses.replace(plan, balanced=False)
     device = query.device
     stream = _native.current_stream(device)
     counters_ptr = None
@@ -466,8 +514,10 @@ def paged_gqa_decode_attention(
     _LAST_ATTENTION_LAUNCH = {
         "kernel": kernel,
         "waves_per_head": plan.waves_per_head if kernel == "mfma" else 1,
-        "grid": (batch * kv_heads, num_splits),
+        "grid": ((kv_heads * num_splits, 1) if use_split_kv and plan.balanced
+                 else (batch * kv_heads, num_splits)),
         "in_kernel_merge": bool(use_split_kv and counters_ptr is not None),
+        "balanced_partitions": bool(use_split_kv and plan.balanced),
         "group_size": group,
         "launch_context": launch_context,
     }

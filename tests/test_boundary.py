@@ -75,7 +75,7 @@ def test_library_exports_every_declared_symbol(lib) -> None:
 def test_header_constants_match_the_python_binding() -> None:
     text = HEADER.read_text()
     for name in ("TF_ATTENTION_FLAG_FORCE_GENERIC", "TF_ATTENTION_FLAG_STREAM",
-                 "TF_ATTENTION_FLAG_VALU",
+                 "TF_ATTENTION_FLAG_VALU", "TF_ATTENTION_FLAG_BALANCED",
                  "TF_ATTENTION_WAVES_PER_CU_SHIFT", "TF_ATTENTION_DEPTH_SHIFT",
                  "TF_ATTENTION_HEADS_PER_WG_SHIFT", "TF_ATTENTION_TOKENS_PER_WAVE_SHIFT"):
         match = re.search(rf"#define {name} (\d+)", text)
@@ -242,11 +242,13 @@ def test_attention_plan() -> None:
     wavefronts per kv head, one per 576 tokens); for narrow calls one pass
     with up to 8 wavefronts (one per 64 tokens) at short contexts and
     split-KV with up to 4 wavefronts per split at long ones (the reference's
-    own 1 x 8 case keeps its 256-token partitions; cfg3 takes 4096); one
-    wavefront per split when the caller fixes the partition size or forces
-    split-KV."""
+    own 1 x 8 case keeps its 256-token partitions), with balanced
+    partitions -- one slot per compute unit and kv head, the size set on the
+    device -- for 2..64 rows of >= 8k when the slots fit one per 256 tokens
+    (cfg3: 32 slots of >= 1024 tokens); one wavefront per split when the
+    caller fixes the partition size or forces split-KV."""
 
-    from tensorforge_amd.kernels.attention import narrow_split_size_for
+    from tensorforge_amd.kernels.attention import balanced_slots_for, narrow_split_size_for
 
     cfg2 = attention_plan(2048, 72, 4, 2048)
     assert (cfg2.one_pass, cfg2.num_splits, cfg2.waves_per_head) == (True, 1, 4)
@@ -266,7 +268,16 @@ def test_attention_plan() -> None:
     long8 = attention_plan(4000, 8, 4, 4096)
     assert (long8.one_pass, long8.split_size, long8.num_splits) == (False, 512, 8)
     cfg3 = attention_plan(32768, 4, 8, 32768)
-    assert (cfg3.one_pass, cfg3.split_size, cfg3.num_splits) == (False, 4096, 8)
+    assert (cfg3.one_pass, cfg3.split_size, cfg3.num_splits, cfg3.balanced) == (False, 1024, 32,
+                                                                                True)
+    assert cfg3.flags == 32 | (1 << 24) | (1 << 20) | (2 << 8)
+    assert balanced_slots_for(32768, 1, 8) == 0      # one row: fixed partitions
+    assert balanced_slots_for(8191, 4, 8) == 0       # below 8k
+    assert balanced_slots_for(8192, 8, 4) == 0       # 64 slots > 8192 / 256
+    assert balanced_slots_for(16384, 8, 4) == 64
+    assert balanced_slots_for(16384, 64, 4) == 0     # slots must outnumber rows
+    assert balanced_slots_for(65536, 65, 1) == 0     # at most 64 rows
+    assert not attention_plan(8192, 8, 4, 8192).balanced
     assert narrow_split_size_for(32768, 1, 4) == 2048  # at most 16 splits per row
     assert narrow_split_size_for(4000, 1, 4) == 256
     assert attention_plan(4096, 64, 4, 4096).waves_per_head == 8

@@ -235,9 +235,10 @@ def test_llama3_long_context_split_kv(device):
 
 
 def test_llama3_long_context_auto_plan(device):
-    """BASELINE config 3 under the entry point's own plan: 4096-token
-    partitions with up to four wavefronts each (whole-row loads at D 128),
-    then the merge launch."""
+    """BASELINE config 3 under the entry point's own plan: partitions sized
+    on the device from the rows' lengths (at least 1024 tokens, 32 slots per
+    kv head) with two wavefronts each (whole-row loads at D 128), then the
+    merge launch."""
 
     case = llama3_long_context_case(seed=1)
     gpu = case.to(device)
@@ -246,9 +247,10 @@ def test_llama3_long_context_auto_plan(device):
         max_context_length=32768,
     )
     assert selected_attention_autotune_config() == {
-        "path": "split_kv", "split_size": 4096, "num_splits": 8,
+        "path": "split_kv", "split_size": 1024, "num_splits": 32,
     }
-    assert selected_attention_launch()["waves_per_head"] == 4
+    assert selected_attention_launch()["waves_per_head"] == 2
+    assert selected_attention_launch()["balanced_partitions"]
     _check_against_oracle(case, output.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, "cfg3 auto")
 
 
