@@ -84,16 +84,13 @@ enum tf_attention_variant {
 };
 
 /* tf_paged_gqa_decode* flags.  FORCE_GENERIC selects the generic family.
- * STREAM (MFMA family, split_counters given, num_splits >= 2) replaces the
- * one-workgroup-per-split grid by a balanced streaming kernel: equal
- * contiguous ranges of 16-token tiles per wavefront whatever the length
- * distribution.  Tuning fields (0 selects the defaults):
- *   bits 8-15   grid kernel: wavefronts per kv head (heads x this <= 8);
- *               streaming kernel: wavefronts per compute unit
- *   bits 16-19  streaming kernel: tiles in flight per wavefront (2..4)
- *   bits 20-23  grid kernel: kv heads per workgroup (must divide kv_heads)
- *   bits 24-30  grid kernel: tokens per wavefront / 64; a row then uses
- *               ceil(its tokens / that) of the head's wavefronts (0: all)
+ * Tuning fields of the MFMA grid kernel (0 selects the defaults):
+ *   bits 8-15   wavefronts per kv head (heads x this <= 8)
+ *   bits 20-23  kv heads per workgroup (must divide kv_heads)
+ *   bits 24-30  tokens per wavefront / 64; a row then uses ceil(its tokens
+ *               / that) of the head's wavefronts (0: all)
+ * Other bits (2, 4, 8, 64, 128 and bits 16-19) are rejected with
+ * TF_ERROR_UNSUPPORTED.
  * VALU (the MFMA grid kernel's calls, head_dim 64, no RoPE) computes the
  * score and P.V products on the VALU -- packed two-element dot products
  * (v_dot2_f32_bf16 / _f16) and fp32 FMAs -- with the same grid, loads and
@@ -110,11 +107,9 @@ enum tf_attention_variant {
  * most of it without work.  Partials land in slot j < ceil(len / partition)
  * of their row, as with fixed partitions; the merge recomputes the size. */
 #define TF_ATTENTION_FLAG_FORCE_GENERIC 1
-#define TF_ATTENTION_FLAG_STREAM 4
 #define TF_ATTENTION_FLAG_VALU 16
 #define TF_ATTENTION_FLAG_BALANCED 32
 #define TF_ATTENTION_WAVES_PER_CU_SHIFT 8
-#define TF_ATTENTION_DEPTH_SHIFT 16
 #define TF_ATTENTION_HEADS_PER_WG_SHIFT 20
 #define TF_ATTENTION_TOKENS_PER_WAVE_SHIFT 24
 
@@ -167,7 +162,7 @@ int32_t tf_paged_gqa_decode(
 /*
  * tf_paged_gqa_decode fused with the decode step's RoPE and KV append
  * (MFMA grid kernel only: bf16/fp16, head_dim 32/64/128, group <= 16,
- * block_size % 16 == 0; no STREAM flag).  Row b of `qkv` (qkv_row_stride
+ * block_size % 16 == 0).  Row b of `qkv` (qkv_row_stride
  * elements apart) holds [query heads | kv heads of k | kv heads of v],
  * head_dim each, unrotated.  Each workgroup rotates its query group at
  * positions[b] (half-split RoPE with the cos/sin tables [table_rows,
@@ -203,8 +198,8 @@ int32_t tf_paged_gqa_decode_rope_append(
  * process ends; larger requests fail with TF_ERROR_INVALID_ARGUMENT.  The
  * split stage writes every partial the merge reads, so the array needs no
  * clearing.  All calls on one GPU share that array: calls that overlap in
- * time on one GPU race.  The STREAM flag (which needs counters) is
- * rejected; other arguments are as in tf_paged_gqa_decode, whose kernels it
+ * time on one GPU race.  There are no arrival counters (the merge is a
+ * launch); other arguments are as in tf_paged_gqa_decode, whose kernels it
  * runs, with the same results.
  */
 #define TF_NOALLOC_SCRATCH_BYTES (8LL << 20)

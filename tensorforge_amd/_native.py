@@ -23,11 +23,9 @@ TF_DTYPE_BFLOAT16 = 2
 TF_ATTENTION_GENERIC = 0
 TF_ATTENTION_MFMA = 1
 TF_ATTENTION_FLAG_FORCE_GENERIC = 1
-TF_ATTENTION_FLAG_STREAM = 4
 TF_ATTENTION_FLAG_VALU = 16
 TF_ATTENTION_FLAG_BALANCED = 32
 TF_ATTENTION_WAVES_PER_CU_SHIFT = 8
-TF_ATTENTION_DEPTH_SHIFT = 16
 TF_ATTENTION_HEADS_PER_WG_SHIFT = 20
 TF_ATTENTION_TOKENS_PER_WAVE_SHIFT = 24
 TF_NOALLOC_SCRATCH_BYTES = 8 << 20

@@ -31,10 +31,6 @@
 //    partials).  With arrival counters the last workgroup of a (row, kv
 //    head) to finish merges the split partials in the same launch.
 //
-//  * Streaming (opt-in, TF_ATTENTION_FLAG_STREAM): one wavefront per
-//    workgroup, equal contiguous ranges of 16-token tiles per wavefront
-//    over the whole batch, so ragged lengths cannot leave workgroups idle.
-//
 //  * Generic (any dtype, head_dim <= 256, group <= 64, any page size).  A
 //    straightforward LDS-tiled implementation kept for fp32 and unusual
 //    shapes; it is the accuracy reference path on the GPU (fp32 math
@@ -1057,623 +1053,6 @@ paged_decode_mfma_kernel(AttnParams p) {
 }
 
 // ===========================================================================
-// Balanced streaming MFMA kernel (split mode with arrival counters)
-// ===========================================================================
-// One wavefront per workgroup.  The work is the global sequence of 16-token
-// tiles ordered by (row, kv-head group, tile).  A kv-head group is HG
-// adjacent kv heads whose slices of a token row form one contiguous run of
-// HG * head_dim elements (>= 512 bytes where the geometry allows): the
-// cache stores [page, token, kv head, head_dim], so a wavefront that reads
-// all heads of a group for a tile requests whole DRAM rows together instead
-// of scattering 128-byte pieces over time (measured: ~1.5x the bandwidth of
-// one head per wavefront).  A prefix sum of the device-side lengths
-// (computed by every wavefront; the lengths are a few hundred bytes) gives
-// each of the `nw` wavefronts an equal contiguous range of tiles, so there
-// are no empty or ragged workgroups whatever the length distribution.  A
-// wavefront streams its range with DEPTH tiles of K/V in flight, across
-// unit boundaries.  A unit (row, head group) wholly inside one range is
-// finished in place; one shared by several ranges leaves one partial per
-// range ("piece"), and the last wavefront to count itself in merges them.
-// Piece p of a unit lands in partial slot p of its rows, and the range
-// length is kept >= max tiles / (slots - 1) so a unit never spans more
-// pieces than there are slots.
-//
-// Per tile and head: scores S^T = K q^T with v_mfma_f32_16x16x32 (lane
-// (l16, q4) holds S[token 4q4 + r][query head l16]); P in that layout is
-// directly the B operand of v_mfma_f32_16x16x16 (k = the 4 tokens of the
-// lane group), and V^T (A operand: dim 16n + l16, tokens 4q4..4q4+3) is one
-// ds_read_b64_tr_b16 of V staged token-major in LDS.
-constexpr int kStreamMinTiles = 4;  // floor on tiles per wavefront range
-constexpr int kStreamMaxRows = 4096;
-constexpr int kStreamWavesPerCu = 4;  // default: one wavefront per SIMD
-
-__device__ __forceinline__ int32_t wave_of_tile(int64_t t, int32_t nw, int64_t total) {
-  // largest w with floor(w * total / nw) <= t
-  return static_cast<int32_t>(((t + 1) * nw - 1) / total);
-}
-
-template <typename T>
-struct Mfma16;
-
-template <>
-struct Mfma16<__bf16> {
-  static __device__ __forceinline__ f32x4 mma(i16x4 a, i16x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ i16x4 pack(float a, float b, float c, float d) {
-    typedef __bf16 v4 __attribute__((ext_vector_type(4)));
-    const v4 v = {static_cast<__bf16>(a), static_cast<__bf16>(b), static_cast<__bf16>(c),
-                  static_cast<__bf16>(d)};
-    return __builtin_bit_cast(i16x4, v);
-  }
-};
-
-template <>
-struct Mfma16<_Float16> {
-  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-  static __device__ __forceinline__ f32x4 mma(i16x4 a, i16x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a),
-                                                 __builtin_bit_cast(h4, b), c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ i16x4 pack(float a, float b, float c, float d) {
-    const h4 v = {static_cast<_Float16>(a), static_cast<_Float16>(b), static_cast<_Float16>(c),
-                  static_cast<_Float16>(d)};
-    return __builtin_bit_cast(i16x4, v);
-  }
-};
-
-// Dynamic LDS of the streaming kernel: row starts (rows + 1 ints), row
-// lengths (rows ints), then a region shared by the V staging tiles (HG
-// heads x 16 tokens) and the merge weights (16 heads x 64 pieces floats).
-__host__ __device__ inline size_t stream_meta_bytes(int32_t rows) {
-  return (static_cast<size_t>(2 * rows + 1) * 4 + 15) / 16 * 16;
-}
-
-// Query blocks staged per page window: a unit's query heads are one
-// contiguous block of HU * head_dim elements; a window holds at most
-// stream_q_slots units (>= 2) within kStreamQBytes of LDS.
-constexpr int32_t kStreamQBytes = 8192;
-
-__host__ __device__ inline int32_t stream_q_slots(int32_t unit_heads, int32_t head_dim) {
-  const int32_t per_unit = unit_heads * head_dim * 2;
-  const int32_t slots = kStreamQBytes / per_unit;
-  return slots < 2 ? 2 : slots;
-}
-
-size_t stream_lds_bytes(int head_dim, int32_t heads_per_group, int32_t group, int32_t rows) {
-  const size_t vtiles = static_cast<size_t>(heads_per_group) * 16 * (head_dim * 2 + 16);
-  const size_t weights = 16 * 64 * sizeof(float);
-  const size_t transpose = 16 * static_cast<size_t>(head_dim) * sizeof(float);
-  size_t region = vtiles > weights ? vtiles : weights;
-  if (transpose > region) region = transpose;
-  const int32_t unit_heads = heads_per_group * group;
-  const size_t qbytes = static_cast<size_t>(stream_q_slots(unit_heads, head_dim)) * unit_heads *
-                        head_dim * 2;
-  return stream_meta_bytes(rows) + qbytes + region;
-}
-
-template <typename T, int D, int HG, int DEPTH>
-__global__ void __launch_bounds__(64)
-paged_decode_stream_kernel(AttnParams p) {
-  using M = Mfma<T>;
-  using M16 = Mfma16<T>;
-  using vec8 = typename M::vec8;
-  constexpr int KS = D / 32;
-  constexpr int NB = D / 16;
-  constexpr int kRow = v_row_bytes<D>();
-  extern __shared__ __attribute__((aligned(16))) unsigned char stream_smem[];
-  const int lane = threadIdx.x;
-  const int l16 = lane & 15;
-  const int q4 = lane >> 4;
-  const int32_t R = p.batch;
-  const int32_t NG = p.kv_heads / HG;  // head groups per row
-  const int32_t G = p.group;
-  const int32_t HU = HG * G;  // query heads of a unit
-  const int32_t QSLOTS = stream_q_slots(HU, D);
-  int32_t *rstart = reinterpret_cast<int32_t *>(stream_smem);  // [R + 1] first tile of row / NG
-  int32_t *rctx = rstart + R + 1;                               // [R] clamped row length
-  T *qs = reinterpret_cast<T *>(stream_smem + stream_meta_bytes(R));  // [QSLOTS][HU][D] queries
-  unsigned char *vt = stream_smem + stream_meta_bytes(R) + static_cast<size_t>(QSLOTS) * HU * D * 2;
-  float *weights = reinterpret_cast<float *>(vt);               // merge weights (after streaming)
-
-  // ---- row lengths (all loads in flight together) and their prefix sum ------
-  // Unit u = b * NG + hg covers tiles [NG * rstart[b] + hg * n_b, + n_b) of
-  // the global tile sequence, n_b = ceil(ctx_b / 16).
-#pragma unroll 8
-  for (int32_t b = lane; b < R; b += 64) rctx[b] = clamp_context(p, b);
-  __asm__ volatile("" ::: "memory");
-  int32_t carry = 0, nmax = 0;
-  for (int32_t base = 0; base < R; base += 64) {
-    const int32_t b = base + lane;
-    const int32_t n = b < R ? (rctx[b] + 15) >> 4 : 0;
-    nmax = max(nmax, n);
-    int32_t x = n;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int32_t y = __shfl_up(x, off, 64);
-      if (lane >= off) x += y;
-    }
-    if (b < R) rstart[b + 1] = carry + x;
-    carry += __shfl(x, 63, 64);
-  }
-  if (lane == 0) rstart[0] = 0;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) nmax = max(nmax, __shfl_xor(nmax, off, 64));
-  const int64_t total = static_cast<int64_t>(carry) * NG;
-  __asm__ volatile("" ::: "memory");
-  auto unit_start = [&](int32_t u) -> int64_t {
-    const int32_t b = u / NG;
-    const int32_t hg = u - b * NG;
-    return static_cast<int64_t>(NG) * rstart[b] +
-           static_cast<int64_t>(hg) * (rstart[b + 1] - rstart[b]);
-  };
-
-  // Zero-length rows: outputs are zeros (spread over the wavefronts).
-  for (int32_t b = blockIdx.x; b < R; b += gridDim.x) {
-    if (rctx[b] != 0) continue;
-    T *out = static_cast<T *>(p.output) + static_cast<int64_t>(b) * p.query_heads * D;
-    for (int i = lane; i < p.query_heads * D; i += 64) out[i] = from_float<T>(0.f);
-  }
-  if (total == 0) return;
-
-  // ---- this wavefront's range ----------------------------------------------
-  // Each wavefront owns two partial slots of HU = HG * G rows (its first and
-  // its last unit), so the partial buffers bound the wavefront count.  The
-  // range length is kept >= ceil(nmax / 62) tiles so that no unit spans
-  // more than 63 pieces (the merge keeps one weight per (head, piece) in
-  // a 64-wide LDS row).
-  const int32_t min_tiles = max(kStreamMinTiles, (nmax + 61) / 62);
-  int64_t nw64 = min<int64_t>(total / min_tiles, p.partial_rows / (2 * HU));
-  if (nw64 < 1) nw64 = 1;
-  const int32_t nw = static_cast<int32_t>(min<int64_t>(nw64, gridDim.x));
-  const int32_t w = blockIdx.x;
-  if (w >= nw) return;
-  const int64_t t_begin = static_cast<int64_t>(w) * total / nw;
-  const int64_t t_end = static_cast<int64_t>(w + 1) * total / nw;
-  const int32_t range = static_cast<int32_t>(t_end - t_begin);
-
-  const uint32_t token_bytes = static_cast<uint32_t>(p.kv_heads) * D * sizeof(T);
-  const unsigned char *kbytes = static_cast<const unsigned char *>(p.key_cache);
-  const unsigned char *vbytes = static_cast<const unsigned char *>(p.value_cache);
-  const uint32_t lane_full = static_cast<uint32_t>(l16) * token_bytes + 16u * q4;
-  const uint32_t lane_first = 16u * q4;
-
-  // ---- tile window: lane i describes tile t_begin + win + i ---------------
-  int32_t win = 0;         // range-relative index of lane 0's tile
-  int32_t win_count = 0;   // tiles of the range inside the window
-  int32_t next = 0;        // next window slot to issue
-  int32_t w_unit = -1;     // unit of the tile
-  int32_t w_page = -1;     // physical page
-  int32_t w_inpage = 0;    // token offset of the tile inside its page
-  int32_t w_ntok = 0;      // present tokens of the tile (0..16)
-  int32_t w_row = 0;       // row (sequence) of the tile's unit
-  int32_t w_hg = 0;        // kv-head group of the tile's unit
-  int32_t cont_unit = -1;  // unit of the first tile after the window, if in range
-  int32_t win_u0 = 0;      // unit in query slot 0
-  auto find_unit = [&](int64_t g) {  // u with unit_start(u) <= g < unit_start(u + 1)
-    int32_t lo = 0, hi = R;  // row b with NG * rstart[b] <= g < NG * rstart[b + 1]
-    while (hi - lo > 1) {
-      const int32_t mid = (lo + hi) >> 1;
-      if (static_cast<int64_t>(NG) * rstart[mid] <= g) lo = mid; else hi = mid;
-    }
-    const int32_t n = rstart[lo + 1] - rstart[lo];
-    const int64_t rel = g - static_cast<int64_t>(NG) * rstart[lo];
-    return lo * NG + static_cast<int32_t>(n > 0 ? rel / n : 0);
-  };
-  // A window is the next (up to) 64 tiles of the range whose units have a
-  // query slot: units win_u0 .. win_u0 + QSLOTS - 1, whose query blocks are
-  // staged into LDS here, so tiles carry no query loads of their own.
-  auto load_window = [&](int32_t first) {
-    win = first;
-    const int32_t avail = min(64, range - first);
-    const bool avail_lane = lane < avail;
-    const int64_t g = t_begin + first + (avail_lane ? lane : 0);
-    const int32_t u = find_unit(g);  // non-decreasing over the lanes
-    const int32_t u0 = __builtin_amdgcn_readfirstlane(u);
-    const bool in_range = avail_lane && u - u0 < QSLOTS;
-    win_count = __builtin_popcountll(__ballot(in_range));
-    win_u0 = u0;
-    next = 0;
-    cont_unit = first + win_count < range ? find_unit(t_begin + first + win_count) : -1;
-    w_unit = in_range ? u : -1;
-    w_page = -1;
-    w_ntok = 0;
-    w_inpage = 0;
-    w_row = u / NG;
-    w_hg = u - w_row * NG;
-    if (in_range) {
-      const int32_t tile = static_cast<int32_t>(g - unit_start(u));
-      const int32_t tok = 16 * tile;
-      const int32_t bb = w_row;
-      const int32_t logical = p.page_shift >= 0 ? (tok >> p.page_shift) : (tok / p.block_size);
-      const int32_t page = p.block_tables[static_cast<int64_t>(bb) * p.table_width + logical];
-      w_inpage = tok - logical * p.block_size;
-      const bool ok = page >= 0 && page < p.num_blocks;
-      w_page = ok ? page : -1;
-      w_ntok = ok ? min(16, rctx[bb] - tok) : 0;
-    }
-    // Query blocks of the window's units (16 bytes per lane and step).
-    const int32_t nq = __builtin_amdgcn_readlane(u, win_count - 1) - u0 + 1;
-    const int32_t chunks = HU * D / 8;
-    for (int32_t c = lane; c < nq * chunks; c += 64) {
-      const int32_t j = c / chunks;
-      const int32_t off = c - j * chunks;
-      const int32_t uj = u0 + j;
-      const int32_t bj = uj / NG;
-      const T *src = static_cast<const T *>(p.query) +
-                     (static_cast<int64_t>(bj) * p.query_heads + static_cast<int64_t>(uj - bj * NG) * HU) * D +
-                     8 * off;
-      *reinterpret_cast<vec8 *>(qs + static_cast<int64_t>(j) * HU * D + 8 * off) =
-          *reinterpret_cast<const vec8 *>(src);
-    }
-    // Complete the window's loads here, where no tile is in flight: a load
-    // still pending at the streaming loop's entry would make the compiler
-    // wait for all loads at every use inside the loop.
-    __builtin_amdgcn_s_waitcnt(0);
-  };
-  load_window(0);
-
-  // ---- per-tile register sets -----------------------------------------------
-  struct Set {
-    vec8 k[HG][KS], v[HG][KS];
-    uint32_t valid;  // bit t: token t of the tile is present
-    int32_t unit;    // -1: no tile
-  };
-
-  // Issue the loads of the next tile of the window into `st`.  Past the end
-  // the same loads read a stand-in line (cache element 0), so the load
-  // sequence never branches and the wait counts stay exact.
-  auto issue = [&](Set &st) {
-    // next and win_count are wave-uniform; readfirstlane makes that visible
-    // to the compiler, so the selects below stay scalar and branch-free.
-    const int32_t nx = __builtin_amdgcn_readfirstlane(next);
-    const bool have = nx < __builtin_amdgcn_readfirstlane(win_count);
-    const int f = have ? nx : 0;
-    next = nx + (have ? 1 : 0);
-    const int32_t unit_f = __builtin_amdgcn_readlane(w_unit, f);
-    const int32_t ntok_f = __builtin_amdgcn_readlane(w_ntok, f);
-    const int32_t unit = have ? unit_f : -1;
-    const int32_t ntok = have ? ntok_f : 0;
-    const int32_t page = __builtin_amdgcn_readlane(w_page, f);
-    const int32_t inpage = __builtin_amdgcn_readlane(w_inpage, f);
-    st.unit = unit;
-    st.valid = ntok >= 16 ? 0xffffu : ((1u << ntok) - 1u);
-    const int32_t hg_f = __builtin_amdgcn_readlane(w_hg, f);
-    const int32_t hg = have ? hg_f : 0;
-    const int64_t tile_off =
-        ntok > 0 ? (static_cast<int64_t>(page) * p.block_size + inpage) * token_bytes +
-                       static_cast<int64_t>(hg) * HG * D * sizeof(T)
-                 : 0;
-    const uint32_t lane_off = l16 < ntok ? lane_full : lane_first;
-#pragma unroll
-    for (int h = 0; h < HG; ++h)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const uint32_t o = lane_off + (ntok > 0 ? h * D * sizeof(T) : 0) + 64 * ks;
-        st.k[h][ks] = load_stream16<vec8>(kbytes + tile_off + o);
-        st.v[h][ks] = load_stream16<vec8>(vbytes + tile_off + o);
-      }
-  };
-
-  f32x4 acc[HG][NB];
-  float m_run[HG], l_run[HG];
-  auto reset = [&]() {
-#pragma unroll
-    for (int h = 0; h < HG; ++h) {
-#pragma unroll
-      for (int n = 0; n < NB; ++n) acc[h][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-      m_run[h] = kNegInf;
-      l_run[h] = 0.f;
-    }
-  };
-  reset();
-  // Units whose piece was left as a partial: at most the first and the last
-  // unit of the range.
-  int32_t pending_first = -1, pending_last = -1;
-
-  auto compute = [&](Set &st) {
-    const bool partial = st.valid != 0xffffu;  // uniform
-#pragma unroll
-    for (int h = 0; h < HG; ++h) {
-      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-      {
-        // Query operand from the window's LDS slot; columns l16 >= G repeat
-        // head 0 of the group and their results are never stored.
-        const T *qrow = qs + (static_cast<int64_t>(st.unit - win_u0) * HU + h * G +
-                              (l16 < G ? l16 : 0)) * D;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          s = M::mma(st.k[h][ks], *reinterpret_cast<const vec8 *>(qrow + 32 * ks + 8 * q4), s);
-      }
-      float sc[4] = {s[0], s[1], s[2], s[3]};  // token 4q4 + r, query head l16
-      if (partial) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (!((st.valid >> (4 * q4 + r)) & 1u)) sc[r] = kNegInf;
-        // Stand-in V rows of absent tokens are cleared so that 0 * (non-finite)
-        // cannot leak into the accumulator.
-        const bool mine = (st.valid >> l16) & 1u;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) st.v[h][ks] = mine ? st.v[h][ks] : vec8{};
-      }
-      float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])) * p.scale_log2;
-      if (__ballot(mx > m_run[h] + kRescaleThreshold) != 0) {
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float m_new = fmaxf(m_run[h], mx);
-        if (m_new != kNegInf) {  // uniform
-          const float alpha = fast_exp2(m_run[h] - m_new);
-          m_run[h] = m_new;
-          l_run[h] *= alpha;
-#pragma unroll
-          for (int n = 0; n < NB; ++n) acc[h][n] *= alpha;
-        }
-      }
-      if (m_run[h] == kNegInf) continue;  // uniform: nothing present yet
-      float pr[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(__builtin_fmaf(sc[r], p.scale_log2, -m_run[h]));
-      l_run[h] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-      const i16x4 pf = M16::pack(pr[0], pr[1], pr[2], pr[3]);
-      unsigned char *vh = vt + h * 16 * kRow;
-      __asm__ volatile("" ::: "memory");
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        *reinterpret_cast<vec8 *>(vh + l16 * kRow + (32 * ks + 8 * q4) * 2) = st.v[h][ks];
-      __asm__ volatile("" ::: "memory");
-      const unsigned char *rd = vh + (4 * q4 + (l16 >> 2)) * kRow + (l16 & 3) * 8;
-#pragma unroll
-      for (int n = 0; n < NB; ++n) {
-        const i16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(rd + 32 * n));
-        acc[h][n] = M16::mma(a, pf, acc[h][n]);
-      }
-      __asm__ volatile("" ::: "memory");
-    }
-  };
-
-  // Partial slot of (wavefront wv, unit starting at tile u_first): 2 wv for
-  // the unit holding the first tile of wv's range, 2 wv + 1 for the one
-  // holding its last tile (when different).
-  auto piece_slot = [&](int32_t wv, int64_t u_first) -> int64_t {
-    const int64_t tb = static_cast<int64_t>(wv) * total / nw;
-    return 2 * static_cast<int64_t>(wv) + (u_first > tb ? 1 : 0);
-  };
-
-  // Finish the piece of `unit` held in (m_run, l_run, acc): the output when
-  // the unit lies inside this range, else a partial in this wavefront's
-  // slot, transposed through LDS so each store writes consecutive floats.
-  auto flush = [&](int32_t unit) {
-    const int32_t bb = unit / NG;
-    const int32_t hg = unit - bb * NG;
-    const int64_t u_first = unit_start(unit);
-    const int32_t w0 = wave_of_tile(u_first, nw, total);
-    const int32_t w1 = wave_of_tile(u_first + (rstart[bb + 1] - rstart[bb]) - 1, nw, total);
-    const int64_t slot_row = piece_slot(w, u_first) * HU;
-    float *xt = reinterpret_cast<float *>(vt);
-#pragma unroll
-    for (int h = 0; h < HG; ++h) {
-      float l = l_run[h];
-      l += __shfl_xor(l, 16, 64);
-      l += __shfl_xor(l, 32, 64);
-      if (w0 == w1) {
-        if (l16 < G) {
-          T *out = output_row<T>(p, bb, (hg * HG + h) * G + l16);
-          const float inv = l > 0.f ? 1.f / l : 0.f;
-#pragma unroll
-          for (int n = 0; n < NB; ++n) {
-            typedef T t4 __attribute__((ext_vector_type(4)));
-            const t4 v = {from_float<T>(acc[h][n][0] * inv), from_float<T>(acc[h][n][1] * inv),
-                          from_float<T>(acc[h][n][2] * inv), from_float<T>(acc[h][n][3] * inv)};
-            *reinterpret_cast<t4 *>(out + 16 * n + 4 * q4) = v;
-          }
-        }
-      } else {
-        __asm__ volatile("" ::: "memory");
-        if (l16 < G) {
-#pragma unroll
-          for (int n = 0; n < NB; ++n)
-            *reinterpret_cast<f32x4 *>(xt + l16 * D + 16 * n + 4 * q4) = acc[h][n];
-        }
-        __asm__ volatile("" ::: "memory");
-        const int64_t row0 = slot_row + h * G;
-        for (int idx = lane; idx < G * D; idx += 64) {
-          const int g = idx / D;
-          __hip_atomic_store(p.partial_acc + (row0 + g) * p.partial_stride + (idx - g * D),
-                             xt[idx], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        if (l16 < G && q4 == 0) {
-          __hip_atomic_store(p.partial_max + row0 + l16, m_run[h], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(p.partial_sum + row0 + l16, l, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __asm__ volatile("" ::: "memory");
-      }
-    }
-    if (w0 != w1) {
-      if (pending_first < 0)
-        pending_first = unit;
-      else
-        pending_last = unit;
-    }
-    reset();
-  };
-
-  // Log-sum-exp merge of the pieces of unit (bb, hg), held by wavefronts
-  // w0..w1, by the whole wavefront, 16 query heads at a time.  Pass 1:
-  // lanes (head, piece mod lph) load the partial maxima and sums (all in
-  // flight at once), reduce them per head and leave the weights
-  // exp2(m_s - M) / den in LDS.  Pass 2: lanes over (head, dim) accumulate
-  // the weighted partial rows with SB pieces of loads in flight.  Partials
-  // are read with agent-scope atomic loads (coherent across XCDs).
-  auto merge_unit = [&](int32_t bb, int32_t hg, int32_t w0, int32_t w1, int64_t u_first) {
-    const int32_t pieces = w1 - w0 + 1;  // <= 63
-    const int32_t qh0 = hg * HU;
-    for (int32_t hb = 0; hb < HU; hb += 16) {
-      const int32_t nh = min(16, HU - hb);
-      const int gp = nh <= 1 ? 1 : nh <= 2 ? 2 : nh <= 4 ? 4 : nh <= 8 ? 8 : 16;
-      const int lph = 64 / gp;  // lanes per head
-      const int g = lane / lph;
-      const int j = lane - g * lph;
-      const bool head_ok = g < nh;
-      constexpr int kItems = (16 * D + 63) / 64;
-      constexpr int SB = kItems >= 64 ? 1 : 64 / kItems;  // pieces of loads in flight
-      // Loads of the accumulators of pieces [s0, s0 + SB) (independent of the
-      // weights, so the first batch is issued together with pass 1).
-      auto load_acc = [&](int32_t s0, float (&v)[SB][kItems]) {
-#pragma unroll
-        for (int sb = 0; sb < SB; ++sb) {
-          const int64_t base = piece_slot(w0 + min(s0 + sb, pieces - 1), u_first) * HU + hb;
-#pragma unroll
-          for (int k = 0; k < kItems; ++k) {
-            const int idx = lane + 64 * k;
-            const int gg = min(idx / D, nh - 1);
-            const int d = idx - (idx / D) * D;
-            v[sb][k] = __hip_atomic_load(p.partial_acc + (base + gg) * p.partial_stride + d,
-                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      };
-      float v[SB][kItems];
-      float pm[16], ps[16];
-      const int pass1 = min(16, (pieces + lph - 1) / lph);  // uniform
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        if (k >= pass1) break;
-        const int32_t sidx = j + k * lph;
-        const bool ok = head_ok && sidx < pieces;
-        const int64_t at = piece_slot(w0 + (ok ? sidx : 0), u_first) * HU + hb + (head_ok ? g : 0);
-        pm[k] = __hip_atomic_load(p.partial_max + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ps[k] = __hip_atomic_load(p.partial_sum + at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      load_acc(0, v);
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const int32_t sidx = j + k * lph;
-        if (k >= pass1 || !(head_ok && sidx < pieces)) {
-          pm[k] = kNegInf;
-          ps[k] = 0.f;
-        }
-      }
-      float mloc = kNegInf;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) mloc = fmaxf(mloc, pm[k]);
-      for (int off = lph >> 1; off > 0; off >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off, 64));
-      float dloc = 0.f;
-      if (mloc != kNegInf) {
-#pragma unroll
-        for (int k = 0; k < 16; ++k) dloc += ps[k] * fast_exp2(pm[k] - mloc);
-      }
-      for (int off = lph >> 1; off > 0; off >>= 1) dloc += __shfl_xor(dloc, off, 64);
-      const float inv = dloc > 0.f ? 1.f / dloc : 0.f;
-      __asm__ volatile("" ::: "memory");
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const int32_t sidx = j + k * lph;
-        if (head_ok && sidx < pieces)
-          weights[g * 64 + sidx] = mloc != kNegInf ? fast_exp2(pm[k] - mloc) * inv : 0.f;
-      }
-      __asm__ volatile("" ::: "memory");
-      float num[kItems];
-#pragma unroll
-      for (int k = 0; k < kItems; ++k) num[k] = 0.f;
-      for (int32_t s0 = 0; s0 < pieces; s0 += SB) {
-        if (s0 > 0) load_acc(s0, v);
-#pragma unroll
-        for (int sb = 0; sb < SB; ++sb) {
-          if (s0 + sb >= pieces) break;
-#pragma unroll
-          for (int k = 0; k < kItems; ++k) {
-            const int idx = lane + 64 * k;
-            const int gg = min(idx / D, nh - 1);
-            num[k] += weights[gg * 64 + s0 + sb] * v[sb][k];
-          }
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < kItems; ++k) {
-        const int idx = lane + 64 * k;
-        if (idx < nh * D) output_row<T>(p, bb, qh0 + hb + idx / D)[idx - (idx / D) * D] = from_float<T>(num[k]);
-      }
-      __asm__ volatile("" ::: "memory");
-    }
-  };
-
-  // ---- stream the range ------------------------------------------------------
-  // DEPTH register sets rotate: while one tile is computed the next
-  // DEPTH - 1 are in flight.  step() computes `cur` and closes its unit's
-  // piece when the following tile (`nxt`) belongs elsewhere -- unless the
-  // window ends inside the unit, which then continues in the next window.
-  // It returns true once the window is exhausted.  Windows (64 tiles) are
-  // reloaded outside the pipelined loop, so the loop itself carries no
-  // conditional loads and its waits stay partial.  The rotation is spelled
-  // out with constant set indices so the sets stay in registers.
-  static_assert(DEPTH >= 2 && DEPTH <= 4, "2..4 tiles in flight");
-  Set st[DEPTH];
-  auto step = [&](Set &cur, const Set &nxt) -> bool {
-    if (cur.unit < 0) return true;
-    compute(cur);
-    const bool continues = nxt.unit < 0 && cur.unit == cont_unit;
-    if (nxt.unit != cur.unit && !continues) flush(cur.unit);
-    return false;
-  };
-  while (true) {
-#pragma unroll
-    for (int i = 0; i < DEPTH - 1; ++i) issue(st[i]);
-    while (true) {
-      issue(st[DEPTH - 1]);
-      if (step(st[0], st[1 % DEPTH])) break;
-      issue(st[0]);
-      if (step(st[1], st[2 % DEPTH])) break;
-      if constexpr (DEPTH > 2) {
-        issue(st[1]);
-        if (step(st[2], st[3 % DEPTH])) break;
-      }
-      if constexpr (DEPTH > 3) {
-        issue(st[2]);
-        if (step(st[3], st[0])) break;
-      }
-    }
-    if (win + win_count >= range) break;
-    load_window(win + win_count);
-  }
-
-  // ---- count the partial pieces in; the last arrival merges its unit ----------
-  // Lanes 0 and 1 count this wavefront in for its first and last pending
-  // unit with one atomic instruction; the wavefront then merges each unit
-  // for which it arrived last.
-  if (pending_first < 0) return;
-  __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wavefront has completed
-  {
-    const int32_t my_unit = lane == 0 ? pending_first : (lane == 1 ? pending_last : -1);
-    int32_t arrived_last = 0;
-    if (my_unit >= 0) {
-      const int32_t bb = my_unit / NG;
-      const int64_t u_first = unit_start(my_unit);
-      const int32_t w0 = wave_of_tile(u_first, nw, total);
-      const int32_t w1 = wave_of_tile(u_first + (rstart[bb + 1] - rstart[bb]) - 1, nw, total);
-      const int32_t prev = __hip_atomic_fetch_add(p.split_counters + my_unit, 1, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-      arrived_last = prev == w1 - w0;
-      if (arrived_last)
-        __hip_atomic_store(p.split_counters + my_unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    const int32_t last0 = __builtin_amdgcn_readlane(arrived_last, 0);
-    const int32_t last1 = __builtin_amdgcn_readlane(arrived_last, 1);
-    for (int i = 0; i < 2; ++i) {
-      if ((i == 0 ? last0 : last1) == 0) continue;
-      const int32_t unit = i == 0 ? pending_first : pending_last;
-      const int32_t bb = unit / NG;
-      const int32_t hg = unit - bb * NG;
-      const int64_t u_first = unit_start(unit);
-      const int32_t w0 = wave_of_tile(u_first, nw, total);
-      const int32_t w1 = wave_of_tile(u_first + (rstart[bb + 1] - rstart[bb]) - 1, nw, total);
-      merge_unit(bb, hg, w0, w1, u_first);
-    }
-  }
-}
-
-// ===========================================================================
 // Generic kernel (fp32 math, LDS tiles)
 // ===========================================================================
 constexpr int kGenericThreads = 256;
@@ -2054,100 +1433,23 @@ int32_t make_params(AttnParams &p, const void *query, const void *key_cache,
   return TF_SUCCESS;
 }
 
-// Compute units of the current device (cached per device id).
-int32_t device_compute_units() {
-  static int32_t cached[64] = {0};
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess || device < 0) return 256;
-  if (device < 64 && cached[device] > 0) return cached[device];
-  int count = 0;
-  if (hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
-      count <= 0)
-    count = 256;
-  if (device < 64) cached[device] = count;
-  return count;
-}
-
-// Kv heads per streaming unit: 1 by default (measured as fast as grouping
-// and the lightest in registers); flag bits 20-23 may ask for 2 or 4 when
-// that divides kv_heads and HG * head_dim <= 256.
-int32_t stream_heads_per_group(int32_t kv_heads, int32_t head_dim, int32_t flags) {
-  const int32_t want = (flags >> TF_ATTENTION_HEADS_PER_WG_SHIFT) & 0xf;
-  if ((want == 2 || want == 4) && kv_heads % want == 0 && want * head_dim <= 256) return want;
-  return 1;
-}
-
-template <typename T, int D, int HG>
-void launch_stream_hg(const AttnParams &p, int32_t waves, int32_t depth, size_t lds,
-                      hipStream_t stream) {
-  // Deeper pipelines for the smaller register footprints.
-  constexpr int kMaxDepth = (D * HG <= 128) ? 4 : 2;
-  if (depth <= 2)
-    hipLaunchKernelGGL((paged_decode_stream_kernel<T, D, HG, 2>), dim3(waves), dim3(64), lds, stream, p);
-  else if (depth == 3 || kMaxDepth == 3)
-    hipLaunchKernelGGL((paged_decode_stream_kernel<T, D, HG, 3>), dim3(waves), dim3(64), lds, stream, p);
-  else
-    hipLaunchKernelGGL((paged_decode_stream_kernel<T, D, HG, kMaxDepth>), dim3(waves), dim3(64), lds, stream, p);
-}
-
-template <typename T, int D>
-void launch_stream_dim(const AttnParams &p, int32_t hg, int32_t waves, int32_t depth,
-                       hipStream_t stream) {
-  const size_t lds = stream_lds_bytes(D, hg, p.group, p.batch);
-  if (hg == 1) {
-    launch_stream_hg<T, D, 1>(p, waves, depth, lds, stream);
-  } else if (hg == 2 || D == 128) {
-    launch_stream_hg<T, D, 2>(p, waves, depth, lds, stream);
-  } else if constexpr (D < 128) {
-    launch_stream_hg<T, D, 4>(p, waves, depth, lds, stream);
-  }
-}
-
-int32_t default_stream_depth(int32_t head_dim, int32_t hg) { return head_dim * hg <= 128 ? 4 : 2; }
-
-template <typename T>
-void launch_stream(const AttnParams &p, int32_t hg, int32_t waves, int32_t depth,
-                   hipStream_t stream) {
-  switch (p.head_dim) {
-    case 32: launch_stream_dim<T, 32>(p, hg, waves, depth, stream); break;
-    case 64: launch_stream_dim<T, 64>(p, hg, waves, depth, stream); break;
-    default: launch_stream_dim<T, 128>(p, hg, waves, depth, stream); break;
-  }
-}
-
-// Fewest wavefronts the streaming kernel is used with: below this the
-// partial buffers are too small for it and the grid kernel runs instead.
-constexpr int64_t kStreamMinWaves = 64;
+// Flag bits with no meaning in this ABI (bit 2 once selected a streaming
+// kernel that has been removed, bits 16-19 its pipeline depth).
+constexpr int32_t kUnknownFlagBits = 0x2 | 0x4 | 0x8 | 0x40 | 0x80 | 0xF0000;
 
 int32_t launch_split_stage(const AttnParams &p, int32_t dtype, int32_t flags, hipStream_t stream) {
+  if (flags & kUnknownFlagBits)
+    return fail(TF_ERROR_UNSUPPORTED, "unknown attention flag bits");
   if (p.batch == 0) return TF_SUCCESS;
   const bool balanced = (flags & TF_ATTENTION_FLAG_BALANCED) != 0;
   if (balanced &&
       (choose_variant(dtype, p.head_dim, p.group, p.block_size, flags) != TF_ATTENTION_MFMA ||
-       (flags & (TF_ATTENTION_FLAG_STREAM | TF_ATTENTION_FLAG_VALU)) || p.num_splits <= p.batch ||
+       (flags & TF_ATTENTION_FLAG_VALU) || p.num_splits <= p.batch ||
        p.batch > 64 || p.split_counters != nullptr || p.split_size % 32 != 0))
     return fail(TF_ERROR_UNSUPPORTED,
                 "balanced partitions need the MFMA grid kernel in split-KV mode with the merge "
-                "launch (no arrival counters, no STREAM or VALU flag), num_splits > batch, "
+                "launch (no arrival counters, no VALU flag), num_splits > batch, "
                 "batch <= 64 and split_size % 32 == 0");
-  {
-    const int32_t variant = choose_variant(dtype, p.head_dim, p.group, p.block_size, flags);
-    const int32_t hg = stream_heads_per_group(p.kv_heads, p.head_dim, flags);
-    if (variant == TF_ATTENTION_MFMA && (flags & TF_ATTENTION_FLAG_STREAM) && p.num_splits >= 2 &&
-        p.split_counters != nullptr && p.batch <= kStreamMaxRows &&
-        p.partial_rows / (2 * static_cast<int64_t>(hg) * p.group) >= kStreamMinWaves) {
-      int32_t per_cu = (flags >> TF_ATTENTION_WAVES_PER_CU_SHIFT) & 0xff;
-      if (per_cu == 0) per_cu = kStreamWavesPerCu;
-      const int32_t waves = device_compute_units() * per_cu;
-      int32_t depth = (flags >> TF_ATTENTION_DEPTH_SHIFT) & 0xf;
-      if (depth == 0) depth = default_stream_depth(p.head_dim, hg);
-      if (dtype == TF_DTYPE_BFLOAT16)
-        launch_stream<__bf16>(p, hg, waves, depth, stream);
-      else
-        launch_stream<_Float16>(p, hg, waves, depth, stream);
-      return check_launch("paged_gqa_decode (stream)");
-    }
-  }
   const dim3 grid(static_cast<unsigned>(p.batch) * static_cast<unsigned>(p.kv_heads),
                   static_cast<unsigned>(p.num_splits));
   int32_t variant = choose_variant(dtype, p.head_dim, p.group, p.block_size, flags);
@@ -2285,7 +1587,7 @@ extern "C" int32_t tf_paged_gqa_decode_rope_append(
     return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
   if (choose_variant(dtype, head_dim, query_heads / (kv_heads > 0 ? kv_heads : 1), block_size,
                      flags) != TF_ATTENTION_MFMA ||
-      (flags & TF_ATTENTION_FLAG_STREAM) || (num_splits > 1 && split_size % 32 != 0))
+      (num_splits > 1 && split_size % 32 != 0))
     return fail(TF_ERROR_UNSUPPORTED,
                 "fused RoPE + append attention needs the MFMA grid kernel (bf16/fp16, head_dim "
                 "32/64/128, group <= 16, block_size % 16 == 0, split_size % 32 == 0)");
@@ -2381,7 +1683,7 @@ extern "C" int32_t tf_paged_gqa_decode_merge(
 // the first call there, and only that address is passed to kernels.  The
 // split kernel writes every partial the merge reads (empty splits are never
 // read), so nothing in `scratch` has to start at zero; arrival counters are
-// not used (no in-kernel merge, no STREAM flag).  Every call on a GPU shares
+// not used (no in-kernel merge).  Every call on a GPU shares
 // that GPU's array: calls that overlap in time on one GPU race.
 
 static __device__ __align__(256) unsigned char scratch[TF_NOALLOC_SCRATCH_BYTES];
@@ -2428,9 +1730,7 @@ extern "C" int32_t tf_paged_gqa_decode_noalloc(
     int32_t dtype, int32_t flags, void *stream) {
   using namespace tf;
   clear_error();
-  if (flags & TF_ATTENTION_FLAG_STREAM)
-    return fail(TF_ERROR_UNSUPPORTED,
-                "the no-allocation attention call has no arrival counters (no STREAM flag)");
+  if (flags & kUnknownFlagBits) return fail(TF_ERROR_UNSUPPORTED, "unknown attention flag bits");
   if (batch < 0 || query_heads <= 0 || head_dim <= 0 || head_dim > 256 || num_splits <= 0)
     return fail(TF_ERROR_INVALID_ARGUMENT, "attention dimensions out of range");
   // Partials as the workspace lays them out: accumulator rows of

@@ -74,9 +74,9 @@ def test_library_exports_every_declared_symbol(lib) -> None:
 
 def test_header_constants_match_the_python_binding() -> None:
     text = HEADER.read_text()
-    for name in ("TF_ATTENTION_FLAG_FORCE_GENERIC", "TF_ATTENTION_FLAG_STREAM",
+    for name in ("TF_ATTENTION_FLAG_FORCE_GENERIC",
                  "TF_ATTENTION_FLAG_VALU", "TF_ATTENTION_FLAG_BALANCED",
-                 "TF_ATTENTION_WAVES_PER_CU_SHIFT", "TF_ATTENTION_DEPTH_SHIFT",
+                 "TF_ATTENTION_WAVES_PER_CU_SHIFT",
                  "TF_ATTENTION_HEADS_PER_WG_SHIFT", "TF_ATTENTION_TOKENS_PER_WAVE_SHIFT"):
         match = re.search(rf"#define {name} (\d+)", text)
         assert match and int(match.group(1)) == getattr(_native, name), name
@@ -87,7 +87,7 @@ def test_header_constants_match_the_python_binding() -> None:
 
 
 def test_abi_version_and_variant_selection(lib) -> None:
-    assert lib.tf_abi_version() == 12
+    assert lib.tf_abi_version() == 13
     variant = lib.tf_paged_gqa_decode_variant
     bf16, f16, f32 = (_native.TF_DTYPE_BFLOAT16, _native.TF_DTYPE_FLOAT16,
                       _native.TF_DTYPE_FLOAT32)
@@ -373,16 +373,18 @@ def test_bench_refuses_more_than_one_gpu() -> None:
 def test_noalloc_attention_rejects_what_its_scratch_cannot_hold(lib) -> None:
     """The size checks of tf_paged_gqa_decode_noalloc come before any HIP
     call: 4 rows x 32 heads x 2048 splits of (64 + 2) floats exceed the
-    8 MiB array, and the STREAM flag needs counters the call does not have."""
+    8 MiB array, and flag bits with no meaning in this ABI (bit 2 once
+    selected a streaming kernel that has been removed) are rejected."""
 
     bf16 = _native.TF_DTYPE_BFLOAT16
     call = lib.tf_paged_gqa_decode_noalloc
     status = call(None, None, None, None, None, None, 4, 32, 4, 64, 10, 16, 64, 32, 2048,
                   0.125, bf16, 0, None)
     assert status == 1 and b"no-allocation scratch holds 8388608" in lib.tf_last_error()
-    status = call(None, None, None, None, None, None, 4, 32, 4, 64, 10, 16, 64, 32, 2, 0.125,
-                  bf16, _native.TF_ATTENTION_FLAG_STREAM, None)
-    assert status == 2 and b"no arrival counters" in lib.tf_last_error()
+    for bits in (4, 8, 2 << 16):
+        status = call(None, None, None, None, None, None, 4, 32, 4, 64, 10, 16, 64, 32, 2, 0.125,
+                      bf16, bits, None)
+        assert status == 2 and b"unknown attention flag bits" in lib.tf_last_error()
     assert _native.TF_NOALLOC_SCRATCH_BYTES == 8 << 20
 
 

@@ -327,7 +327,6 @@ def test_mfma_and_generic_kernels_agree_through_the_c_abi(device):
     outputs = {}
     for name, flags, counter_ptr in (
         ("mfma, merge kernel", 0, None),
-        ("mfma stream, in-kernel merge", _native.TF_ATTENTION_FLAG_STREAM, counters),
         ("mfma grid, in-kernel merge", 0, counters),
         ("generic, merge kernel", _native.TF_ATTENTION_FLAG_FORCE_GENERIC, None),
         ("generic, in-kernel merge", _native.TF_ATTENTION_FLAG_FORCE_GENERIC, counters),
@@ -340,8 +339,6 @@ def test_mfma_and_generic_kernels_agree_through_the_c_abi(device):
     assert int(workspace.split_counters.sum()) == 0, "arrival counters were not reset"
     assert_close(outputs["mfma, merge kernel"], outputs["generic, merge kernel"],
                  NORTH_STAR_ATOL, NORTH_STAR_RTOL, "mfma vs generic")
-    assert_close(outputs["mfma, merge kernel"], outputs["mfma stream, in-kernel merge"],
-                 1e-2, 1e-2, "merge kernel vs streaming kernel")
     assert_close(outputs["mfma, merge kernel"], outputs["mfma grid, in-kernel merge"],
                  1e-2, 1e-2, "merge kernel vs grid kernel with in-kernel merge")
 
@@ -472,48 +469,3 @@ def test_in_kernel_merge_is_fresh_on_every_call(device):
     assert int(workspace.split_counters.sum()) == 0
     case.query = queries[-1].cpu()
     _check_against_oracle(case, fused_out[-1].cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, "last call")
-
-
-@pytest.mark.parametrize("waves_per_cu", [1, 4, 8])
-def test_stream_kernel_long_ranges_cross_page_windows(device, waves_per_cu):
-    """Two partial slots per row force wavefront ranges of >= 2048 tiles:
-    the 64-tile page windows are reloaded and rows continue across them."""
-
-    lengths = [32768, 100, 5000, 0, 17]
-    case = make_decode_attention_case(
-        lengths, query_heads=8, kv_heads=2, head_dim=64, block_size=16, dtype=torch.bfloat16,
-        seed=9,
-    )
-    gpu = case.to(device)
-    workspace = PagedAttentionWorkspace.allocate(
-        batch_capacity=len(lengths), query_heads=8, head_dim=64, max_context_length=32768,
-        device=device,
-    )
-    out = torch.full_like(gpu.query, float("nan"))
-    flags = _native.TF_ATTENTION_FLAG_STREAM | (waves_per_cu << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
-    _raw_decode(gpu, out, flags, 16384, 2, workspace, workspace.split_counters.data_ptr())
-    torch.cuda.synchronize()
-    assert int(workspace.split_counters.sum()) == 0
-    _check_against_oracle(case, out.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL,
-                          f"stream kernel, {waves_per_cu} waves/CU")
-
-
-@pytest.mark.parametrize("head_dim", [32, 64, 128])
-@pytest.mark.parametrize("block_size", [16, 32, 48])
-def test_stream_kernel_head_dims_and_pages(device, head_dim, block_size):
-    lengths = [1, 16, 31, 33, 700, 64, 0, 1025]
-    case = make_decode_attention_case(
-        lengths, query_heads=16, kv_heads=4, head_dim=head_dim, block_size=block_size,
-        dtype=torch.float16, seed=head_dim + block_size,
-    )
-    gpu = case.to(device)
-    workspace = PagedAttentionWorkspace.allocate(
-        batch_capacity=len(lengths), query_heads=16, head_dim=head_dim,
-        max_context_length=1025, device=device,
-    )
-    output = torch.full_like(gpu.query, float("nan"))
-    _raw_decode(gpu, output, _native.TF_ATTENTION_FLAG_STREAM, 256, 5, workspace,
-                workspace.split_counters.data_ptr())
-    torch.cuda.synchronize()
-    assert int(workspace.split_counters.sum()) == 0
-    _check_against_oracle(case, output.cpu(), 3e-3, 3e-3, f"D={head_dim} page={block_size}")

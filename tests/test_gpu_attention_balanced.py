@@ -263,6 +263,9 @@ def test_unsupported_combinations_are_rejected(device):
         status, _ = _call(gpu, out, flags, 256, splits, counters=ctr)
         assert status == UNSUPPORTED, what
         assert b"balanced partitions need" in _native.library().tf_last_error(), what
+    status, _ = _call(gpu, out, 4, 256, 8)  # bit 2: no meaning in this ABI
+    assert status == UNSUPPORTED
+    assert b"unknown attention flag bits" in _native.library().tf_last_error()
     many = make_decode_attention_case([40] * 65, query_heads=8, kv_heads=2, head_dim=64,
                                       block_size=16, dtype=torch.bfloat16, seed=2)
     gpu65 = many.to(device)
