@@ -537,6 +537,29 @@ __device__ __forceinline__ float dot8<_Float16>(_Float16 __attribute__((ext_vect
                                 __builtin_shufflevector(b, b, 6, 7), c, false);
 }
 
+// Max / sum over the 16 lanes of a DPP row (every lane gets the result):
+// quad_perm [1,0,3,2] and [2,3,0,1] combine within quads, row_half_mirror
+// (lane i <-> 7 - i of each half row) pairs the two quads of a half row and
+// row_mirror (i <-> 15 - i) the two halves -- in-register lane moves instead
+// of LDS-routed shuffles.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_move<0xb1>(v));
+  v = fmaxf(v, dpp_move<0x4e>(v));
+  v = fmaxf(v, dpp_move<0x141>(v));
+  return fmaxf(v, dpp_move<0x140>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_move<0xb1>(v);
+  v += dpp_move<0x4e>(v);
+  v += dpp_move<0x141>(v);
+  return v + dpp_move<0x140>(v);
+}
+
 // Wave-level layout of one 32-token chunk (tiles j = 0, 1 of 16 tokens):
 //   loads    LINES: lane holds bytes [16 (lane % (D/8)), +16) of the K / V
 //            slice of token 16j + lane / (D/8) + (512/D) ks (whole token
@@ -660,16 +683,20 @@ paged_decode_mfma_kernel(AttnParams p) {
     }
   }
   if constexpr (!ROPE) page_win = load_window(0);
-  // VALU form: the whole query row of head l16 (zeros for l16 >= group).
-  vec8 qv[VALU ? D / 8 : 1];
+  // VALU form (head_dim 64, group <= 8): lane (t16, qd) holds dims
+  // [16 qd, 16 qd + 16) of every query head of the group (zeros past it).
+  constexpr int kValuHeads = 8;
+  vec8 qq[VALU ? kValuHeads : 1][2];
   if constexpr (VALU) {
-    const bool own = l16 < p.group;
-    const T *qrow = static_cast<const T *>(p.query) +
-                    (static_cast<int64_t>(b) * p.query_heads + static_cast<int64_t>(kvh) * p.group +
-                     (own ? l16 : 0)) * D;
+    const T *qgroup = static_cast<const T *>(p.query) +
+                      (static_cast<int64_t>(b) * p.query_heads +
+                       static_cast<int64_t>(kvh) * p.group) * D + 16 * q4;
 #pragma unroll
-    for (int c = 0; c < D / 8; ++c)
-      qv[c] = own ? *reinterpret_cast<const vec8 *>(qrow + 8 * c) : vec8{};
+    for (int h = 0; h < kValuHeads; ++h) {
+      const bool own = h < p.group;
+      qq[h][0] = own ? *reinterpret_cast<const vec8 *>(qgroup + h * D) : vec8{};
+      qq[h][1] = own ? *reinterpret_cast<const vec8 *>(qgroup + h * D + 8) : vec8{};
+    }
   }
 
   if (s0 >= ctx) {
@@ -736,6 +763,20 @@ paged_decode_mfma_kernel(AttnParams p) {
   float m_run = kNegInf;  // reference max of head l16 (base 2, scaled)
   float l_run = 0.f;      // lane-partial sum of head l16
   unsigned char *vt = lds + wave * kChunk * kRow;
+  // VALU form state: per head h of the group the reference max and sum
+  // (the same on every lane) and the accumulator of output dimension `lane`.
+  float vm[VALU ? kValuHeads : 1], vl[VALU ? kValuHeads : 1], vacc[VALU ? kValuHeads : 1];
+#pragma unroll
+  for (int h = 0; h < (VALU ? kValuHeads : 1); ++h) {
+    vm[h] = kNegInf;
+    vl[h] = 0.f;
+    vacc[h] = 0.f;
+  }
+  // The wavefront's VALU slice: P as [32 tokens][8 heads] floats, at the end
+  // the accumulators as [8 heads][64 dims].
+  float *vslice = VALU ? reinterpret_cast<float *>(lds + mfma_lds_bytes(D, blockDim.x >> 6)) +
+                             wave * kValuHeads * 64
+                       : nullptr;
 
   // Issue the K/V loads of segment-relative chunk c (valid or not: absent
   // tokens and chunks past the end read a stand-in row, so every load is
@@ -770,6 +811,109 @@ paged_decode_mfma_kernel(AttnParams p) {
     }
   };
 
+  // VALU form of one chunk, K staged token-major in vt.  Scores: lane
+  // (t16, qd) takes token 16j + t16 and dims [16 qd, +16) of every head
+  // (packed two-element dot products), summed over the four dimension
+  // quarters by two cross-lane adds.  Per-head online softmax with the same
+  // lazy rescale as the MFMA form; P (rounded to T, as the MFMA form feeds
+  // it) goes through the wavefront's slice as [token][head], and P.V runs
+  // with lane = output dimension: one conversion per V element and G fp32
+  // FMAs per token.
+  auto valu_chunk = [&](vec8(&vf)[2][KS], const uint32_t(&valid)[2]) {
+    const bool wide = p.group > 4;  // uniform: heads 4..7 in use
+    float sj[2][kValuHeads];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const unsigned char *krow = vt + (16 * j + l16) * kRow + 32 * q4;
+      const vec8 k0 = *reinterpret_cast<const vec8 *>(krow);
+      const vec8 k1 = *reinterpret_cast<const vec8 *>(krow + 16);
+      const bool present = (valid[j] >> l16) & 1u;
+#pragma unroll
+      for (int h = 0; h < kValuHeads; ++h) {
+        float d = 0.f;
+        if (h < 4 || wide) d = dot8<T>(qq[h][1], k1, dot8<T>(qq[h][0], k0, 0.f));
+        d += __shfl_xor(d, 16, 64);
+        d += __shfl_xor(d, 32, 64);
+        sj[j][h] = present ? d : kNegInf;
+      }
+    }
+    float cm[kValuHeads];
+#pragma unroll
+    for (int h = 0; h < kValuHeads; ++h) {
+      cm[h] = row16_max(fmaxf(sj[0][h], sj[1][h])) * p.scale_log2;  // scale > 0 commutes with max
+    }
+    if (cm[0] == kNegInf) return;  // uniform: no token of the chunk is present
+    bool raise = false;
+#pragma unroll
+    for (int h = 0; h < kValuHeads; ++h) raise |= cm[h] > vm[h] + kRescaleThreshold;
+    if (raise) {  // uniform
+#pragma unroll
+      for (int h = 0; h < kValuHeads; ++h) {
+        const float mn = fmaxf(vm[h], cm[h]);
+        const float alpha = fast_exp2(vm[h] - mn);
+        vm[h] = mn;
+        vl[h] *= alpha;
+        vacc[h] *= alpha;
+      }
+    }
+    float pj[2][kValuHeads];
+#pragma unroll
+    for (int h = 0; h < kValuHeads; ++h) {
+      float ps = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float pr = fast_exp2(__builtin_fmaf(sj[j][h], p.scale_log2, -vm[h]));
+        ps += pr;
+        pj[j][h] = to_float(from_float<T>(pr));
+      }
+      vl[h] += row16_sum(ps);
+    }
+    __asm__ volatile("" ::: "memory");
+    if (q4 == 0) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float *dst = vslice + (16 * j + l16) * kValuHeads;
+        *reinterpret_cast<f32x4 *>(dst) = f32x4{pj[j][0], pj[j][1], pj[j][2], pj[j][3]};
+        *reinterpret_cast<f32x4 *>(dst + 4) = f32x4{pj[j][4], pj[j][5], pj[j][6], pj[j][7]};
+      }
+    }
+    // V replaces K in the tile (the wavefront's LDS requests are served in
+    // order); stand-in rows of absent tokens are cleared so that
+    // 0 * (non-finite) cannot leak into the accumulators.
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bool mine = (valid[j] >> (v_tok + kVTokens * ks)) & 1u;
+        *reinterpret_cast<vec8 *>(vt + (16 * j + v_tok + kVTokens * ks) * kRow + v_piece) =
+            mine ? vf[j][ks] : vec8{};
+      }
+    __asm__ volatile("" ::: "memory");
+    const unsigned char *vcol = vt + 2 * lane;
+    if (wide) {
+#pragma unroll 8
+      for (int t = 0; t < kChunk; ++t) {
+        const f32x4 p0 = *reinterpret_cast<const f32x4 *>(vslice + t * kValuHeads);
+        const f32x4 p1 = *reinterpret_cast<const f32x4 *>(vslice + t * kValuHeads + 4);
+        const float v = to_float(*reinterpret_cast<const T *>(vcol + t * kRow));
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          vacc[h] = __builtin_fmaf(p0[h], v, vacc[h]);
+          vacc[4 + h] = __builtin_fmaf(p1[h], v, vacc[4 + h]);
+        }
+      }
+    } else {
+#pragma unroll 8
+      for (int t = 0; t < kChunk; ++t) {
+        const f32x4 p0 = *reinterpret_cast<const f32x4 *>(vslice + t * kValuHeads);
+        const float v = to_float(*reinterpret_cast<const T *>(vcol + t * kRow));
+#pragma unroll
+        for (int h = 0; h < 4; ++h) vacc[h] = __builtin_fmaf(p0[h], v, vacc[h]);
+      }
+    }
+    __asm__ volatile("" ::: "memory");
+  };
+
   auto compute = [&](vec8(&kf)[2][KS], vec8(&vf)[2][KS], const uint32_t(&valid)[2]) {
     if constexpr (LINES) {
       // Stage K token-major in the wavefront's LDS tile and read it back in
@@ -782,41 +926,26 @@ paged_decode_mfma_kernel(AttnParams p) {
         for (int ks = 0; ks < KS; ++ks)
           *reinterpret_cast<vec8 *>(vt + (16 * j + v_tok + kVTokens * ks) * kRow + v_piece) = kf[j][ks];
       __asm__ volatile("" ::: "memory");
-      if constexpr (!VALU) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int ks = 0; ks < KS; ++ks)
-            kf[j][ks] =
-                *reinterpret_cast<const vec8 *>(vt + (16 * j + l16) * kRow + (32 * ks + 8 * q4) * 2);
-        __asm__ volatile("" ::: "memory");
+      if constexpr (VALU) {
+        valu_chunk(vf, valid);
+        return;
       }
-    }
-    float sc[8];  // raw q.k of token 16j + 4q4 + r, head l16
-    if constexpr (VALU) {
-      // Packed two-element dot products of the whole query row against the
-      // staged K rows of the lane's 8 tokens (v_dot2_f32_{bf16,f16}).
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const unsigned char *krow = vt + (16 * j + 4 * q4 + r) * kRow;
-          float dot = 0.f;
-#pragma unroll
-          for (int c = 0; c < D / 8; ++c)
-            dot = dot8<T>(qv[c], *reinterpret_cast<const vec8 *>(krow + 16 * c), dot);
-          sc[4 * j + r] = dot;
-        }
+        for (int ks = 0; ks < KS; ++ks)
+          kf[j][ks] =
+              *reinterpret_cast<const vec8 *>(vt + (16 * j + l16) * kRow + (32 * ks + 8 * q4) * 2);
       __asm__ volatile("" ::: "memory");
-    } else {
+    }
+    float sc[8];  // raw q.k of token 16j + 4q4 + r, head l16
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; ++j) {
+      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) s = M::mma(kf[j][ks], qf[ks], s);
+      for (int ks = 0; ks < KS; ++ks) s = M::mma(kf[j][ks], qf[ks], s);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[4 * j + r] = s[r];
-      }
+      for (int r = 0; r < 4; ++r) sc[4 * j + r] = s[r];
     }
     if ((valid[0] & valid[1]) != 0xffffu) {  // uniform: partial chunk
 #pragma unroll
@@ -873,33 +1002,7 @@ paged_decode_mfma_kernel(AttnParams p) {
             vt + (LINES ? (16 * j + v_tok + kVTokens * ks) * kRow + v_piece
                         : (16 * j + l16) * kRow + (32 * ks + 8 * q4) * 2)) = vf[j][ks];
     __asm__ volatile("" ::: "memory");
-    if constexpr (VALU) {
-      // P of head l16 for all 32 tokens through the wavefront's LDS slice
-      // (the weights rounded to T, as the MFMA form feeds them), then
-      // acc[n][r] += p[t] * V[t][16n + 4q4 + r] with fp32 FMAs.
-      float *pb = reinterpret_cast<float *>(lds + mfma_lds_bytes(D, blockDim.x >> 6)) +
-                  wave * 16 * kChunk + l16 * kChunk;
-      *reinterpret_cast<f32x4 *>(pb + 4 * q4) =
-          f32x4{to_float(pf[0]), to_float(pf[1]), to_float(pf[2]), to_float(pf[3])};
-      *reinterpret_cast<f32x4 *>(pb + 16 + 4 * q4) =
-          f32x4{to_float(pf[4]), to_float(pf[5]), to_float(pf[6]), to_float(pf[7])};
-      __asm__ volatile("" ::: "memory");
-#pragma unroll
-      for (int t4 = 0; t4 < kChunk; t4 += 4) {
-        const f32x4 pt = *reinterpret_cast<const f32x4 *>(pb + t4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const unsigned char *vrow = vt + (t4 + e) * kRow + 8 * q4;
-#pragma unroll
-          for (int n = 0; n < NB; ++n) {
-            typedef T t4v __attribute__((ext_vector_type(4)));
-            const t4v v = *reinterpret_cast<const t4v *>(vrow + 32 * n);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[n][r] = __builtin_fmaf(pt[e], to_float(v[r]), acc[n][r]);
-          }
-        }
-      }
-    } else {
+    {
       const unsigned char *rd = vt + (4 * q4 + (l16 >> 2)) * kRow + (l16 & 3) * 8;
 #pragma unroll
       for (int n = 0; n < NB; ++n) {
@@ -935,6 +1038,30 @@ paged_decode_mfma_kernel(AttnParams p) {
       load_kv(seg_first_tile, seg_s0, seg_s1, chunk(i + 2), ka, va, vala);
       compute(kb, vb, valb);
     }
+  }
+
+  if constexpr (VALU) {
+    // Into the MFMA form's lane layout (head l16, dims 16n + 4q4 + r, the
+    // sum of head l16 on its q4 = 0 lane) through the slice, for the shared
+    // combine and epilogue; lanes of heads past the group are never stored.
+    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int h = 0; h < kValuHeads; ++h) vslice[h * 64 + lane] = vacc[h];
+    __asm__ volatile("" ::: "memory");
+    const bool own = l16 < kValuHeads;
+    const int hh = own ? l16 : 0;
+#pragma unroll
+    for (int n = 0; n < NB; ++n)
+      acc[n] = own ? *reinterpret_cast<const f32x4 *>(vslice + hh * 64 + 16 * n + 4 * q4)
+                   : f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = vm[0], l = vl[0];
+#pragma unroll
+    for (int h = 1; h < kValuHeads; ++h) {
+      m = hh == h ? vm[h] : m;
+      l = hh == h ? vl[h] : l;
+    }
+    m_run = m;
+    l_run = own && q4 == 0 ? l : 0.f;
   }
 
   // Lane-partial sums -> per-head sums within the wave.
