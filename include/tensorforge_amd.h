@@ -480,9 +480,9 @@ int32_t tf_linear_partials_sum(const float *partials, int32_t splits, int32_t m,
  *   q [T, query_heads * head_dim], k and v [T, kv_heads * head_dim] (row
  *   strides in elements), output [T, query_heads * head_dim].
  * tiles [num_tiles][3] int32: (first query token i0, prompt start s, prompt
- * end e) of each 16-token query tile, s <= i0 < e, i0 - s a multiple of 16;
- * the tile's tokens [i0, min(i0 + 16, e)) attend to [s, token] of their
- * prompt.  Heaviest tiles first runs best.  fp16/bf16, head_dim 32/64/128,
+ * end e) of each 64-token query block, s <= i0 < e, i0 - s a multiple of 64;
+ * the block's tokens [i0, min(i0 + 64, e)) attend to [s, token] of their
+ * prompt.  Heaviest blocks first runs best.  fp16/bf16, head_dim 32/64/128,
  * groups of 1..16 query heads per kv head; heads_per_wave (0: default)
  * picks how many of a group's heads one wavefront serves.  Replaces the
  * masked SDPA of prefill (runtime/prefill.py:84-88, 109-118).

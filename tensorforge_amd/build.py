@@ -40,6 +40,14 @@ DEVICE_FLAGS = (
 )
 
 
+# Translation units whose MFMA accumulators the compiler otherwise keeps in
+# AGPRs and copies to VGPRs around every VALU use (the online softmax's
+# rescale, the split-K epilogue): the VGPR form of the MFMA instructions
+# (gfx950 reads and writes C/D in VGPRs) removes those copies.
+VGPR_MFMA_SOURCES = {"tf_prefill_attention.hip", "tf_linear_splitk.hip"}
+VGPR_MFMA_FLAGS = ("-mllvm", "-amdgpu-mfma-vgpr-form")
+
+
 def hipcc() -> str:
     candidate = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(candidate).exists():
@@ -49,7 +57,8 @@ def hipcc() -> str:
 
 def _compile(source: Path, compiler: str) -> Path:
     obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [compiler, *DEVICE_FLAGS, "-c", str(source), "-o", str(obj)]
+    extra = VGPR_MFMA_FLAGS if source.name in VGPR_MFMA_SOURCES else ()
+    cmd = [compiler, *DEVICE_FLAGS, *extra, "-c", str(source), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"hipcc failed for {source.name}:\n{result.stderr}")

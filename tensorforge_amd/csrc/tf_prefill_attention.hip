@@ -3,29 +3,34 @@
 // The prompts of a prefill batch are packed into one token stream with no
 // padding: token rows q [T, Hq * D], k [T, Hkv * D], v [T, Hkv * D] (row
 // strides in elements, so v can be a column slice of the fused QKV rows).
-// A work item is a 16-token query tile of one prompt: its tokens
-// [i0, i0 + 16) attend causally to the prompt's tokens [s, min(i0 + 16, e)),
-// where [s, e) is the prompt's token range.  The host lists the tiles
-// (query start, prompt start, prompt end), heaviest first.
+// A work item is a 64-token query block of one prompt: its tokens
+// [b0, b0 + 64) attend causally to the prompt's tokens [s, min(b0 + 64, e)),
+// where [s, e) is the prompt's token range.  The host lists the blocks
+// (block start, prompt start, prompt end), heaviest first.
 //
-// One wavefront per (tile, kv head, group of QH query heads of that kv
-// head): each 32-token K/V chunk is read once for its QH heads.
+// One workgroup of four wavefronts per (block, kv head, group of QH query
+// heads of that kv head); wavefront w serves the block's 16-token tile
+// [b0 + 16 w, +16) for the QH heads.  Each 32-token K/V chunk is loaded once
+// for the workgroup (whole rows, 16 bytes per thread) into one of two LDS
+// buffers while the previous chunk is computed, so a chunk's bytes serve 64
+// query tokens x QH heads instead of the 16 x QH of a wavefront alone.
 //   scores  v_mfma_f32_16x16x32 with the K chunk (16 tokens x 32 dims per
-//           tile) as the A operand straight from memory and the head's
+//           tile, read from LDS in the A-operand layout) and the head's
 //           query tile as the B operand: lane (l16, q4), register r holds
 //           S[key token t0 + 16 j + 4 q4 + r][query token i0 + l16], so the
 //           online softmax of a query token is lane-local across q4 lanes;
 //   P.V     P converted to the storage type is already the B operand; V^T
-//           (A operand) is read from the chunk staged token-major in the
-//           wavefront's LDS with ds_read_b64_tr_b16, once per chunk for all
-//           QH heads.
+//           (A operand) is read from the chunk staged token-major with
+//           ds_read_b64_tr_b16, once per chunk for all QH heads.
 // Softmax in base 2 with a lazily raised running maximum (raised only when a
 // score exceeds it by more than 2^8), fp32 accumulation, one rounding of the
-// output.  Two chunks of loads are in flight.
-//
+// output.
+
 // Reference semantics: the causal scaled-dot-product attention of prefill,
 // tensorforge/runtime/prefill.py:84-88 (causal mask over the padded
 // prompts) and :109-118 (torch SDPA with enable_gqa), here without padding.
+#include <type_traits>
+
 #include "tf_common.hpp"
 
 namespace tf {
@@ -34,7 +39,9 @@ namespace {
 constexpr float kPrefillLog2e = 1.4426950408889634f;
 constexpr float kPrefillNegInf = -__builtin_huge_valf();
 constexpr float kPrefillRescale = 8.f;
-constexpr int kPrefillTile = 16;   // query tokens per work item
+constexpr int kPrefillTile = 16;   // query tokens per wavefront
+constexpr int kPrefillWaves = 4;   // wavefronts per workgroup
+constexpr int kPrefillBlock = kPrefillTile * kPrefillWaves;  // query tokens per work item
 constexpr int kPrefillChunk = 32;  // key tokens per step
 
 template <typename T>
@@ -80,25 +87,43 @@ template <int D>
 constexpr int prefill_row_bytes() { return D * 2 + 16; }
 
 template <typename T, int D, int QH>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(64 * kPrefillWaves)
 prefill_attention_kernel(PrefillParams p) {
   using M = PrefillMfma<T>;
   using vec8 = typename M::vec8;
   constexpr int KS = D / 32;
   constexpr int NB = D / 16;
-  constexpr int kRow = prefill_row_bytes<D>();
-  __shared__ __attribute__((aligned(16))) unsigned char vt[kPrefillChunk * kRow];
+  constexpr int kRow = prefill_row_bytes<D>();  // V rows (padded for the transpose reads)
+  // K rows are 2 D bytes with their 16-byte pieces permuted: piece p of row r
+  // sits at p ^ ((r / R) % P), P = D / 8 pieces per row, R = 128 / D rows
+  // per 256 bytes (1 at D 128), so the 16 lanes of an A-operand read (rows
+  // 16 j .. +15, one piece each) and the 16 threads of a staging store
+  // cover the 64 banks once.
+  constexpr int kPieces = D / 8;
+  constexpr int kRowsPer256 = D >= 128 ? 1 : 128 / D;
+  constexpr int kRowK = 2 * D;
+  __shared__ __attribute__((aligned(16))) unsigned char k_lds[2][kPrefillChunk * kRowK];
+  __shared__ __attribute__((aligned(16))) unsigned char v_lds[2][kPrefillChunk * kRow];
+  auto k_offset = [](int row, int piece) {
+    return row * kRowK + 16 * (piece ^ ((row / kRowsPer256) & (kPieces - 1)));
+  };
 
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int l16 = lane & 15;
   const int q4 = lane >> 4;
   const int32_t *tile = p.tiles + 3 * static_cast<int64_t>(blockIdx.x);
-  const int32_t i0 = tile[0];
+  const int32_t b0 = tile[0];
   const int32_t s = tile[1];
   const int32_t e = tile[2];
   const int32_t groups = p.group / QH;
   const int32_t kvh = blockIdx.y / groups;
   const int32_t h0 = kvh * p.group + (blockIdx.y - kvh * groups) * QH;
+  // Keys of the block [s, kend_blk); this wavefront's tile [i0, i0 + 16)
+  // needs [s, kend) (none when the tile starts past the prompt).
+  const int32_t kend_blk = min(b0 + kPrefillBlock, e);
+  const int32_t i0 = b0 + kPrefillTile * wave;
   const int32_t kend = min(i0 + kPrefillTile, e);
   const int32_t qt = i0 + l16;  // this lane's query token (column)
   const bool q_ok = qt < e;
@@ -128,47 +153,66 @@ prefill_attention_kernel(PrefillParams p) {
 #pragma unroll
     for (int n = 0; n < NB; ++n) acc[hq][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  const int32_t nch = (kend - s + kPrefillChunk - 1) / kPrefillChunk;
+  const int32_t nch = (kend_blk - s + kPrefillChunk - 1) / kPrefillChunk;
+  const int32_t my_nch = i0 < e ? (kend - s + kPrefillChunk - 1) / kPrefillChunk : 0;
 
-  // K/V of chunk c (c >= nch: a masked stand-in chunk, so every load is
-  // unconditional).  Lane (l16, q4) of tile j holds token t0 + 16 j + l16.
-  auto load = [&](int32_t c, vec8(&kf)[2][KS], vec8(&vf)[2][KS]) {
+  // Staging: the workgroup loads a chunk's K and V rows whole (D / 8
+  // threads of 16 bytes per row) into one of two register sets, two chunks
+  // ahead of the one being computed, and stores them token-major into the
+  // chunk's buffer.  Rows past the block's keys read the prompt's first
+  // row: their V rows are stored as zeros (0 * p), their scores are masked.
+  constexpr int kLanesPerRow = D / 8;
+  constexpr int kRowsPerPass = 64 * kPrefillWaves / kLanesPerRow;
+  constexpr int kPasses = (kPrefillChunk + kRowsPerPass - 1) / kRowsPerPass;
+  const int srow = tid / kLanesPerRow;
+  const int spiece = tid - srow * kLanesPerRow;
+  vec8 kreg[2][kPasses], vreg[2][kPasses];  // register set c % 2 holds chunk c
+  // (the set is a compile-time index: the chunk loop is unrolled by two, so
+  // the sets stay in registers)
+  auto gload = [&](int32_t c, auto set_tag) {
+    constexpr int set = decltype(set_tag)::value;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int32_t t = s + kPrefillChunk * c + 16 * j + l16;
-      const int32_t row = (c < nch && t < kend) ? t : s;
-      const T *kr = kbase + static_cast<int64_t>(row) * p.k_stride + 8 * q4;
-      const T *vr = vbase + static_cast<int64_t>(row) * p.v_stride + 8 * q4;
+    for (int ps = 0; ps < kPasses; ++ps) {
+      const int row = srow + kRowsPerPass * ps;
+      const int32_t t = s + kPrefillChunk * c + row;
+      const int32_t src = (row < kPrefillChunk && t < kend_blk) ? t : s;
+      kreg[set][ps] = *reinterpret_cast<const vec8 *>(kbase + static_cast<int64_t>(src) * p.k_stride + 8 * spiece);
+      vreg[set][ps] = *reinterpret_cast<const vec8 *>(vbase + static_cast<int64_t>(src) * p.v_stride + 8 * spiece);
+    }
+  };
+  auto lstore = [&](int32_t c, auto set_tag) {
+    constexpr int set = decltype(set_tag)::value;
+    unsigned char *kdst = k_lds[set];
+    unsigned char *vdst = v_lds[set];
+    const bool tail = s + kPrefillChunk * (c + 1) > kend_blk;  // uniform
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        kf[j][ks] = *reinterpret_cast<const vec8 *>(kr + 32 * ks);
-        vf[j][ks] = *reinterpret_cast<const vec8 *>(vr + 32 * ks);
+    for (int ps = 0; ps < kPasses; ++ps) {
+      const int row = srow + kRowsPerPass * ps;
+      if (row < kPrefillChunk) {
+        *reinterpret_cast<vec8 *>(kdst + k_offset(row, spiece)) = kreg[set][ps];
+        vec8 v = vreg[set][ps];
+        if (tail && s + kPrefillChunk * c + row >= kend_blk) v = vec8{};
+        *reinterpret_cast<vec8 *>(vdst + row * kRow + 16 * spiece) = v;
       }
     }
   };
 
-  auto compute = [&](int32_t c, vec8(&kf)[2][KS], vec8(&vf)[2][KS]) {
+  auto compute = [&](int32_t c, int buf) {
     const int32_t t0 = s + kPrefillChunk * c;
-    // Tokens past kend read a stand-in row: zero their V rows.
-    const bool partial = t0 + kPrefillChunk > kend;
-    if (partial) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          vf[j][ks] = (t0 + 16 * j + l16 < kend) ? vf[j][ks] : vec8{};
-    }
-    // Stage V token-major and read V^T once for all heads.
-    __asm__ volatile("" ::: "memory");
+    const unsigned char *kb = k_lds[buf];
+    const unsigned char *vb = v_lds[buf];
+    // K in the A-operand layout: lane (l16, q4) of tile j holds token
+    // t0 + 16 j + l16, dims [32 ks + 8 q4, +8).
+    vec8 kf[2][KS];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        *reinterpret_cast<vec8 *>(vt + (16 * j + l16) * kRow + (32 * ks + 8 * q4) * 2) = vf[j][ks];
-    __asm__ volatile("" ::: "memory");
+        kf[j][ks] = *reinterpret_cast<const vec8 *>(kb + k_offset(16 * j + l16, 4 * ks + q4));
+    // V^T once for all heads.
     vec8 vtf[NB];
     {
-      const unsigned char *rd = vt + (4 * q4 + (l16 >> 2)) * kRow + (l16 & 3) * 8;
+      const unsigned char *rd = vb + (4 * q4 + (l16 >> 2)) * kRow + (l16 & 3) * 8;
 #pragma unroll
       for (int n = 0; n < NB; ++n) {
         const pf_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((pf_lds_i16x4 *)(rd + 32 * n));
@@ -177,10 +221,9 @@ prefill_attention_kernel(PrefillParams p) {
         vtf[n] = __builtin_bit_cast(vec8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
     }
-    __asm__ volatile("" ::: "memory");
     // Causal mask: needed when some key token of the chunk lies past the
-    // tile's first query token or past kend.
-    const bool masked = partial || t0 + kPrefillChunk - 1 > i0;
+    // tile's first query token or past the tile's keys.
+    const bool masked = t0 + kPrefillChunk > kend || t0 + kPrefillChunk - 1 > i0;
 #pragma unroll
     for (int hq = 0; hq < QH; ++hq) {
       float sc[8];
@@ -215,13 +258,14 @@ prefill_attention_kernel(PrefillParams p) {
 #pragma unroll
         for (int n = 0; n < NB; ++n) acc[hq][n] *= alpha;
       }
+      // m_run is finite here: every query column sees its prompt's first
+      // key (token s <= the query) in chunk 0, whose scores raise it from
+      // -inf; masked scores give weights exp2(-inf) = 0.
       vec8 pf;
       float psum = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float pr = m_run[hq] == kPrefillNegInf
-                             ? 0.f
-                             : __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], p.scale_log2, -m_run[hq]));
+        const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], p.scale_log2, -m_run[hq]));
         psum += pr;
         pf[i] = static_cast<T>(pr);
       }
@@ -231,14 +275,34 @@ prefill_attention_kernel(PrefillParams p) {
     }
   };
 
-  vec8 ka[2][KS], va[2][KS], kb[2][KS], vb[2][KS];
-  load(0, ka, va);
+  // Chunk c is computed from buffer c % 2 while the loads of chunks c + 1
+  // and c + 2 are in flight; after it, chunk c + 1 is stored into the other
+  // buffer (last read for chunk c - 1, before the previous barrier) and the
+  // loads of c + 3 are issued into the register set c + 1 freed.  One
+  // barrier per chunk publishes the stored buffer and retires the one just
+  // read.
+  using Set0 = std::integral_constant<int, 0>;
+  using Set1 = std::integral_constant<int, 1>;
+  gload(0, Set0{});
+  if (nch > 1) gload(1, Set1{});
+  lstore(0, Set0{});
+  if (nch > 2) gload(2, Set0{});
+  __syncthreads();
   for (int32_t c = 0; c < nch; c += 2) {
-    load(c + 1, kb, vb);
-    compute(c, ka, va);
+    // even chunk c: buffer and register set 0; then chunk c + 1 (set 1)
+    if (c < my_nch) compute(c, 0);  // wavefront-uniform
+    if (c + 1 < nch) {
+      lstore(c + 1, Set1{});
+      if (c + 3 < nch) gload(c + 3, Set1{});
+    }
+    __syncthreads();
     if (c + 1 >= nch) break;
-    load(c + 2, ka, va);
-    compute(c + 1, kb, vb);
+    if (c + 1 < my_nch) compute(c + 1, 1);
+    if (c + 2 < nch) {
+      lstore(c + 2, Set0{});
+      if (c + 4 < nch) gload(c + 4, Set0{});
+    }
+    __syncthreads();
   }
 
   // Lane-partial sums -> per-column sums; write the query tokens of the prompt.
@@ -265,16 +329,20 @@ template <typename T, int D, int QH>
 void launch_prefill(const PrefillParams &p, int32_t ntiles, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(ntiles),
                   static_cast<unsigned>(p.kv_heads * (p.group / QH)));
-  hipLaunchKernelGGL((prefill_attention_kernel<T, D, QH>), grid, dim3(64), 0, stream, p);
+  hipLaunchKernelGGL((prefill_attention_kernel<T, D, QH>), grid, dim3(64 * kPrefillWaves), 0,
+                     stream, p);
 }
 
 template <typename T, int D>
 void launch_prefill_qh(const PrefillParams &p, int32_t ntiles, int32_t heads_per_wave,
                        hipStream_t stream) {
   // Query heads per wavefront (a power of two dividing the group): as asked,
-  // else 4 (at most 4 at head_dim 128, for registers).
+  // else 2 at head_dim >= 64 and 1 at 32 (measured best on MI355X over a
+  // cfg5 batch of 19 prompts, 8,058 tokens: 97.5 / 102.1 / 111.8 us for 2 /
+  // 1 / 4 at D 64, 165 / 165 / 199 at D 128, 39.8 / 47.0 for 1 / 2 at D 32);
+  // at most 4 at head_dim 128, for registers.
   constexpr int kMax = D >= 128 ? 4 : 8;
-  int32_t qh = heads_per_wave > 0 ? heads_per_wave : 4;
+  int32_t qh = heads_per_wave > 0 ? heads_per_wave : (D >= 64 ? 2 : 1);
   if (qh > kMax) qh = kMax;
   if (qh > p.group) qh = p.group;
   switch (qh) {

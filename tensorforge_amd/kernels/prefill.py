@@ -4,7 +4,7 @@ Prefill packs the tokens of all admitted prompts into one stream with no
 padding.  ``prefill_attention`` attends every token causally within its own
 prompt in one launch, where the reference pads the prompts into one batch
 and runs a masked SDPA (tensorforge/runtime/prefill.py:84-88, 109-118).
-The work list -- 16-token query tiles, heaviest first -- is built on the
+The work list -- 64-token query blocks, heaviest first -- is built on the
 host from the prompt lengths once per prefill and reused by every layer.
 """
 
@@ -16,7 +16,7 @@ from torch import Tensor
 
 from tensorforge_amd import _native
 
-TILE = 16
+TILE = 64  # query tokens per work item (four wavefronts of 16)
 
 
 def prefill_attention_supported(dtype: torch.dtype, query_heads: int, kv_heads: int,
@@ -30,8 +30,8 @@ def prefill_attention_supported(dtype: torch.dtype, query_heads: int, kv_heads: 
 
 
 def prefill_tiles(lengths: list[int]) -> np.ndarray:
-    """[tiles, 3] int32 rows (first query token, prompt start, prompt end) of
-    the packed prompts' 16-token query tiles, most key tokens first."""
+    """[blocks, 3] int32 rows (first query token, prompt start, prompt end) of
+    the packed prompts' TILE-token query blocks, most key tokens first."""
 
     rows = []
     start = 0

@@ -5,18 +5,19 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from tensorforge_amd.kernels.prefill import prefill_attention_supported, prefill_tiles
+from tensorforge_amd.kernels.prefill import TILE, prefill_attention_supported, prefill_tiles
 
 
 def test_prefill_tiles_cover_every_token_once():
-    lengths = [1, 16, 17, 40]
+    assert TILE == 64  # the kernel's work item: four wavefronts of 16 query tokens
+    lengths = [1, 16, 17, 40, 64, 65, 200]
     tiles = prefill_tiles(lengths)
     covered = []
     for i0, s, e in tiles.tolist():
-        assert s <= i0 < e and (i0 - s) % 16 == 0
-        covered.extend(range(i0, min(i0 + 16, e)))
+        assert s <= i0 < e and (i0 - s) % TILE == 0
+        covered.extend(range(i0, min(i0 + TILE, e)))
     assert sorted(covered) == list(range(sum(lengths)))
-    work = np.minimum(tiles[:, 0] + 16, tiles[:, 2]) - tiles[:, 1]
+    work = np.minimum(tiles[:, 0] + TILE, tiles[:, 2]) - tiles[:, 1]
     assert (np.diff(work) <= 0).all()  # heaviest first
     with pytest.raises(ValueError):
         prefill_tiles([3, 0])
