@@ -321,12 +321,16 @@ linear_stream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restr
 // ---------------------------------------------------------------------------
 // K-split form of the weight stream for narrow weights (few 64-column tiles,
 // e.g. a 2560-row qkv projection) and for the gate|up + SwiGLU launch: a
-// workgroup owns 16 output columns over all of K and its four wavefronts
+// workgroup owns NT 16-column tiles over all of K and its four wavefronts
 // take a quarter of K each.  Every wavefront stages its own KC-wide k
 // chunks of x (16 MT rows) and of its weight rows in a private LDS region
 // with whole-row loads (KC / 8 lanes per row piece), so the x re-reads (once
-// per 16 columns) run at the L2 rate of whole-line loads, and the four
-// tiles meet once in LDS.
+// per workgroup) run at the L2 rate of whole-line loads, and the four
+// tiles meet once in LDS.  Each x operand read from LDS feeds NT (twice NT
+// for SwiGLU) products: two tiles halve the workgroups that re-read x, which
+// is what a 64-row call of a wide weight spends most on (TinyLlama's gate|up
+// at 64 rows: 18.4 -> 16.2 us on MI355X; with 2048-2560 columns one tile
+// keeps more workgroups streaming and stays faster).
 // ---------------------------------------------------------------------------
 // Chunk rows are KC * 2 bytes; pieces are permuted by (piece ^ (row & mask))
 // with mask = min(KC / 8, 16) - 1.
@@ -336,11 +340,11 @@ __device__ __forceinline__ int kstream_lds_offset(int row, int piece) {
   return row * KC + ((piece ^ (row & kMask)) << 3);
 }
 
-// SWIGLU: the workgroup's 16 columns j are activation columns; the weight
-// stacks gate rows [0, n) over up rows [n, 2n), each wavefront accumulates
-// both tiles over its quarter of K, and the output is
-// round(swiglu_act(round(g), round(u))).
-template <typename T, int MT, int KC, bool SWIGLU>
+// SWIGLU: the workgroup's 16 NT columns j are activation columns; the
+// weight stacks gate rows [0, n) over up rows [n, 2n), each wavefront
+// accumulates both tiles of every column tile over its quarter of K, and
+// the output is round(swiglu_act(round(g), round(u))).
+template <typename T, int MT, int KC, bool SWIGLU, int NT>
 __global__ void __launch_bounds__(256)
 linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restrict__ w,
                       int64_t w_stride, T *__restrict__ y, int64_t y_stride, int32_t m,
@@ -348,12 +352,18 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
   using M = SplitMma<T>;
   using vec8 = typename M::vec8;
   constexpr int XR = 16 * MT;
-  constexpr int WR = SWIGLU ? 32 : 16;
+  constexpr int CW = 16 * NT;                  // output columns per workgroup
+  constexpr int WR = SWIGLU ? 2 * CW : CW;     // weight rows per workgroup
   constexpr int kLanesPerRow = KC / 8;
   constexpr int kRowsPerLoad = 64 / kLanesPerRow;
   constexpr int kLoadsX = XR / kRowsPerLoad;
   constexpr int kLoadsW = WR / kRowsPerLoad;
   constexpr int kWaveElems = (XR + WR) * KC;
+  constexpr int kItems = MT * 4 * 64;          // floats of one 16-column tile
+  constexpr int kTiles = SWIGLU ? 2 : 1;
+  // The tile sums reuse the staging regions.
+  static_assert(4 * kTiles * NT * kItems * 4 <= 4 * kWaveElems * static_cast<int>(sizeof(T)),
+                "tile sums exceed the staging LDS");
   extern __shared__ __attribute__((aligned(16))) unsigned char kstream_smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -361,7 +371,7 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
   T *wl = xl + XR * KC;                                             // [WR][KC]
   const int l16 = lane & 15;
   const int q4 = lane >> 4;
-  const int32_t n0 = blockIdx.x * 16;
+  const int32_t n0 = blockIdx.x * CW;
   const int32_t k0 = min(wave * k_per_wave, k);
   const int32_t k1 = min(k0 + k_per_wave, k);
   const int lrow = lane / kLanesPerRow;  // staging: piece lane % (KC/8) of row R i + lane / (KC/8)
@@ -374,8 +384,8 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
   const T *wsrc[kLoadsW];
 #pragma unroll
   for (int i = 0; i < kLoadsW; ++i) {
-    const int tr = kRowsPerLoad * i + lrow;  // tile row
-    const int64_t row = SWIGLU ? (tr < 16 ? 0 : n) + min(n0 + (tr & 15), n - 1)
+    const int tr = kRowsPerLoad * i + lrow;  // tile row: gate rows [0, CW), then up rows
+    const int64_t row = SWIGLU ? (tr < CW ? 0 : n) + min(n0 + (tr % CW), n - 1)
                                : min(n0 + tr, n - 1);
     wsrc[i] = w + row * w_stride + 8 * lpiece;
   }
@@ -390,11 +400,15 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
 #pragma unroll
     for (int i = 0; i < kLoadsW; ++i) wr[i] = *reinterpret_cast<const vec8 *>(wsrc[i] + c);
   };
-  f32x4 acc[MT], accu[SWIGLU ? MT : 1];
+  f32x4 acc[MT][NT], accu[SWIGLU ? MT : 1][NT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-  for (int mt = 0; mt < (SWIGLU ? MT : 1); ++mt) accu[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ct = 0; ct < NT; ++ct) acc[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int mt = 0; mt < (SWIGLU ? MT : 1); ++mt)
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct) accu[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
   // The region is private to the wavefront, whose LDS requests are served in
   // order: compiler barriers order the stores, the operand reads and the
   // next chunk's stores.
@@ -412,57 +426,72 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
     for (int st = 0; st < KC / 32; ++st) {
       if (st >= steps) break;  // uniform
       const int piece = 4 * st + q4;
-      const vec8 b = *reinterpret_cast<const vec8 *>(wl + kstream_lds_offset<KC>(l16, piece));
-      vec8 bu;
-      if constexpr (SWIGLU)
-        bu = *reinterpret_cast<const vec8 *>(wl + kstream_lds_offset<KC>(16 + l16, piece));
+      vec8 b[NT], bu[NT];
+#pragma unroll
+      for (int ct = 0; ct < NT; ++ct) {
+        b[ct] = *reinterpret_cast<const vec8 *>(wl + kstream_lds_offset<KC>(16 * ct + l16, piece));
+        if constexpr (SWIGLU)
+          bu[ct] = *reinterpret_cast<const vec8 *>(wl + kstream_lds_offset<KC>(CW + 16 * ct + l16, piece));
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const vec8 a = *reinterpret_cast<const vec8 *>(xl + kstream_lds_offset<KC>(16 * mt + l16, piece));
-        acc[mt] = M::mma(a, b, acc[mt]);
-        if constexpr (SWIGLU) accu[mt] = M::mma(a, bu, accu[mt]);
+#pragma unroll
+        for (int ct = 0; ct < NT; ++ct) {
+          acc[mt][ct] = M::mma(a, b[ct], acc[mt][ct]);
+          if constexpr (SWIGLU) accu[mt][ct] = M::mma(a, bu[ct], accu[mt][ct]);
+        }
       }
     }
     __asm__ volatile("" ::: "memory");
   };
 
+  // Two chunks in flight.  Every iteration issues both register sets'
+  // loads, past the wavefront's last chunk re-reading that chunk (unused),
+  // so the loop head holds the same loads outstanding from the entry and
+  // from the back edge and each set is waited for alone; a load issued on
+  // only some paths would make the wait at the head drain both sets.
   if (k0 < k1) {
+    const int32_t last = k0 + ((k1 - k0 - 1) / KC) * KC;
     load_chunk(k0, xa, wa);
-    if (k0 + KC < k1) load_chunk(k0 + KC, xb, wb);
+    load_chunk(min(k0 + KC, last), xb, wb);
     for (int32_t kk = k0; kk < k1; kk += 2 * KC) {
       stage_compute(kk, xa, wa);
-      if (kk + 2 * KC < k1) load_chunk(kk + 2 * KC, xa, wa);
-      if (kk + KC >= k1) break;
-      stage_compute(kk + KC, xb, wb);
-      if (kk + 3 * KC < k1) load_chunk(kk + 3 * KC, xb, wb);
+      load_chunk(min(kk + 2 * KC, last), xa, wa);
+      stage_compute(kk + KC, xb, wb);  // no products past the range
+      load_chunk(min(kk + 3 * KC, last), xb, wb);
     }
   }
 
-  // Sum the four wavefront tiles: item (mt, r, lane) is y[16 mt + 4 q4 + r][n0 + l16].
-  constexpr int kItems = MT * 4 * 64;
-  constexpr int kTiles = SWIGLU ? 2 : 1;
+  // Sum the four wavefront tiles: item (mt, r, lane) of column tile ct is
+  // y[16 mt + 4 q4 + r][n0 + 16 ct + l16].
   __syncthreads();  // every wavefront's operand reads are done
-  float *tiles = reinterpret_cast<float *>(kstream_smem);  // [4 waves][kTiles][kItems]
+  float *tiles = reinterpret_cast<float *>(kstream_smem);  // [4 waves][kTiles][NT][kItems]
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int ct = 0; ct < NT; ++ct)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      tiles[(wave * kTiles) * kItems + (mt * 4 + r) * 64 + lane] = acc[mt][r];
-      if constexpr (SWIGLU) tiles[(wave * kTiles + 1) * kItems + (mt * 4 + r) * 64 + lane] = accu[mt][r];
-    }
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        tiles[((wave * kTiles) * NT + ct) * kItems + (mt * 4 + r) * 64 + lane] = acc[mt][ct][r];
+        if constexpr (SWIGLU)
+          tiles[((wave * kTiles + 1) * NT + ct) * kItems + (mt * 4 + r) * 64 + lane] = accu[mt][ct][r];
+      }
   __syncthreads();
-  for (int item = threadIdx.x; item < kItems; item += 256) {
+  for (int it = threadIdx.x; it < NT * kItems; it += 256) {
+    const int ct = it / kItems;
+    const int item = it - ct * kItems;
     float sum = 0.f, sumu = 0.f;
 #pragma unroll
     for (int wv = 0; wv < 4; ++wv) {
-      sum += tiles[(wv * kTiles) * kItems + item];
-      if constexpr (SWIGLU) sumu += tiles[(wv * kTiles + 1) * kItems + item];
+      sum += tiles[((wv * kTiles) * NT + ct) * kItems + item];
+      if constexpr (SWIGLU) sumu += tiles[((wv * kTiles + 1) * NT + ct) * kItems + item];
     }
     const int mt = item >> 8;
     const int r = (item >> 6) & 3;
     const int il = item & 63;
     const int32_t row = 16 * mt + 4 * (il >> 4) + r;
-    const int32_t col = n0 + (il & 15);
+    const int32_t col = n0 + 16 * ct + (il & 15);
     if (row >= m || col >= n) continue;
     T out;
     if constexpr (SWIGLU)
@@ -473,13 +502,13 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
   }
 }
 
-template <typename T, int MT, int KC, bool SWIGLU>
+template <typename T, int MT, int KC, bool SWIGLU, int NT>
 void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
                     int64_t y_stride, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
   const int32_t steps = k / 32;
   const int32_t k_per_wave = ((steps + 3) / 4) * 32;
   const size_t lds =
-      static_cast<size_t>(4) * (16 * MT + (SWIGLU ? 32 : 16)) * KC * sizeof(T);
+      static_cast<size_t>(4) * (16 * MT + (SWIGLU ? 32 : 16) * NT) * KC * sizeof(T);
   if (lds > 64 * 1024) {
     // Raise the kernel's dynamic LDS limit once per device (a failure shows
     // up as a launch error).
@@ -489,29 +518,41 @@ void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_st
     if (hipGetDevice(&device) == hipSuccess && device >= 0 && device < kMaxDevices &&
         !raised[device].load(std::memory_order_acquire)) {
       if (hipFuncSetAttribute(
-              reinterpret_cast<const void *>(&linear_kstream_kernel<T, MT, KC, SWIGLU>),
+              reinterpret_cast<const void *>(&linear_kstream_kernel<T, MT, KC, SWIGLU, NT>),
               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) == hipSuccess)
         raised[device].store(true, std::memory_order_release);
     }
   }
-  hipLaunchKernelGGL((linear_kstream_kernel<T, MT, KC, SWIGLU>), dim3((n + 15) / 16), dim3(256),
-                     lds, stream, static_cast<const T *>(x), x_stride, static_cast<const T *>(w),
-                     w_stride, static_cast<T *>(y), y_stride, m, n, k, k_per_wave);
+  hipLaunchKernelGGL((linear_kstream_kernel<T, MT, KC, SWIGLU, NT>),
+                     dim3((n + 16 * NT - 1) / (16 * NT)), dim3(256), lds, stream,
+                     static_cast<const T *>(x), x_stride, static_cast<const T *>(w), w_stride,
+                     static_cast<T *>(y), y_stride, m, n, k, k_per_wave);
 }
 
 // Chunk 128 for a plain projection (80 KB of LDS at 64 rows: one workgroup
 // per compute unit, enough for a 160-workgroup qkv), 64 for the SwiGLU form
-// (48 KB: several of its 352 TinyLlama workgroups share a compute unit).
+// (48 KB with one column tile: several of its workgroups share a compute
+// unit; 64 KB with two).  The SwiGLU form takes two column tiles when that
+// still gives >= 128 workgroups (>= 4096 activation columns).
 template <typename T, bool SWIGLU>
 void launch_kstream_mt(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
                        int64_t y_stride, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
   constexpr int KC = SWIGLU ? 64 : 128;
-  switch ((m + 15) / 16) {
-    case 1: launch_kstream<T, 1, KC, SWIGLU>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
-    case 2: launch_kstream<T, 2, KC, SWIGLU>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
-    case 3: launch_kstream<T, 3, KC, SWIGLU>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
-    default: launch_kstream<T, 4, KC, SWIGLU>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break;
+#define TF_KSTREAM_MT(NT)                                                                      \
+  switch ((m + 15) / 16) {                                                                     \
+    case 1: launch_kstream<T, 1, KC, SWIGLU, NT>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break; \
+    case 2: launch_kstream<T, 2, KC, SWIGLU, NT>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break; \
+    case 3: launch_kstream<T, 3, KC, SWIGLU, NT>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break; \
+    default: launch_kstream<T, 4, KC, SWIGLU, NT>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break; \
   }
+  if constexpr (SWIGLU) {
+    if (n >= 4096) {
+      TF_KSTREAM_MT(2)
+      return;
+    }
+  }
+  TF_KSTREAM_MT(1)
+#undef TF_KSTREAM_MT
 }
 
 template <typename T, int MT, bool SWIGLU>

@@ -182,11 +182,13 @@ def test_linear_kstream_matches_fp32(device, dtype, rows, n, k):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows", [1, 33, 64])
-@pytest.mark.parametrize(("inter", "k"), [(5632, 2048), (100, 800), (48, 96)])
+@pytest.mark.parametrize(("inter", "k"), [(5632, 2048), (4100, 256), (100, 800), (48, 96)])
 def test_linear_kswiglu_equals_kstream_then_activation(device, dtype, rows, inter, k):
     """The K-split gate|up + SwiGLU launch is bit-identical to linear_kstream
     of the stacked weight followed by swiglu_gate_up, and within the storage
-    bar of the fp32 reference."""
+    bar of the fp32 reference.  From 4096 activation columns a workgroup
+    takes two 16-column tiles (4100: the last workgroup holds 4 columns of
+    its first tile and none of its second)."""
 
     from tensorforge_amd.kernels import linear_kstream, linear_swiglu, swiglu_gate_up
 
