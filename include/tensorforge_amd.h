@@ -43,6 +43,8 @@
  *   tf_linear_swiglu         the MLP's gate|up projection with its SwiGLU
  *                            (model/layers.py:144-158)
  *   tf_prefill_attention     prefill's causal attention (runtime/prefill.py:84-88, 109-118)
+ *   tf_argmax_rows           greedy sampling, torch.argmax(logits, dim=-1)
+ *                            (scheduler/continuous.py:265-275)
  *   tf_hbm_read_probe        measurement only: the read-rate ceiling the attention
  *                            roofline is compared with (the reference measures
  *                            its ceiling with a device copy,
@@ -382,6 +384,17 @@ int32_t tf_swiglu(const void *gate, const void *up, void *output,
 int32_t tf_swiglu_rows(const void *gate_up, int64_t gate_up_row_stride,
                        void *output, int64_t output_row_stride, int64_t rows,
                        int32_t columns, int32_t dtype, void *stream);
+
+/*
+ * Greedy sampling: out[r] = argmax over c < columns of logits[r * row_stride
+ * + c] for r < rows (fp32, fp16 or bf16; out int64) -- torch.argmax(logits,
+ * dim=-1) as the continuous scheduler applies it to a step's logits
+ * (tensorforge/scheduler/continuous.py:265-275): the first index of the
+ * largest value, a NaN counting as larger than every number.  columns >= 1,
+ * row_stride >= columns (elements).
+ */
+int32_t tf_argmax_rows(const void *logits, int64_t row_stride, int32_t rows, int32_t columns,
+                       int32_t dtype, int64_t *out, void *stream);
 
 /*
  * Decode-shaped linear layer y[m, n] = x[m, k] . weight[n, k]^T (no bias),

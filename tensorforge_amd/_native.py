@@ -105,6 +105,7 @@ SIGNATURES: dict[str, tuple[Any, ...]] = {
     "tf_residual_rms_norm_partials": (_p, _i32, _p, _p, _p, _p, _i64, _i32, _f32, _i32, _p),
     "tf_swiglu": (_p, _p, _p, _i64, _i32, _p),
     "tf_swiglu_rows": (_p, _i64, _p, _i64, _i64, _i32, _i32, _p),
+    "tf_argmax_rows": (_p, _i64, _i32, _i32, _i32, _p, _p),
     "tf_linear_rows": (_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _i32, _p),
     "tf_linear_partials": (_p, _i64, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p),
     "tf_linear_partials_sum": (_p, _i32, _i32, _i32, _p, _i64, _i32, _p),

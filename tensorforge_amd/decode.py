@@ -49,6 +49,7 @@ from tensorforge_amd import _native
 from tensorforge_amd.batch import BatchExecutionResult
 from tensorforge_amd.cache import AppendReservation, PagedKVCache
 from tensorforge_amd.kernels import (
+    argmax_rows,
     embedding_rms_norm,
     PagedAttentionWorkspace,
     linear_kstream,
@@ -504,7 +505,7 @@ class DecodeGraphBucket:
                                                     residual_output=torch.empty_like(mlp),
                                                     norm_output=self.norm_output)
             _project(h, self.weights.lm_head, output=self.logits)
-            torch.argmax(self.logits, dim=-1, out=self.next_tokens)
+            argmax_rows(self.logits, output=self.next_tokens)
         finally:
             set_attention_split_size(previous)
 

@@ -24,6 +24,7 @@ from tensorforge_amd.kernels.linear import (
     linear_rows_supported,
 )
 from tensorforge_amd.kernels.ops import (
+    argmax_rows,
     autotune_cache_size,
     is_hip_available,
     embedding_rms_norm,
@@ -37,6 +38,7 @@ from tensorforge_amd.kernels.rope import rope_paged_kv_append
 
 __all__ = [
     "PagedAttentionWorkspace",
+    "argmax_rows",
     "autotune_cache_size",
     "is_hip_attention_available",
     "is_hip_available",

@@ -346,6 +346,39 @@ def swiglu_gate_up(gate_up: Tensor, *, output: Tensor | None = None) -> Tensor:
     return output
 
 
+def argmax_rows(logits: Tensor, *, output: Tensor | None = None) -> Tensor:
+    """``torch.argmax(logits, dim=-1)`` of a ``[rows, columns]`` matrix with
+    contiguous rows (rows may be strided) into int64 ``output`` -- greedy
+    sampling as the reference's scheduler applies it
+    (scheduler/continuous.py:265-275): the first index of the largest value,
+    a NaN counting as larger than every number."""
+
+    _require_library()
+    if logits.ndim != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [rows, columns] with contiguous rows")
+    if not logits.is_cuda:
+        raise ValueError("argmax_rows requires CUDA tensors")
+    if logits.dtype not in _native.DTYPE_CODES:
+        raise TypeError(f"unsupported dtype: {logits.dtype}")
+    rows, columns = logits.shape
+    if columns < 1:
+        raise ValueError("argmax of an empty row")
+    if output is None:
+        output = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    if (output.shape != (rows,) or output.dtype != torch.int64 or output.device != logits.device
+            or (rows > 1 and output.stride(0) != 1)):
+        raise ValueError("output must be a contiguous int64 [rows] tensor on the logits' device")
+    _native.check(
+        _native.library().tf_argmax_rows(
+            logits.data_ptr(), logits.stride(0) if rows > 1 else columns, rows, columns,
+            _native.dtype_code(logits.dtype), output.data_ptr(),
+            _native.current_stream(logits.device),
+        ),
+        "argmax_rows",
+    )
+    return output
+
+
 def selected_autotune_config(operation: str) -> dict[str, Any] | None:
     """Most recent launch configuration of ``operation`` (reference: triton_ops.py:263-283)."""
 

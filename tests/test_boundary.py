@@ -21,6 +21,7 @@ import torch
 from tensorforge_amd import _native
 from tensorforge_amd.kernels import (
     PagedAttentionWorkspace,
+    argmax_rows,
     autotune_cache_size,
     paged_gqa_decode_attention,
     paged_kv_write_slots,
@@ -143,6 +144,12 @@ def test_c_abi_rejects_bad_arguments_before_launch(lib) -> None:
     status = lib.tf_paged_kv_write_slots(fake, fake, fake, fake, None, 3, 4, 64, 8, 16,
                                          _native.TF_DTYPE_BFLOAT16, stream)
     assert status == invalid and "slot mapping" in _error(lib)
+    status = lib.tf_argmax_rows(fake, 0, 4, 0, _native.TF_DTYPE_BFLOAT16, fake, stream)
+    assert status == invalid and "at least one column" in _error(lib)
+    status = lib.tf_argmax_rows(fake, 10, 4, 16, _native.TF_DTYPE_BFLOAT16, fake, stream)
+    assert status == invalid and "row stride" in _error(lib)
+    status = lib.tf_argmax_rows(fake, 16, 4, 16, _native.TF_DTYPE_BFLOAT16, None, stream)
+    assert status == invalid and "null" in _error(lib)
     # The message is per call: a successful no-op clears it.
     assert lib.tf_swiglu(fake, fake, fake, 0, _native.TF_DTYPE_BFLOAT16, stream) == 0
     assert _error(lib) == ""
@@ -181,6 +188,8 @@ def test_ops_reject_cpu_tensors_like_the_reference(lib) -> None:
         residual_rms_norm(x, x, w)
     with pytest.raises(ValueError, match="CUDA"):
         swiglu(x, x)
+    with pytest.raises(ValueError, match="CUDA"):
+        argmax_rows(x)
 
 
 def test_kv_writes_reject_cpu_tensors(lib) -> None:
