@@ -351,6 +351,11 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
                       int32_t n, int32_t k, int32_t k_per_wave) {
   using M = SplitMma<T>;
   using vec8 = typename M::vec8;
+  // blockIdx.y: a block of 16 MT rows of x and y.
+  const int32_t r0 = static_cast<int32_t>(blockIdx.y) * 16 * MT;
+  x += static_cast<int64_t>(r0) * x_stride;
+  y += static_cast<int64_t>(r0) * y_stride;
+  m = min(m - r0, 16 * MT);
   constexpr int XR = 16 * MT;
   constexpr int CW = 16 * NT;                  // output columns per workgroup
   constexpr int WR = SWIGLU ? 2 * CW : CW;     // weight rows per workgroup
@@ -505,6 +510,7 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
 template <typename T, int MT, int KC, bool SWIGLU, int NT>
 void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
                     int64_t y_stride, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
+  const unsigned row_blocks = static_cast<unsigned>((m + 16 * MT - 1) / (16 * MT));
   const int32_t steps = k / 32;
   const int32_t k_per_wave = ((steps + 3) / 4) * 32;
   const size_t lds =
@@ -524,35 +530,64 @@ void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_st
     }
   }
   hipLaunchKernelGGL((linear_kstream_kernel<T, MT, KC, SWIGLU, NT>),
-                     dim3((n + 16 * NT - 1) / (16 * NT)), dim3(256), lds, stream,
+                     dim3((n + 16 * NT - 1) / (16 * NT), row_blocks), dim3(256), lds, stream,
                      static_cast<const T *>(x), x_stride, static_cast<const T *>(w), w_stride,
                      static_cast<T *>(y), y_stride, m, n, k, k_per_wave);
 }
 
-// Chunk 128 for a plain projection (80 KB of LDS at 64 rows: one workgroup
-// per compute unit, enough for a 160-workgroup qkv), 64 for the SwiGLU form
-// (48 KB with one column tile: several of its workgroups share a compute
-// unit; 64 KB with two).  The SwiGLU form takes two column tiles when that
-// still gives >= 128 workgroups (>= 4096 activation columns).
+// Chunk 128 for a plain projection, 64 for the SwiGLU form.  A workgroup
+// reads 16 (MT + NT) rows of K (x rows and weight rows; twice NT weight
+// rows for SwiGLU), so fewer rows per workgroup means fewer re-reads of x;
+// one workgroup per compute unit is what keeps the split even.  The plain
+// form therefore takes, among workgroups of 1-4 row tiles (MT) and 1-2
+// column tiles (NT) whose grid fits the 256 compute units, the one with the
+// fewest rows (then the larger grid, then one column tile); a grid that
+// fits with none keeps MT = ceil(m / 16), NT = 1.  On MI355X at 64 rows:
+// qkv (2560 columns) MT 2, NT 2 (160 workgroups) 9.2 -> 7.9 us; 2048
+// columns MT 2, NT 1 (256) 8.8 -> 6.5 us; at 33-48 rows qkv MT 1, NT 2
+// (240) 7.5-7.8 -> 6.5-6.6 us.  The SwiGLU form takes MT = ceil(m / 16)
+// and two column tiles from 4096 activation columns.
 template <typename T, bool SWIGLU>
 void launch_kstream_mt(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
                        int64_t y_stride, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
   constexpr int KC = SWIGLU ? 64 : 128;
-#define TF_KSTREAM_MT(NT)                                                                      \
-  switch ((m + 15) / 16) {                                                                     \
-    case 1: launch_kstream<T, 1, KC, SWIGLU, NT>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break; \
-    case 2: launch_kstream<T, 2, KC, SWIGLU, NT>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break; \
-    case 3: launch_kstream<T, 3, KC, SWIGLU, NT>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break; \
-    default: launch_kstream<T, 4, KC, SWIGLU, NT>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); break; \
-  }
+  const int32_t row_tiles = (m + 15) / 16;
+  int mt = row_tiles > 4 ? 4 : row_tiles;
+  int nt = 1;
   if constexpr (SWIGLU) {
-    if (n >= 4096) {
-      TF_KSTREAM_MT(2)
-      return;
+    if (n >= 4096) nt = 2;
+  } else {
+    int best_rows = 1 << 30;
+    int64_t best_grid = 0;
+    for (int cm = 1; cm <= 4 && cm <= row_tiles; ++cm) {
+      for (int cn = 1; cn <= 2; ++cn) {
+        const int64_t grid = static_cast<int64_t>((row_tiles + cm - 1) / cm) *
+                             ((n + 16 * cn - 1) / (16 * cn));
+        if (grid > 256) continue;
+        if (cm + cn < best_rows || (cm + cn == best_rows && grid > best_grid) ||
+            (cm + cn == best_rows && grid == best_grid && cn < nt)) {
+          best_rows = cm + cn;
+          best_grid = grid;
+          mt = cm;
+          nt = cn;
+        }
+      }
     }
   }
-  TF_KSTREAM_MT(1)
-#undef TF_KSTREAM_MT
+#define TF_KSTREAM_CASE(MT, NT)                                                                \
+  if (mt == MT && nt == NT) {                                                                  \
+    launch_kstream<T, MT, KC, SWIGLU, NT>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); \
+    return;                                                                                    \
+  }
+  TF_KSTREAM_CASE(1, 1)
+  TF_KSTREAM_CASE(2, 1)
+  TF_KSTREAM_CASE(3, 1)
+  TF_KSTREAM_CASE(4, 1)
+  TF_KSTREAM_CASE(1, 2)
+  TF_KSTREAM_CASE(2, 2)
+  TF_KSTREAM_CASE(3, 2)
+  TF_KSTREAM_CASE(4, 2)
+#undef TF_KSTREAM_CASE
 }
 
 template <typename T, int MT, bool SWIGLU>

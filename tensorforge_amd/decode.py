@@ -177,8 +177,8 @@ def _project(x: Tensor, weight: Tensor, output: Tensor | None = None) -> Tensor:
     LDS-staged weight stream (linear_stream: 24.6-25.0 us against 30.4-30.7
     for hipBLASLt at 32000 x 2048; 12.6-12.8 us against 12.5-14.7 at
     11264 x 2048).  Narrower weights with K >= 1024 (the stacked q/k/v)
-    take the K-split weight stream (linear_kstream: 5.2-9.4 us at 1..64 rows
-    against 5.7-12.7 for linear_rows and 11.1-11.9 for hipBLASLt at
+    take the K-split weight stream (linear_kstream: 4.7-7.9 us at 1..64 rows
+    against 5.7-12.9 for linear_rows and 11.2-11.9 for hipBLASLt at
     2560 x 2048).  Other weights up to 16 rows use the K-split MFMA kernel
     (linear_rows) when small (<= 8M elements), where the library GEMM
     launches too few workgroups; otherwise hipBLASLt."""
@@ -292,7 +292,10 @@ class DecodeGraphBucket:
         # down shapes: at 64 rows 6.1 / 10.6 us against 10.9 / 18.2 for
         # hipBLASLt; at up to 16 rows only for weights of >= 1M elements --
         # smaller ones make too few 64-column workgroups and stay on
-        # linear_rows).
+        # linear_rows).  Above 32 rows an output projection with K >= 1024
+        # instead takes the K-split weight stream with a rounded output and
+        # the plain residual RMSNorm (TinyLlama b64 step 1.559 -> 1.549 ms;
+        # at 16-32 rows the partials stay as fast or faster).
         self.split_o = self.split_down = 0
         layer0 = weights.layers[0]
         large = min(layer0.o_proj.numel(), layer0.down.numel()) >= 1024 * 1024
@@ -302,7 +305,8 @@ class DecodeGraphBucket:
             probe_d = torch.empty((b, config.intermediate_size), dtype=dtype, device=device)
             if (linear_partials_supported(probe_o, layer0.o_proj)
                     and linear_partials_supported(probe_d, layer0.down)):
-                self.split_o = default_splits(*layer0.o_proj.shape)
+                kstream_o = b > 32 and layer0.o_proj.shape[1] >= 1024
+                self.split_o = 0 if kstream_o else default_splits(*layer0.o_proj.shape)
                 self.split_down = default_splits(*layer0.down.shape)
                 self.partials_o = torch.empty((self.split_o, b, config.hidden_size),
                                               dtype=torch.float32, device=device)
