@@ -159,12 +159,16 @@ def test_linear_swiglu_equals_projection_then_activation(device, dtype, rows, in
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows", [1, 17, 33, 64])
-@pytest.mark.parametrize(("n", "k"), [(2560, 2048), (100, 96), (48, 800), (256, 4128)])
+@pytest.mark.parametrize(("n", "k"), [(2560, 2048), (2048, 2048), (100, 96), (48, 800),
+                                    (256, 4128)])
 def test_linear_kstream_matches_fp32(device, dtype, rows, n, k):
-    """K split over a 16-column workgroup's wavefronts: within the storage
-    bar of the fp32 product, on tail column tiles, K that ends inside a
-    chunk or leaves a wavefront without work (K = 96: 3 k-steps for 4
-    wavefronts) and strided output rows."""
+    """K split over a workgroup's wavefronts: within the storage bar of the
+    fp32 product, on tail column tiles, K that ends inside a chunk or leaves
+    a wavefront without work (K = 96: 3 k-steps for 4 wavefronts) and
+    strided output rows, under each tiling the launcher picks (2560 columns:
+    1 row tile x 2 column tiles in 3 row blocks at 33 rows, 2 x 2 in 2
+    blocks at 64; 2048 columns: 2 x 1 in 2 blocks at 33-64 rows; 100
+    columns: 1 x 1 in up to 4 blocks)."""
 
     from tensorforge_amd.kernels import linear_kstream
 
