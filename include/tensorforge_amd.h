@@ -40,6 +40,10 @@
  *   tf_linear_kstream        the same projections, K split over a 16-column
  *                            workgroup's wavefronts (narrow weights)
  *   tf_linear_kswiglu        its K-split form
+ *   tf_linear_kstream_norm,  the same K-split projections fused with the
+ *   tf_linear_kswiglu_norm   RMSNorm before them (triton_ops.py:179-205)
+ *   tf_linear_kstream_residual  and with the residual add after them
+ *                            (triton_ops.py:208-243)
  *   tf_linear_swiglu         the MLP's gate|up projection with its SwiGLU
  *                            (model/layers.py:144-158)
  *   tf_prefill_attention     prefill's causal attention (runtime/prefill.py:84-88, 109-118)
@@ -461,6 +465,45 @@ int32_t tf_linear_kstream(const void *x, int64_t x_row_stride, const void *weigh
 int32_t tf_linear_kswiglu(const void *x, int64_t x_row_stride, const void *gate_up_weight,
                           int64_t weight_row_stride, void *y, int64_t y_row_stride, int32_t m,
                           int32_t intermediate, int32_t k, int32_t dtype, void *stream);
+
+/*
+ * tf_linear_kstream with the RMSNorm of x's rows applied to the product:
+ *   y[i][j] = round(rsqrt(mean_k(x[i][k]^2) + eps) * (x[i] . w'[j]))
+ * for a weight w' whose columns carry the norm's gain (w'[j][k] =
+ * round(w[j][k] * gain[k]), the caller folds it once).  Replaces the
+ * reference's RMSNorm (tensorforge/kernels/triton_ops.py:179-205) followed
+ * by the projection (model/layers.py:88-95) -- the same product with the
+ * gain rounded into the weight instead of into the normalised row; no
+ * normalised x is written.  eps > 0.
+ */
+int32_t tf_linear_kstream_norm(const void *x, int64_t x_row_stride, const void *weight,
+                               int64_t weight_row_stride, void *y, int64_t y_row_stride, int32_t m,
+                               int32_t n, int32_t k, float eps, int32_t dtype, void *stream);
+
+/*
+ * tf_linear_kswiglu under the same row norm: both products of row i are
+ * scaled by rsqrt(mean_k(x[i][k]^2) + eps) before the activation, the
+ * stacked weight carrying the norm's gain.  Replaces the reference's
+ * post-attention RMSNorm followed by the MLP's gate and up projections and
+ * SwiGLU (triton_ops.py:179-205; model/layers.py:144-158).
+ */
+int32_t tf_linear_kswiglu_norm(const void *x, int64_t x_row_stride, const void *gate_up_weight,
+                               int64_t weight_row_stride, void *y, int64_t y_row_stride, int32_t m,
+                               int32_t intermediate, int32_t k, float eps, int32_t dtype,
+                               void *stream);
+
+/*
+ * tf_linear_kstream added to the residual stream:
+ *   y[i][j] = round(round(x[i] . w[j]) + residual[i][j])
+ * -- the residual output of the reference's residual_rms_norm
+ * (triton_ops.py:208-243) over the projection (the o / down projections of
+ * runtime/decode_bucket.py:470-474, 505), bit for bit; the norm itself is
+ * left to the consumer (tf_linear_kstream_norm).  y may not alias residual.
+ */
+int32_t tf_linear_kstream_residual(const void *x, int64_t x_row_stride, const void *weight,
+                                   int64_t weight_row_stride, const void *residual,
+                                   int64_t residual_row_stride, void *y, int64_t y_row_stride,
+                                   int32_t m, int32_t n, int32_t k, int32_t dtype, void *stream);
 
 /*
  * The MLP's stacked gate|up projection and its SwiGLU in one launch:

@@ -113,6 +113,10 @@ SIGNATURES: dict[str, tuple[Any, ...]] = {
     "tf_linear_swiglu": (_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p),
     "tf_linear_kstream": (_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p),
     "tf_linear_kswiglu": (_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p),
+    "tf_linear_kstream_norm": (_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _f32, _i32, _p),
+    "tf_linear_kswiglu_norm": (_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _f32, _i32, _p),
+    "tf_linear_kstream_residual": (_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32,
+                                   _i32, _p),
     "tf_prefill_attention": (_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i32, _i32, _i32, _i32,
                              _f32, _i32, _i32, _p),
 }

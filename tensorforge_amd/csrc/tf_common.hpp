@@ -105,6 +105,42 @@ __device__ __forceinline__ float swiglu_act(float g, float u) {
   return silu * u;
 }
 
+// c + a . b over 8 elements with the packed two-element dot product
+// (v_dot2_f32_bf16 / v_dot2_f32_f16: fp32 products and accumulation): the
+// VALU form of the attention score product, and a row's sum of squares in
+// the norm-fused projections.
+template <typename T>
+__device__ __forceinline__ float dot8(T __attribute__((ext_vector_type(8))) a,
+                                      T __attribute__((ext_vector_type(8))) b, float c);
+
+template <>
+__device__ __forceinline__ float dot8<__bf16>(__bf16 __attribute__((ext_vector_type(8))) a,
+                                              __bf16 __attribute__((ext_vector_type(8))) b,
+                                              float c) {
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 0, 1),
+                                      __builtin_shufflevector(b, b, 0, 1), c, false);
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 2, 3),
+                                      __builtin_shufflevector(b, b, 2, 3), c, false);
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 4, 5),
+                                      __builtin_shufflevector(b, b, 4, 5), c, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 6, 7),
+                                         __builtin_shufflevector(b, b, 6, 7), c, false);
+}
+
+template <>
+__device__ __forceinline__ float dot8<_Float16>(_Float16 __attribute__((ext_vector_type(8))) a,
+                                                _Float16 __attribute__((ext_vector_type(8))) b,
+                                                float c) {
+  c = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 0, 1),
+                             __builtin_shufflevector(b, b, 0, 1), c, false);
+  c = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 2, 3),
+                             __builtin_shufflevector(b, b, 2, 3), c, false);
+  c = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 4, 5),
+                             __builtin_shufflevector(b, b, 4, 5), c, false);
+  return __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 6, 7),
+                                __builtin_shufflevector(b, b, 6, 7), c, false);
+}
+
 // ---------------------------------------------------------------------------
 // Wavefront (64-lane) reductions.
 // ---------------------------------------------------------------------------

@@ -340,21 +340,41 @@ __device__ __forceinline__ int kstream_lds_offset(int row, int piece) {
   return row * KC + ((piece ^ (row & kMask)) << 3);
 }
 
+// Epilogues of the K-split kernel.
+//   kEpiPlain     y = round(sum)
+//   kEpiNorm      y = round(rsqrt(mean_k(x[r][k]^2) + eps) * sum): the
+//                 RMSNorm of x's rows applied to the product, for a weight
+//                 whose columns carry the norm's gain (w'[n][k] = w[n][k] g[k]);
+//                 each workgroup sees all of K, so the row sums of squares
+//                 come from the x chunks it stages anyway
+//   kEpiResidual  y = round(round(sum) + residual[r][n]): the projection
+//                 added to the residual stream, rounded as a separate add is
+enum KstreamEpi : int { kEpiPlain = 0, kEpiNorm = 1, kEpiResidual = 2 };
+template <typename T>
+struct KstreamExtra {
+  float eps = 0.f;
+  const T *residual = nullptr;
+  int64_t residual_stride = 0;
+};
+
 // SWIGLU: the workgroup's 16 NT columns j are activation columns; the
 // weight stacks gate rows [0, n) over up rows [n, 2n), each wavefront
 // accumulates both tiles of every column tile over its quarter of K, and
-// the output is round(swiglu_act(round(g), round(u))).
-template <typename T, int MT, int KC, bool SWIGLU, int NT>
+// the output is round(swiglu_act(round(g), round(u))) (g and u scaled by
+// the row's norm first under kEpiNorm).
+template <typename T, int MT, int KC, bool SWIGLU, int NT, int EPI>
 __global__ void __launch_bounds__(256)
 linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restrict__ w,
                       int64_t w_stride, T *__restrict__ y, int64_t y_stride, int32_t m,
-                      int32_t n, int32_t k, int32_t k_per_wave) {
+                      int32_t n, int32_t k, int32_t k_per_wave, KstreamExtra<T> extra) {
   using M = SplitMma<T>;
   using vec8 = typename M::vec8;
+  static_assert(!(SWIGLU && EPI == kEpiResidual), "the residual epilogue has no SwiGLU form");
   // blockIdx.y: a block of 16 MT rows of x and y.
   const int32_t r0 = static_cast<int32_t>(blockIdx.y) * 16 * MT;
   x += static_cast<int64_t>(r0) * x_stride;
   y += static_cast<int64_t>(r0) * y_stride;
+  if constexpr (EPI == kEpiResidual) extra.residual += static_cast<int64_t>(r0) * extra.residual_stride;
   m = min(m - r0, 16 * MT);
   constexpr int XR = 16 * MT;
   constexpr int CW = 16 * NT;                  // output columns per workgroup
@@ -417,6 +437,12 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
   // The region is private to the wavefront, whose LDS requests are served in
   // order: compiler barriers order the stores, the operand reads and the
   // next chunk's stores.
+  // kEpiNorm: this lane's sums of squares of the x operands it feeds the
+  // MFMAs (row 16 mt + l16, eight elements of every k-step in range), taken
+  // from the operand registers so they cost no load and overlap the MFMAs.
+  float ssq[EPI == kEpiNorm ? MT : 1];
+#pragma unroll
+  for (int i = 0; i < (EPI == kEpiNorm ? MT : 1); ++i) ssq[i] = 0.f;
   auto stage_compute = [&](int32_t kk, const vec8(&xr)[kLoadsX], const vec8(&wr)[kLoadsW]) {
     __asm__ volatile("" ::: "memory");
 #pragma unroll
@@ -446,6 +472,7 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
           acc[mt][ct] = M::mma(a, b[ct], acc[mt][ct]);
           if constexpr (SWIGLU) accu[mt][ct] = M::mma(a, bu[ct], accu[mt][ct]);
         }
+        if constexpr (EPI == kEpiNorm) ssq[mt] = dot8<T>(a, a, ssq[mt]);
       }
     }
     __asm__ volatile("" ::: "memory");
@@ -468,6 +495,19 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
     }
   }
 
+  // kEpiNorm: a row's sum of squares over its four lanes, then over the
+  // four wavefronts' quarters of K.
+  // Rows of sums [4 waves][XR] past the staging regions.
+  float *ssq_rows = reinterpret_cast<float *>(kstream_smem + 4 * kWaveElems * sizeof(T));
+  if constexpr (EPI == kEpiNorm) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float v = ssq[mt];
+      v += __shfl_xor(v, 16, 64);  // the four lanes (l16, q4) of row 16 mt + l16
+      v += __shfl_xor(v, 32, 64);
+      if (q4 == 0) ssq_rows[wave * XR + 16 * mt + l16] = v;
+    }
+  }
   // Sum the four wavefront tiles: item (mt, r, lane) of column tile ct is
   // y[16 mt + 4 q4 + r][n0 + 16 ct + l16].
   __syncthreads();  // every wavefront's operand reads are done
@@ -498,23 +538,35 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
     const int32_t row = 16 * mt + 4 * (il >> 4) + r;
     const int32_t col = n0 + 16 * ct + (il & 15);
     if (row >= m || col >= n) continue;
+    if constexpr (EPI == kEpiNorm) {
+      const float sq = ((ssq_rows[row] + ssq_rows[XR + row]) + ssq_rows[2 * XR + row]) +
+                       ssq_rows[3 * XR + row];
+      const float scale = rsqrtf(sq / static_cast<float>(k) + extra.eps);
+      sum *= scale;
+      sumu *= scale;
+    }
     T out;
     if constexpr (SWIGLU)
       out = from_float<T>(swiglu_act(to_float(from_float<T>(sum)), to_float(from_float<T>(sumu))));
+    else if constexpr (EPI == kEpiResidual)
+      out = from_float<T>(to_float(from_float<T>(sum)) +
+                          to_float(extra.residual[static_cast<int64_t>(row) * extra.residual_stride + col]));
     else
       out = from_float<T>(sum);
     y[static_cast<int64_t>(row) * y_stride + col] = out;
   }
 }
 
-template <typename T, int MT, int KC, bool SWIGLU, int NT>
+template <typename T, int MT, int KC, bool SWIGLU, int NT, int EPI>
 void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
-                    int64_t y_stride, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
+                    int64_t y_stride, int32_t m, int32_t n, int32_t k, const KstreamExtra<T> &extra,
+                    hipStream_t stream) {
   const unsigned row_blocks = static_cast<unsigned>((m + 16 * MT - 1) / (16 * MT));
   const int32_t steps = k / 32;
   const int32_t k_per_wave = ((steps + 3) / 4) * 32;
   const size_t lds =
-      static_cast<size_t>(4) * (16 * MT + (SWIGLU ? 32 : 16) * NT) * KC * sizeof(T);
+      static_cast<size_t>(4) * (16 * MT + (SWIGLU ? 32 : 16) * NT) * KC * sizeof(T) +
+      (EPI == kEpiNorm ? static_cast<size_t>(4) * 16 * MT * sizeof(float) : 0);
   if (lds > 64 * 1024) {
     // Raise the kernel's dynamic LDS limit once per device (a failure shows
     // up as a launch error).
@@ -524,15 +576,15 @@ void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_st
     if (hipGetDevice(&device) == hipSuccess && device >= 0 && device < kMaxDevices &&
         !raised[device].load(std::memory_order_acquire)) {
       if (hipFuncSetAttribute(
-              reinterpret_cast<const void *>(&linear_kstream_kernel<T, MT, KC, SWIGLU, NT>),
+              reinterpret_cast<const void *>(&linear_kstream_kernel<T, MT, KC, SWIGLU, NT, EPI>),
               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) == hipSuccess)
         raised[device].store(true, std::memory_order_release);
     }
   }
-  hipLaunchKernelGGL((linear_kstream_kernel<T, MT, KC, SWIGLU, NT>),
+  hipLaunchKernelGGL((linear_kstream_kernel<T, MT, KC, SWIGLU, NT, EPI>),
                      dim3((n + 16 * NT - 1) / (16 * NT), row_blocks), dim3(256), lds, stream,
                      static_cast<const T *>(x), x_stride, static_cast<const T *>(w), w_stride,
-                     static_cast<T *>(y), y_stride, m, n, k, k_per_wave);
+                     static_cast<T *>(y), y_stride, m, n, k, k_per_wave, extra);
 }
 
 // Chunk 128 for a plain projection, 64 for the SwiGLU form.  A workgroup
@@ -547,9 +599,10 @@ void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_st
 // columns MT 2, NT 1 (256) 8.8 -> 6.5 us; at 33-48 rows qkv MT 1, NT 2
 // (240) 7.5-7.8 -> 6.5-6.6 us.  The SwiGLU form takes MT = ceil(m / 16)
 // and two column tiles from 4096 activation columns.
-template <typename T, bool SWIGLU>
+template <typename T, bool SWIGLU, int EPI>
 void launch_kstream_mt(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
-                       int64_t y_stride, int32_t m, int32_t n, int32_t k, hipStream_t stream) {
+                       int64_t y_stride, int32_t m, int32_t n, int32_t k,
+                       const KstreamExtra<T> &extra, hipStream_t stream) {
   constexpr int KC = SWIGLU ? 64 : 128;
   const int32_t row_tiles = (m + 15) / 16;
   int mt = row_tiles > 4 ? 4 : row_tiles;
@@ -576,7 +629,8 @@ void launch_kstream_mt(const void *x, int64_t x_stride, const void *w, int64_t w
   }
 #define TF_KSTREAM_CASE(MT, NT)                                                                \
   if (mt == MT && nt == NT) {                                                                  \
-    launch_kstream<T, MT, KC, SWIGLU, NT>(x, x_stride, w, w_stride, y, y_stride, m, n, k, stream); \
+    launch_kstream<T, MT, KC, SWIGLU, NT, EPI>(x, x_stride, w, w_stride, y, y_stride, m, n, k, \
+                                               extra, stream);                                    \
     return;                                                                                    \
   }
   TF_KSTREAM_CASE(1, 1)
@@ -809,7 +863,8 @@ namespace {
 
 int32_t kstream_entry(const void *x, int64_t x_row_stride, const void *weight,
                       int64_t weight_row_stride, void *y, int64_t y_row_stride, int32_t m,
-                      int32_t n, int32_t k, int32_t dtype, void *stream, bool swiglu,
+                      int32_t n, int32_t k, int32_t dtype, void *stream, bool swiglu, int epi,
+                      float eps, const void *residual, int64_t residual_row_stride,
                       const char *name) {
   clear_error();
   if (dtype != TF_DTYPE_FLOAT16 && dtype != TF_DTYPE_BFLOAT16)
@@ -820,22 +875,45 @@ int32_t kstream_entry(const void *x, int64_t x_row_stride, const void *weight,
     return fail(TF_ERROR_UNSUPPORTED, "linear_kstream needs K to be a positive multiple of 32");
   if (x_row_stride < k || weight_row_stride < k || y_row_stride < n)
     return fail(TF_ERROR_INVALID_ARGUMENT, "row strides are shorter than the rows");
+  if (epi == kEpiNorm && !(eps > 0.f)) return fail(TF_ERROR_INVALID_ARGUMENT, "eps must be positive");
+  if (epi == kEpiResidual && residual_row_stride < n)
+    return fail(TF_ERROR_INVALID_ARGUMENT, "residual row stride is shorter than the rows");
   if (n > 65535 * 16) return fail(TF_ERROR_UNSUPPORTED, "grid too large");
   if (m == 0 || n == 0) return TF_SUCCESS;
-  if (!x || !weight || !y) return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
+  if (!x || !weight || !y || (epi == kEpiResidual && !residual))
+    return fail(TF_ERROR_INVALID_ARGUMENT, "null tensor pointer");
   const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
                           static_cast<uintptr_t>(x_row_stride * 2) |
                           static_cast<uintptr_t>(weight_row_stride * 2);
   if (align % 16 != 0)
     return fail(TF_ERROR_UNSUPPORTED, "linear_kstream needs 16-byte aligned x and weight rows");
   hipStream_t s = static_cast<hipStream_t>(stream);
-#define TF_KSTREAM_LAUNCH(T, G) \
-  launch_kstream_mt<T, G>(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, m, n, k, s)
-  if (dtype == TF_DTYPE_BFLOAT16) {
-    if (swiglu) TF_KSTREAM_LAUNCH(__bf16, true); else TF_KSTREAM_LAUNCH(__bf16, false);
-  } else {
-    if (swiglu) TF_KSTREAM_LAUNCH(_Float16, true); else TF_KSTREAM_LAUNCH(_Float16, false);
-  }
+#define TF_KSTREAM_LAUNCH(T)                                                                  \
+  do {                                                                                        \
+    KstreamExtra<T> extra;                                                                    \
+    extra.eps = eps;                                                                          \
+    extra.residual = static_cast<const T *>(residual);                                       \
+    extra.residual_stride = residual_row_stride;                                              \
+    if (swiglu && epi == kEpiNorm)                                                            \
+      launch_kstream_mt<T, true, kEpiNorm>(x, x_row_stride, weight, weight_row_stride, y,     \
+                                           y_row_stride, m, n, k, extra, s);                  \
+    else if (swiglu)                                                                          \
+      launch_kstream_mt<T, true, kEpiPlain>(x, x_row_stride, weight, weight_row_stride, y,    \
+                                            y_row_stride, m, n, k, extra, s);                 \
+    else if (epi == kEpiNorm)                                                                 \
+      launch_kstream_mt<T, false, kEpiNorm>(x, x_row_stride, weight, weight_row_stride, y,    \
+                                            y_row_stride, m, n, k, extra, s);                 \
+    else if (epi == kEpiResidual)                                                             \
+      launch_kstream_mt<T, false, kEpiResidual>(x, x_row_stride, weight, weight_row_stride, y, \
+                                                y_row_stride, m, n, k, extra, s);             \
+    else                                                                                      \
+      launch_kstream_mt<T, false, kEpiPlain>(x, x_row_stride, weight, weight_row_stride, y,   \
+                                             y_row_stride, m, n, k, extra, s);                \
+  } while (0)
+  if (dtype == TF_DTYPE_BFLOAT16)
+    TF_KSTREAM_LAUNCH(__bf16);
+  else
+    TF_KSTREAM_LAUNCH(_Float16);
 #undef TF_KSTREAM_LAUNCH
   return check_launch(name);
 }
@@ -847,7 +925,26 @@ extern "C" int32_t tf_linear_kstream(const void *x, int64_t x_row_stride, const 
                                      int64_t weight_row_stride, void *y, int64_t y_row_stride,
                                      int32_t m, int32_t n, int32_t k, int32_t dtype, void *stream) {
   return tf::kstream_entry(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, m, n, k,
-                           dtype, stream, false, "linear_kstream");
+                           dtype, stream, false, tf::kEpiPlain, 0.f, nullptr, 0, "linear_kstream");
+}
+
+extern "C" int32_t tf_linear_kstream_norm(const void *x, int64_t x_row_stride,
+                                          const void *weight, int64_t weight_row_stride, void *y,
+                                          int64_t y_row_stride, int32_t m, int32_t n, int32_t k,
+                                          float eps, int32_t dtype, void *stream) {
+  return tf::kstream_entry(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, m, n, k,
+                           dtype, stream, false, tf::kEpiNorm, eps, nullptr, 0,
+                           "linear_kstream_norm");
+}
+
+extern "C" int32_t tf_linear_kstream_residual(const void *x, int64_t x_row_stride,
+                                              const void *weight, int64_t weight_row_stride,
+                                              const void *residual, int64_t residual_row_stride,
+                                              void *y, int64_t y_row_stride, int32_t m, int32_t n,
+                                              int32_t k, int32_t dtype, void *stream) {
+  return tf::kstream_entry(x, x_row_stride, weight, weight_row_stride, y, y_row_stride, m, n, k,
+                           dtype, stream, false, tf::kEpiResidual, 0.f, residual,
+                           residual_row_stride, "linear_kstream_residual");
 }
 
 extern "C" int32_t tf_linear_kswiglu(const void *x, int64_t x_row_stride,
@@ -856,5 +953,16 @@ extern "C" int32_t tf_linear_kswiglu(const void *x, int64_t x_row_stride,
                                      int32_t intermediate, int32_t k, int32_t dtype,
                                      void *stream) {
   return tf::kstream_entry(x, x_row_stride, gate_up_weight, weight_row_stride, y, y_row_stride,
-                           m, intermediate, k, dtype, stream, true, "linear_kswiglu");
+                           m, intermediate, k, dtype, stream, true, tf::kEpiPlain, 0.f, nullptr, 0,
+                           "linear_kswiglu");
+}
+
+extern "C" int32_t tf_linear_kswiglu_norm(const void *x, int64_t x_row_stride,
+                                          const void *gate_up_weight, int64_t weight_row_stride,
+                                          void *y, int64_t y_row_stride, int32_t m,
+                                          int32_t intermediate, int32_t k, float eps,
+                                          int32_t dtype, void *stream) {
+  return tf::kstream_entry(x, x_row_stride, gate_up_weight, weight_row_stride, y, y_row_stride,
+                           m, intermediate, k, dtype, stream, true, tf::kEpiNorm, eps, nullptr, 0,
+                           "linear_kswiglu_norm");
 }

@@ -502,41 +502,6 @@ __host__ __device__ constexpr int mfma_lds_bytes(int head_dim, int waves) {
 constexpr float kRescaleThreshold = 8.f;
 constexpr int kSegmentTiles = 64;  // page-window capacity: 64 tiles = 1024 tokens
 
-// c + a . b over 8 elements with the packed two-element dot product
-// (v_dot2_f32_bf16 / v_dot2_f32_f16: fp32 products and accumulation) -- the
-// VALU form of the score product.
-template <typename T>
-__device__ __forceinline__ float dot8(T __attribute__((ext_vector_type(8))) a,
-                                      T __attribute__((ext_vector_type(8))) b, float c);
-
-template <>
-__device__ __forceinline__ float dot8<__bf16>(__bf16 __attribute__((ext_vector_type(8))) a,
-                                              __bf16 __attribute__((ext_vector_type(8))) b,
-                                              float c) {
-  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 0, 1),
-                                      __builtin_shufflevector(b, b, 0, 1), c, false);
-  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 2, 3),
-                                      __builtin_shufflevector(b, b, 2, 3), c, false);
-  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 4, 5),
-                                      __builtin_shufflevector(b, b, 4, 5), c, false);
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 6, 7),
-                                         __builtin_shufflevector(b, b, 6, 7), c, false);
-}
-
-template <>
-__device__ __forceinline__ float dot8<_Float16>(_Float16 __attribute__((ext_vector_type(8))) a,
-                                                _Float16 __attribute__((ext_vector_type(8))) b,
-                                                float c) {
-  c = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 0, 1),
-                             __builtin_shufflevector(b, b, 0, 1), c, false);
-  c = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 2, 3),
-                             __builtin_shufflevector(b, b, 2, 3), c, false);
-  c = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 4, 5),
-                             __builtin_shufflevector(b, b, 4, 5), c, false);
-  return __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 6, 7),
-                                __builtin_shufflevector(b, b, 6, 7), c, false);
-}
-
 // Max / sum over the 16 lanes of a DPP row (every lane gets the result):
 // quad_perm [1,0,3,2] and [2,3,0,1] combine within quads, row_half_mirror
 // (lane i <-> 7 - i of each half row) pairs the two quads of a half row and

@@ -36,6 +36,7 @@ initialize_weights (layers.py:174-176).
 from __future__ import annotations
 
 import time
+from collections.abc import Callable
 from contextlib import suppress
 from dataclasses import asdict, dataclass, field
 
@@ -67,7 +68,11 @@ from tensorforge_amd.kernels.attention import (
     paged_gqa_decode_attention_rope_append,
     set_attention_split_size,
 )
-from tensorforge_amd.kernels.linear import default_splits, linear_partials_supported
+from tensorforge_amd.kernels.linear import (
+    default_splits,
+    fold_norm_gain,
+    linear_partials_supported,
+)
 from tensorforge_amd.kernels.ops import residual_rms_norm_partials
 from tensorforge_amd.kernels.prefill import (
     prefill_attention,
@@ -220,7 +225,8 @@ class DecodeGraphBucket:
 
     def __init__(self, weights: DecoderWeights, cache: PagedKVCache, *, batch_capacity: int,
                  context_capacity: int, token_state: Tensor | None = None, graph: bool = True,
-                 metrics: _MutableMetrics | None = None) -> None:
+                 metrics: _MutableMetrics | None = None,
+                 folded: Callable[[], list[tuple[Tensor, Tensor]]] | None = None) -> None:
         config = weights.config
         self.weights = weights
         self.cache = cache
@@ -318,6 +324,22 @@ class DecodeGraphBucket:
         # projection + SwiGLU pair).
         probe_h = torch.empty((b, config.hidden_size), dtype=dtype, device=device)
         self.fused_gate_up = linear_rows_supported(probe_h, layer0.gate_up)
+        # Norms fused into the projections around them (every weight through
+        # the K-split stream): qkv and gate|up scale their products by the
+        # RMSNorm of their input rows, with the norm gains folded into
+        # copies of their weights (`folded`, shared by the executor's
+        # buckets), and o and down add their products to the residual
+        # stream -- five launches per layer instead of seven, and no
+        # normalised activations written.  The LM head keeps the final norm.
+        probe_a = torch.empty((b, hq * d), dtype=dtype, device=device)
+        probe_f = torch.empty((b, config.intermediate_size), dtype=dtype, device=device)
+        self.fused_norms = (folded is not None and self.fused_gate_up
+                            and linear_rows_supported(probe_h, layer0.qkv)
+                            and linear_rows_supported(probe_a, layer0.o_proj)
+                            and linear_rows_supported(probe_f, layer0.down))
+        self._folded = folded if self.fused_norms else None
+        if self.fused_norms:
+            self.split_o = self.split_down = 0
         self._graph: torch.cuda.CUDAGraph | None = None
 
     def addresses(self) -> dict[str, int]:
@@ -454,8 +476,12 @@ class DecodeGraphBucket:
                 self.token_state, self.source_lanes, self.host_tokens, self.weights.embedding,
                 self.weights.layers[0].input_norm, eps, x_output=self.embedding_output,
                 norm_output=self.norm_output)
+            folded = self._folded() if self._folded is not None else None
             for index, layer in enumerate(self.weights.layers):
-                qkv = _project(h, layer.qkv)
+                if folded is not None:
+                    qkv = linear_kstream(residual, folded[index][0], norm_eps=eps)
+                else:
+                    qkv = _project(h, layer.qkv)
                 key_cache = self.cache.key_cache[index]
                 value_cache = self.cache.value_cache[index]
                 if self.fused_rope:
@@ -479,6 +505,12 @@ class DecodeGraphBucket:
                         scale=d ** -0.5, max_context_length=self.context_capacity,
                         output=self.attention_output, workspace=self.workspace)
                 attention = self.attention_output.view(b, hq * d)
+                if folded is not None:
+                    residual = linear_kstream(attention, layer.o_proj, residual=residual)
+                    act = linear_swiglu(residual, folded[index][1], output=self.swiglu_output,
+                                        k_split=True, norm_eps=eps)
+                    residual = linear_kstream(act, layer.down, residual=residual)
+                    continue
                 if self.split_o:
                     linear_stream(attention, layer.o_proj, splits=self.split_o,
                                   partials=self.partials_o)
@@ -508,6 +540,8 @@ class DecodeGraphBucket:
                     residual, h = residual_rms_norm(mlp, residual, next_norm, eps,
                                                     residual_output=torch.empty_like(mlp),
                                                     norm_output=self.norm_output)
+            if folded is not None:
+                h = rms_norm(residual, self.weights.final_norm, eps, output=self.norm_output)
             _project(h, self.weights.lm_head, output=self.logits)
             argmax_rows(self.logits, output=self.next_tokens)
         finally:
@@ -783,7 +817,8 @@ class BucketedDecodeExecutor:
 
     def __init__(self, weights: DecoderWeights, cache: PagedKVCache, *,
                  batch_buckets: tuple[int, ...] = DEFAULT_BATCH_BUCKETS,
-                 context_buckets: tuple[int, ...] = DEFAULT_CONTEXT_BUCKETS) -> None:
+                 context_buckets: tuple[int, ...] = DEFAULT_CONTEXT_BUCKETS,
+                 fuse_norms: bool = True) -> None:
         if not batch_buckets or any(value <= 0 for value in batch_buckets):
             raise ValueError("batch_buckets must contain positive capacities")
         if not context_buckets or any(value <= 0 for value in context_buckets):
@@ -813,6 +848,21 @@ class BucketedDecodeExecutor:
         self._next_slot = 0
         self._metrics = _MutableMetrics()
         self.step_records: list[DecodeStepRecord] = []
+        self._folded_weights: list[tuple[Tensor, Tensor]] | None = None
+        # fuse_norms=False keeps the RMSNorm launches between the
+        # projections (the split-K partials path) in every bucket.
+        self._fold = self._folded if fuse_norms else None
+
+    def _folded(self) -> list[tuple[Tensor, Tensor]]:
+        """Per layer, the qkv and gate|up weights with the input and
+        post-attention norm gains folded in (made on first use, shared by
+        every bucket of this executor)."""
+
+        if self._folded_weights is None:
+            self._folded_weights = [(fold_norm_gain(layer.qkv, layer.input_norm),
+                                     fold_norm_gain(layer.gate_up, layer.post_norm))
+                                    for layer in self.weights.layers]
+        return self._folded_weights
 
     @property
     def vocab_size(self) -> int:
@@ -867,7 +917,7 @@ class BucketedDecodeExecutor:
             self._buckets[key] = DecodeGraphBucket(
                 self.weights, self.cache, batch_capacity=batch_capacity,
                 context_capacity=context_capacity, token_state=self.token_state,
-                metrics=self._metrics)
+                metrics=self._metrics, folded=self._fold)
         return self._buckets[key]
 
     def _fallback_bucket(self, batch: int, context: int) -> DecodeGraphBucket:
@@ -882,7 +932,7 @@ class BucketedDecodeExecutor:
             self._fallbacks[key] = DecodeGraphBucket(
                 self.weights, self.cache, batch_capacity=capacity,
                 context_capacity=config.max_sequence_length, token_state=self.token_state,
-                graph=False, metrics=self._metrics)
+                graph=False, metrics=self._metrics, folded=self._fold)
         return self._fallbacks[key]
 
     def capture_all(self) -> None:

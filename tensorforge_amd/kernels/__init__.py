@@ -15,6 +15,7 @@ from tensorforge_amd.kernels.attention import (
 )
 from tensorforge_amd.kernels.cache_write import paged_kv_write_slots, paged_kv_write_token
 from tensorforge_amd.kernels.linear import (
+    fold_norm_gain,
     linear_partials,
     linear_partials_sum,
     linear_kstream,
@@ -53,6 +54,7 @@ __all__ = [
     "paged_kv_write_slots",
     "paged_kv_write_token",
     "embedding_rms_norm",
+    "fold_norm_gain",
     "residual_rms_norm",
     "rms_norm",
     "rope_paged_kv_append",

@@ -168,10 +168,23 @@ def linear_stream(x: Tensor, weight: Tensor, *, splits: int = 1, output: Tensor 
     return result
 
 
-def linear_kstream(x: Tensor, weight: Tensor, *, output: Tensor | None = None) -> Tensor:
+def linear_kstream(x: Tensor, weight: Tensor, *, output: Tensor | None = None,
+                   norm_eps: float | None = None, residual: Tensor | None = None) -> Tensor:
     """``x [m, k] @ weight[n, k].T`` for m <= 64 with K split over the four
-    wavefronts of 16-column workgroups, each staging its chunks through LDS
-    with whole-row loads (the form for weights with few 64-column tiles)."""
+    wavefronts of workgroups of one or two 16-column tiles, each staging its
+    chunks through LDS with whole-row loads (the form for weights with few
+    64-column tiles).
+
+    ``norm_eps``: the RMSNorm of x's rows applied to the product,
+    ``round(rsqrt(mean(x[r]^2) + eps) * (x[r] . weight[n]))``, for a weight
+    whose columns carry the norm's gain (:func:`fold_norm_gain`) -- the
+    reference's RMSNorm followed by the projection
+    (kernels/triton_ops.py:179-205; model/layers.py:88-95), with the gain
+    rounded into the weight instead of into the normalised input.
+
+    ``residual`` (``[m, n]``): the projection added to it,
+    ``round(round(x . weight) + residual)`` -- the residual sum of the
+    reference's residual_rms_norm (triton_ops.py:208-243), bit for bit."""
 
     if not _native.is_available():
         raise RuntimeError(
@@ -181,6 +194,8 @@ def linear_kstream(x: Tensor, weight: Tensor, *, output: Tensor | None = None) -
     if not linear_rows_supported(x, weight):
         raise ValueError("linear_kstream needs fp16/bf16 CUDA operands [m <= 64, k] and [n, k] "
                          "with k % 32 == 0 and 16-byte aligned contiguous rows")
+    if norm_eps is not None and residual is not None:
+        raise ValueError("linear_kstream takes norm_eps or residual, not both")
     m, k = x.shape
     n = weight.shape[0]
     if output is None:
@@ -188,27 +203,64 @@ def linear_kstream(x: Tensor, weight: Tensor, *, output: Tensor | None = None) -
     if (output.shape != (m, n) or output.dtype != x.dtype or output.device != x.device
             or output.stride(1) != 1):
         raise ValueError("output must be [m, n] with contiguous rows, x's dtype and device")
-    _native.check(
-        _native.library().tf_linear_kstream(
-            x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), output.data_ptr(),
-            output.stride(0), m, n, k, _native.dtype_code(x.dtype),
-            _native.current_stream(x.device),
-        ),
-        "linear_kstream",
-    )
+    library = _native.library()
+    stream = _native.current_stream(x.device)
+    if residual is not None:
+        if (residual.shape != (m, n) or residual.dtype != x.dtype
+                or residual.device != x.device or residual.stride(1) != 1):
+            raise ValueError("residual must be [m, n] with contiguous rows, x's dtype and device")
+        _native.check(
+            library.tf_linear_kstream_residual(
+                x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                residual.data_ptr(), residual.stride(0), output.data_ptr(), output.stride(0),
+                m, n, k, _native.dtype_code(x.dtype), stream,
+            ),
+            "linear_kstream_residual",
+        )
+    elif norm_eps is not None:
+        _native.check(
+            library.tf_linear_kstream_norm(
+                x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                output.data_ptr(), output.stride(0), m, n, k, float(norm_eps),
+                _native.dtype_code(x.dtype), stream,
+            ),
+            "linear_kstream_norm",
+        )
+    else:
+        _native.check(
+            library.tf_linear_kstream(
+                x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                output.data_ptr(), output.stride(0), m, n, k, _native.dtype_code(x.dtype),
+                stream,
+            ),
+            "linear_kstream",
+        )
     return output
 
 
+def fold_norm_gain(weight: Tensor, gain: Tensor) -> Tensor:
+    """``round(weight[n][k] * gain[k])`` in the weight's dtype: a projection
+    weight carrying the gain of the RMSNorm before it, for the ``norm_eps``
+    forms of :func:`linear_kstream` and :func:`linear_swiglu`."""
+
+    if gain.ndim != 1 or gain.shape[0] != weight.shape[1]:
+        raise ValueError("gain must have one element per weight column")
+    return (weight.float() * gain.float()).to(weight.dtype).contiguous()
+
+
 def linear_swiglu(x: Tensor, gate_up_weight: Tensor, *, output: Tensor | None = None,
-                  k_split: bool = False) -> Tensor:
+                  k_split: bool = False, norm_eps: float | None = None) -> Tensor:
     """``swiglu(x @ gate.T, x @ up.T)`` for m <= 64 rows, with
     ``gate_up_weight`` stacking the gate rows over the up rows (``[2I, k]``)
     -- the stacked projection and its activation in one launch.  The default
     form is bit-identical to :func:`linear_stream` of the stacked weight
     followed by ``swiglu_gate_up``; ``k_split=True`` splits K over the
-    wavefronts of 16-column workgroups (bit-identical to
-    :func:`linear_kstream` followed by ``swiglu_gate_up``).  Returns
-    ``[m, I]`` in ``output`` (allocated when None)."""
+    wavefronts of workgroups of one or two 16-column tiles (bit-identical to
+    :func:`linear_kstream` followed by ``swiglu_gate_up``).  ``norm_eps``
+    (with ``k_split``): the RMSNorm of x's rows applied to both products
+    before the activation, for a weight carrying the norm's gain
+    (:func:`fold_norm_gain`).  Returns ``[m, I]`` in ``output`` (allocated
+    when None)."""
 
     if not _native.is_available():
         raise RuntimeError(
@@ -218,6 +270,8 @@ def linear_swiglu(x: Tensor, gate_up_weight: Tensor, *, output: Tensor | None = 
     if not linear_rows_supported(x, gate_up_weight) or gate_up_weight.shape[0] % 2:
         raise ValueError("linear_swiglu needs fp16/bf16 CUDA operands [m <= 64, k] and a "
                          "stacked [2I, k] weight with k % 32 == 0 and 16-byte aligned rows")
+    if norm_eps is not None and not k_split:
+        raise ValueError("the norm_eps form of linear_swiglu is the K-split one")
     m, k = x.shape
     inter = gate_up_weight.shape[0] // 2
     if output is None:
@@ -225,13 +279,20 @@ def linear_swiglu(x: Tensor, gate_up_weight: Tensor, *, output: Tensor | None = 
     if (output.shape != (m, inter) or output.dtype != x.dtype or output.device != x.device
             or output.stride(1) != 1):
         raise ValueError("output must be [m, I] with contiguous rows, x's dtype and device")
+    library = _native.library()
+    args = (x.data_ptr(), x.stride(0), gate_up_weight.data_ptr(), gate_up_weight.stride(0),
+            output.data_ptr(), output.stride(0), m, inter, k)
+    if norm_eps is not None:
+        _native.check(
+            library.tf_linear_kswiglu_norm(*args, float(norm_eps), _native.dtype_code(x.dtype),
+                                           _native.current_stream(x.device)),
+            "linear_kswiglu_norm",
+        )
+        return output
     entry = "tf_linear_kswiglu" if k_split else "tf_linear_swiglu"
     _native.check(
-        getattr(_native.library(), entry)(
-            x.data_ptr(), x.stride(0), gate_up_weight.data_ptr(), gate_up_weight.stride(0),
-            output.data_ptr(), output.stride(0), m, inter, k, _native.dtype_code(x.dtype),
-            _native.current_stream(x.device),
-        ),
+        getattr(library, entry)(*args, _native.dtype_code(x.dtype),
+                                _native.current_stream(x.device)),
         entry,
     )
     return output

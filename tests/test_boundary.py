@@ -144,6 +144,15 @@ def test_c_abi_rejects_bad_arguments_before_launch(lib) -> None:
     status = lib.tf_paged_kv_write_slots(fake, fake, fake, fake, None, 3, 4, 64, 8, 16,
                                          _native.TF_DTYPE_BFLOAT16, stream)
     assert status == invalid and "slot mapping" in _error(lib)
+    status = lib.tf_linear_kstream_norm(fake, 64, fake, 64, fake, 64, 4, 64, 64, 0.0,
+                                        _native.TF_DTYPE_BFLOAT16, stream)
+    assert status == invalid and "eps" in _error(lib)
+    status = lib.tf_linear_kstream_residual(fake, 64, fake, 64, None, 64, fake, 64, 4, 64, 64,
+                                            _native.TF_DTYPE_BFLOAT16, stream)
+    assert status == invalid and "null" in _error(lib)
+    status = lib.tf_linear_kstream_residual(fake, 64, fake, 64, fake, 32, fake, 64, 4, 64, 64,
+                                            _native.TF_DTYPE_BFLOAT16, stream)
+    assert status == invalid and "residual row stride" in _error(lib)
     status = lib.tf_argmax_rows(fake, 0, 4, 0, _native.TF_DTYPE_BFLOAT16, fake, stream)
     assert status == invalid and "at least one column" in _error(lib)
     status = lib.tf_argmax_rows(fake, 10, 4, 16, _native.TF_DTYPE_BFLOAT16, fake, stream)

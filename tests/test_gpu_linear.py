@@ -255,3 +255,83 @@ def test_linear_partials_strided_x_and_rejections(device):
     with pytest.raises(ValueError):
         linear_partials(torch.randn(65, 64, dtype=torch.bfloat16, device=device),
                         w[:, :64], 1)
+
+
+def _rms_scale(x: torch.Tensor, eps: float) -> torch.Tensor:
+    return torch.rsqrt(x.float().pow(2).mean(dim=-1, keepdim=True) + eps)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 17, 33, 64])
+@pytest.mark.parametrize(("n", "k"), [(2560, 2048), (2048, 2048), (100, 96), (48, 800)])
+def test_linear_kstream_norm_is_the_norm_then_the_projection(device, dtype, rows, n, k):
+    """The RMSNorm of x's rows fused into the K-split projection, with the
+    norm gain folded into the weight: within the storage bar of
+    rsqrt(mean(x^2) + eps) * (x . w') in fp32, and of the reference's
+    unfused order (RMSNorm rounded to the storage type, then the
+    projection of the unfolded weight)."""
+
+    from tensorforge_amd.kernels import fold_norm_gain, linear_kstream, rms_norm
+
+    eps = 1e-5
+    generator = torch.Generator().manual_seed(rows * 7 + n + k)
+    x = (torch.randn(rows, k, generator=generator) * 3.0).to(dtype)
+    w = (torch.randn(n, k, generator=generator) * 0.02).to(dtype)
+    gain = (1.0 + 0.1 * torch.randn(k, generator=generator)).to(dtype)
+    folded = fold_norm_gain(w.to(device), gain.to(device))
+    assert torch.equal(folded.cpu(), (w.float() * gain.float()).to(dtype))
+    out = torch.full((rows, n + 8), float("nan"), dtype=dtype, device=device)
+    linear_kstream(x.to(device), folded, output=out[:, :n], norm_eps=eps)
+    got = out[:, :n].float().cpu()
+    assert bool(out[:, n:].isnan().all())
+    expected = _rms_scale(x, eps) * (x.float() @ folded.float().cpu().T)
+    tol = TOLERANCE[dtype]
+    torch.testing.assert_close(got, expected, rtol=tol, atol=tol * float(expected.abs().max()))
+    normed = rms_norm(x.to(device), gain.to(device), eps)
+    unfused = linear_kstream(normed, w.to(device)).float().cpu()
+    torch.testing.assert_close(got, unfused, rtol=2 * tol,
+                               atol=2 * tol * float(expected.abs().max()))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 33, 64])
+@pytest.mark.parametrize(("inter", "k"), [(5632, 2048), (4100, 256), (100, 800)])
+def test_linear_kswiglu_norm_is_the_norm_then_the_mlp_input(device, dtype, rows, inter, k):
+    from tensorforge_amd.kernels import fold_norm_gain, linear_swiglu
+
+    eps = 1e-5
+    generator = torch.Generator().manual_seed(rows * 11 + inter + k)
+    x = (torch.randn(rows, k, generator=generator) * 2.0).to(dtype)
+    w = (torch.randn(2 * inter, k, generator=generator) * 0.05).to(dtype)
+    gain = (1.0 + 0.1 * torch.randn(k, generator=generator)).to(dtype)
+    folded = fold_norm_gain(w.to(device), gain.to(device))
+    got = linear_swiglu(x.to(device), folded, k_split=True, norm_eps=eps).float().cpu()
+    gu = (_rms_scale(x, eps) * (x.float() @ folded.float().cpu().T)).to(dtype).float()
+    g, u = gu[:, :inter], gu[:, inter:]
+    expected = g * torch.sigmoid(g) * u
+    tol = TOLERANCE[dtype]
+    torch.testing.assert_close(got, expected, rtol=tol, atol=tol * float(expected.abs().max()))
+    with pytest.raises(ValueError, match="K-split"):
+        linear_swiglu(x.to(device), folded, norm_eps=eps)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 33, 64])
+@pytest.mark.parametrize(("n", "k"), [(2048, 2048), (2048, 5632), (100, 96)])
+def test_linear_kstream_residual_is_the_rounded_residual_sum(device, dtype, rows, n, k):
+    """round(round(x . w) + residual): the residual output of the
+    reference's residual_rms_norm over the projection, bit for bit."""
+
+    from tensorforge_amd.kernels import linear_kstream
+
+    generator = torch.Generator().manual_seed(rows * 13 + n + k)
+    x = torch.randn(rows, k, generator=generator).to(dtype).to(device)
+    w = (torch.randn(n, k, generator=generator) * 0.02).to(dtype).to(device)
+    residual = torch.randn(rows, n, generator=generator).to(dtype).to(device)
+    got = linear_kstream(x, w, residual=residual)
+    want = (linear_kstream(x, w).float() + residual.float()).to(dtype)
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    with pytest.raises(ValueError, match="not both"):
+        linear_kstream(x, w, residual=residual, norm_eps=1e-5)
+    with pytest.raises(ValueError, match="residual must be"):
+        linear_kstream(x, w, residual=residual[:, : n // 2])
