@@ -2,28 +2,31 @@
 
 The caller of the hot path (reference: runtime/decode_bucket.py:175-666).
 One decode step of a Llama-style decoder for up to ``batch_capacity``
-sequences runs as ONE captured HIP graph.  Per layer:
+sequences runs as ONE captured HIP graph.  Per layer, five launches:
 
-* ``rms_norm`` (first layer) or the fused ``residual_rms_norm``;
-* one fused QKV projection;
+* the fused QKV projection with the input RMSNorm applied to its products
+  (the norm gain folded into an executor-held copy of the weight);
 * RoPE on q and k, k and v into their pages, and
   ``paged_gqa_decode_attention`` (one pass for wide buckets, split-KV with
   its merge otherwise) -- one fused launch where the MFMA attention kernel
   serves the geometry, else ``rope_paged_kv_append`` then attention;
-* the output projection;
-* ``residual_rms_norm`` of (attention output, residual);
-* one fused gate|up projection, ``swiglu_gate_up``, the down projection.
+* the output projection added to the residual stream;
+* the fused gate|up projection with the post-attention RMSNorm and SwiGLU;
+* the down projection added to the residual stream;
+
+then the final RMSNorm, the LM head and the greedy argmax.  With
+``fuse_norms=False`` the norms run as launches of their own
+(``residual_rms_norm`` over split-K partials of the o and down
+projections).
 
 The gfx950 kernels of this package do the norm, cache and attention work
-and the projections (``_project`` and the bucket's o / down / gate|up
-launches: the K-split weight stream for qkv and for gate|up with its
-SwiGLU, LDS-staged slice sums for o and down, the weight stream for the LM
-head up to 32 rows); only the LM head of larger buckets is a library GEMM
-(torch -> hipBLASLt).  Every per-step input
-lives in one device "control" slab, filled from one pinned host slab with
-one asynchronous copy per step.  So the graph's addresses never change,
-and a step needs no host synchronisation beyond reading back the sampled
-tokens.
+and the projections (the K-split weight stream for qkv, o, gate|up and
+down, the weight stream for the LM head up to 32 rows); only the LM head of
+larger buckets is a library GEMM (torch -> hipBLASLt).  Every per-step
+input lives in one device "control" slab, filled from one pinned host slab
+with one asynchronous copy per step.  So the graph's addresses never
+change, and a step needs no host synchronisation beyond reading back the
+sampled tokens.
 
 Lanes past the live batch are padded: context length 0, masked cache
 write.  Their attention output is zero and their sampled token is ignored.
