@@ -20,4 +20,4 @@ void clear_error() { g_last_error[0] = '\0'; }
 
 extern "C" const char *tf_last_error(void) { return tf::g_last_error; }
 
-extern "C" int32_t tf_abi_version(void) { return 14; }
+extern "C" int32_t tf_abi_version(void) { return 15; }

@@ -88,7 +88,7 @@ def test_header_constants_match_the_python_binding() -> None:
 
 
 def test_abi_version_and_variant_selection(lib) -> None:
-    assert lib.tf_abi_version() == 14
+    assert lib.tf_abi_version() == 15
     variant = lib.tf_paged_gqa_decode_variant
     bf16, f16, f32 = (_native.TF_DTYPE_BFLOAT16, _native.TF_DTYPE_FLOAT16,
                       _native.TF_DTYPE_FLOAT32)
