@@ -346,7 +346,7 @@ __device__ __forceinline__ int kstream_lds_offset(int row, int piece) {
 //                 RMSNorm of x's rows applied to the product, for a weight
 //                 whose columns carry the norm's gain (w'[n][k] = w[n][k] g[k]);
 //                 each workgroup sees all of K, so the row sums of squares
-//                 come from the x chunks it stages anyway
+//                 come from the x operands it feeds the MFMAs anyway
 //   kEpiResidual  y = round(round(sum) + residual[r][n]): the projection
 //                 added to the residual stream, rounded as a separate add is
 enum KstreamEpi : int { kEpiPlain = 0, kEpiNorm = 1, kEpiResidual = 2 };
