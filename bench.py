@@ -268,7 +268,7 @@ def decode_step(lengths: list[int], cpu_seconds: float, with_cpu: bool) -> dict:
     the 22-layer TinyLlama-geometry model (random init, bf16) for the 64
     active rows of this workload, prompts of the workload's context lengths
     (less the steps decoded), context bucket 2048.  The CPU baseline is the
-    fp32 incremental decode step of the oracle on 4 of the rows."""
+    fp32 incremental decode step of the oracle on the same rows."""
 
     from tensorforge_amd.decode import DecoderWeights, tinyllama_config
     from tensorforge_amd.kernel_bench import measure_decode_step
@@ -291,13 +291,15 @@ def decode_step(lengths: list[int], cpu_seconds: float, with_cpu: bool) -> dict:
                   "launch/collect loop wall time per step",
     }
     if with_cpu:
-        result["cpu_baseline"] = decode_step_cpu_baseline(weights, active[:4], cpu_seconds)
+        result["cpu_baseline"] = decode_step_cpu_baseline(weights, prompts, cpu_seconds)
     return result
 
 
 def decode_step_cpu_baseline(weights, contexts: list[int], seconds: float) -> dict:
     """The oracle's fp32 incremental decode step (oracle/model.py) on the host
-    cores: 4 rows at their contexts, caches filled with random K/V."""
+    cores: every row at its context, caches filled with random K/V (one
+    K and one V buffer serve all layers: the step's arithmetic and reads
+    are the same, at a 22nd of the host memory)."""
 
     from oracle.model import decode_step_reference
     from tensorforge_amd.decode import DecoderWeights, LayerWeights
@@ -315,9 +317,10 @@ def decode_step_cpu_baseline(weights, contexts: list[int], seconds: float) -> di
     config = weights.config
     batch, capacity = len(contexts), max(contexts) + 64
     generator = torch.Generator().manual_seed(0)
-    keys = [torch.randn(batch, capacity, config.num_key_value_heads, config.head_dim,
-                        generator=generator) for _ in cpu.layers]
-    values = [torch.randn_like(k) for k in keys]
+    key = torch.randn(batch, capacity, config.num_key_value_heads, config.head_dim,
+                      generator=generator)
+    value = torch.randn_like(key)
+    keys, values = [key] * len(cpu.layers), [value] * len(cpu.layers)
     positions = torch.tensor(contexts)
     tokens = torch.randint(0, config.vocab_size, (batch,), generator=generator)
     decode_step_reference(cpu, keys, values, tokens, positions)  # warmup
@@ -337,7 +340,7 @@ def decode_step_cpu_baseline(weights, contexts: list[int], seconds: float) -> di
         "kind": "port",
         "sample": (
             f"oracle decode_step_reference (fp32 torch {torch.__version__}), 22 layers, "
-            f"{batch} of the 64 rows (contexts {contexts}), p50 of {len(samples)} steps = "
+            f"all {batch} rows (sum of contexts {sum(contexts)}), p50 of {len(samples)} steps = "
             f"{p50 * 1e3:.1f} ms; {cpu_model()}"
         ),
     }
