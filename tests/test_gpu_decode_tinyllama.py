@@ -41,7 +41,8 @@ pytestmark = pytest.mark.gpu
 BF16_22_LAYER_BOUND = 0.15
 
 
-def test_tinyllama_geometry_greedy_tokens_follow_the_oracle(device):
+@pytest.mark.parametrize("fuse_norms", [True, False], ids=["fused-norms", "norm-launches"])
+def test_tinyllama_geometry_greedy_tokens_follow_the_oracle(device, fuse_norms):
     config = tinyllama_config()
     weights = DecoderWeights.random(config, seed=0, dtype=torch.bfloat16, device=device)
     order = list(range(64))
@@ -52,16 +53,18 @@ def test_tinyllama_geometry_greedy_tokens_follow_the_oracle(device):
                            max_sequences=2, max_sequence_length=512, dtype=torch.bfloat16,
                            device=device),
         page_order=order)
-    executor = BucketedDecodeExecutor(weights, cache, batch_buckets=(2,), context_buckets=(512,))
+    executor = BucketedDecodeExecutor(weights, cache, batch_buckets=(2,), context_buckets=(512,),
+                                      fuse_norms=fuse_norms)
+    assert executor.bucket(2, 512).fused_norms == fuse_norms
     rng = random.Random(0)
     prompts = {"a": [rng.randrange(config.vocab_size) for _ in range(40)],
                "b": [rng.randrange(config.vocab_size) for _ in range(23)]}
     logits: dict[str, list[torch.Tensor]] = {}
     outputs = greedy_decode(executor, prompts, steps=8, logits=logits)
     fp32 = GreedyParity(weights, bound=BF16_22_LAYER_BOUND, device=device,
-                        name="TinyLlama 22 layers bf16 vs fp32 oracle")
+                        name=f"TinyLlama 22 layers bf16 ({'fused norms' if fuse_norms else 'norm launches'}) vs fp32 oracle")
     same = GreedyParity(weights, bound=BF16_22_LAYER_BOUND, device=device, dtype=torch.bfloat16,
-                        name="TinyLlama 22 layers bf16 vs bf16 restatement")
+                        name=f"TinyLlama 22 layers bf16 ({'fused norms' if fuse_norms else 'norm launches'}) vs bf16 restatement")
     for rid, prompt in prompts.items():
         assert len(outputs[rid]) == 8
         fp32.check(rid, prompt, outputs[rid], logits[rid])
