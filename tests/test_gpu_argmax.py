@@ -1,7 +1,7 @@
 """Greedy sampling on the device (tf_argmax_rows) against torch.argmax of
 the same values on the CPU, the reference's sampling rule
 (scheduler/continuous.py:265-275): bit-exact indices, including ties (the
-first index), NaN (the first NaN), rows of -inf, odd widths (the scalar
+first index), NaN (the first NaN), rows of -inf, zeros of either sign, odd widths (the scalar
 tail), several passes per row and strided rows."""
 
 from __future__ import annotations
@@ -32,7 +32,7 @@ def test_argmax_rows_matches_torch(device, dtype, rows, columns):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_argmax_rows_ties_nan_and_infinities(device, dtype):
     columns = 32000
-    values = torch.zeros(6, columns).to(dtype)
+    values = torch.zeros(8, columns).to(dtype)
     values[0, [5, 17, 31999]] = 3.0                 # ties: the first index
     values[1, [9000, 100]] = 7.0                    # ties across threads and passes
     values[2, [40, 20000]] = float("nan")           # the first NaN
@@ -40,8 +40,12 @@ def test_argmax_rows_ties_nan_and_infinities(device, dtype):
     values[3] = float("-inf")                       # all -inf: index 0
     values[4, 12345] = float("inf")
     values[5, -1] = 1e-3                            # the last column
+    values[6] = float("-inf")                       # +0 then -0: the first zero
+    values[6, 5], values[6, 10] = 0.0, -0.0
+    values[7] = float("-inf")                       # -0 then +0: the first zero
+    values[7, 5], values[7, 10] = -0.0, 0.0
     got = argmax_rows(values.to(device)).cpu()
-    assert got.tolist() == [5, 100, 40, 0, 12345, columns - 1]
+    assert got.tolist() == [5, 100, 40, 0, 12345, columns - 1, 5, 5]
     assert torch.equal(got, torch.argmax(values.float(), dim=-1))
 
 
