@@ -669,25 +669,35 @@ paged_decode_mfma_kernel(AttnParams p) {
     return;
   }
   if constexpr (ROPE) {
-    // The row's new token: every wavefront that streams writes the same
-    // rotated k and v into the token's page slot (identical bytes) and
-    // waits for its own stores before its first K/V load, so whichever
-    // wavefront reads that slot sees the token.  Lanes [0, D/8) rotate 8
-    // key elements each, lanes [D/8, D/4) copy 8 value elements.
+    // The row's new token: every wavefront writes the whole token row --
+    // rotated k and v of every kv head, the same bytes from every
+    // wavefront of the row -- and waits for its own stores before its
+    // first K/V load.  Any cache line of the row that a wavefront later
+    // reads (kv heads of 64 bytes or less share a line) then already holds
+    // the token in L2 when it reads it, whichever wavefront of the compute
+    // unit brought the line into L1.  Pieces [0, Hkv D/8) rotate 8 key
+    // elements each, the next Hkv D/8 copy 8 value elements.
     const int32_t page = p.append_pages[b];
     const int32_t off = p.append_offsets[b];
     const bool append = p.append_active[b] != 0 && page >= 0 && page < p.num_blocks && off >= 0 &&
                         off < p.block_size;
-    if (append && lane < D / 4) {
-      const int64_t slot = ((static_cast<int64_t>(page) * p.block_size + off) * p.kv_heads + kvh) * D;
-      if (lane < D / 8) {
-        const vec8 k = rotate8(rope_row + static_cast<int64_t>(p.query_heads + kvh) * D, 8 * lane);
-        *reinterpret_cast<vec8 *>(static_cast<T *>(const_cast<void *>(p.key_cache)) + slot + 8 * lane) = k;
-      } else {
-        const int e0 = 8 * (lane - D / 8);
-        const vec8 v = *reinterpret_cast<const vec8 *>(
-            rope_row + static_cast<int64_t>(p.query_heads + p.kv_heads + kvh) * D + e0);
-        *reinterpret_cast<vec8 *>(static_cast<T *>(const_cast<void *>(p.value_cache)) + slot + e0) = v;
+    if (append) {
+      const int64_t row0 = (static_cast<int64_t>(page) * p.block_size + off) * p.kv_heads * D;
+      const int32_t pieces = p.kv_heads * (D / 8);
+      for (int32_t i = lane; i < 2 * pieces; i += 64) {
+        const int32_t j = i < pieces ? i : i - pieces;
+        const int32_t h = j / (D / 8);
+        const int e0 = 8 * (j - h * (D / 8));
+        if (i < pieces) {
+          const vec8 k = rotate8(rope_row + static_cast<int64_t>(p.query_heads + h) * D, e0);
+          *reinterpret_cast<vec8 *>(static_cast<T *>(const_cast<void *>(p.key_cache)) + row0 +
+                                    static_cast<int64_t>(h) * D + e0) = k;
+        } else {
+          const vec8 v = *reinterpret_cast<const vec8 *>(
+              rope_row + static_cast<int64_t>(p.query_heads + p.kv_heads + h) * D + e0);
+          *reinterpret_cast<vec8 *>(static_cast<T *>(const_cast<void *>(p.value_cache)) + row0 +
+                                    static_cast<int64_t>(h) * D + e0) = v;
+        }
       }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -707,6 +717,12 @@ paged_decode_mfma_kernel(AttnParams p) {
   const unsigned char *kbytes = static_cast<const unsigned char *>(p.key_cache);
   const unsigned char *vbytes = static_cast<const unsigned char *>(p.value_cache);
   const int64_t head_bytes = static_cast<int64_t>(kvh) * D * sizeof(T);
+  // Stand-in row of absent tokens (read, masked out): this row's query
+  // input, at least D elements long.
+  const unsigned char *stand_in =
+      ROPE ? reinterpret_cast<const unsigned char *>(rope_row)
+           : static_cast<const unsigned char *>(p.query) +
+                 static_cast<int64_t>(b) * p.query_heads * D * sizeof(T);
   // Operand-layout loads: lane (l16, q4) reads 16 bytes of token l16.
   const uint32_t lane_full = static_cast<uint32_t>(l16) * token_bytes + 16u * q4;
   const uint32_t lane_first = 16u * q4;  // stand-in row for absent tokens
@@ -760,9 +776,15 @@ paged_decode_mfma_kernel(AttnParams p) {
       valid[j] = ntok >= 16 ? 0xffffu : ((1u << ntok) - 1u);
       const int32_t in_page = p.page_shift >= 0 ? (t0 & (p.block_size - 1))
                                                 : (t0 - (t0 / p.block_size) * p.block_size);
+      // Absent tiles read a stand-in row: the row's query (or QKV) input,
+      // which nothing writes while the kernel runs, so that a stand-in load
+      // never brings a cache page's line into L1 while another workgroup
+      // on this compute unit may be appending to it.
       const int64_t tile_off =
           tile_ok ? (static_cast<int64_t>(page) * p.block_size + in_page) * token_bytes + head_bytes
                   : 0;
+      const unsigned char *kp = tile_ok ? kbytes + tile_off : stand_in;
+      const unsigned char *vp = tile_ok ? vbytes + tile_off : stand_in;
       const uint32_t lane_off = l16 < ntok ? lane_full : lane_first;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -770,8 +792,8 @@ paged_decode_mfma_kernel(AttnParams p) {
         const uint32_t t_off =
             LINES ? (tt < ntok ? static_cast<uint32_t>(tt) * token_bytes : 0u) + v_piece
                   : lane_off + 64u * ks;
-        kf[j][ks] = load_stream16<vec8>(kbytes + tile_off + t_off);
-        vf[j][ks] = load_stream16<vec8>(vbytes + tile_off + t_off);
+        kf[j][ks] = load_stream16<vec8>(kp + t_off);
+        vf[j][ks] = load_stream16<vec8>(vp + t_off);
       }
     }
   };
