@@ -28,12 +28,14 @@ from oracle.reference import rms_norm_reference
 
 def rope_tables(head_dim: int, theta: float, positions: Tensor) -> tuple[Tensor, Tensor]:
     """cos/sin [len, head_dim] in fp32: angle(p, i) = p * theta^(-2i/D), the
-    half-dimension table repeated twice (layers.py:33-46)."""
+    half-dimension table repeated twice, computed as the reference computes
+    it (layers.py:33-46): inv_freq in fp32, the position/frequency outer
+    product in fp32, cos and sin of those fp32 angles."""
 
-    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float64) / head_dim))
-    angles = positions.double()[:, None] * inv_freq[None, :]
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    angles = torch.outer(positions.float(), inv_freq)
     angles = torch.cat((angles, angles), dim=-1)
-    return angles.cos().float(), angles.sin().float()
+    return angles.cos(), angles.sin()
 
 
 def rotate_half(x: Tensor) -> Tensor:

@@ -22,10 +22,16 @@ namespace tf {
 namespace {
 
 // Register-cache capacity (vectors per lane) of the norm kernels: 8 x 16-byte
-// vectors for the vector path, 16 scalars for odd widths; with 1024 lanes
-// both cover the 16384-column limit of the reference contract.
+// vectors for the vector path, 32 scalars for odd widths; with the largest
+// workgroup (kMaxNormThreads lanes) both cover the 16384-column limit of the
+// reference contract.
 template <int VEC>
-constexpr int max_vecs() { return VEC == 1 ? 16 : 8; }
+constexpr int max_vecs() { return VEC == 1 ? 32 : 8; }
+
+// Norm workgroups are 1, 2, 4 or 8 wavefronts: the reference's autotune
+// set for these kernels (tensorforge/kernels/triton_ops.py:28-33), which
+// its observability hook reports as `num_warps`.
+constexpr int kMaxNormThreads = 512;
 
 template <typename T, int VEC>
 struct alignas(sizeof(T) * VEC) Vec {
@@ -64,7 +70,7 @@ struct GatherRows {
 // norm) reads row id(b) of `inputs` -- an embedding table -- and also stores
 // that row to `residual_output`.
 template <typename T, int VEC, bool RESIDUAL, bool PARTIALS, bool GATHER = false>
-__global__ void __launch_bounds__(1024)
+__global__ void __launch_bounds__(kMaxNormThreads)
 rms_norm_kernel(const T *__restrict__ inputs, const T *__restrict__ residual,
                 const T *__restrict__ weight, T *__restrict__ residual_output,
                 T *__restrict__ output, int32_t columns, float eps,
@@ -209,16 +215,14 @@ void launch_norm(const void *inputs, const void *residual, const void *weight,
                  void *residual_output, void *output, int64_t rows, int32_t columns,
                  float eps, const float *partials, int32_t splits, hipStream_t stream,
                  const GatherRows *gather) {
-  constexpr int kMaxVecs = max_vecs<VEC>();
   const int32_t nvec = columns / VEC;
-  // Two vectors per lane where possible (one when the inputs are summed
-  // from split-K partials, which costs more loads per vector); the register
-  // cache holds kMaxVecs.
-  int threads = partials ? (nvec + 63) / 64 * 64 : ((nvec + 1) / 2 + 63) / 64 * 64;
-  const int min_threads = ((nvec + kMaxVecs - 1) / kMaxVecs + 63) / 64 * 64;
-  if (threads < min_threads) threads = min_threads;
-  if (threads < 64) threads = 64;
-  if (threads > 1024) threads = 1024;
+  // The fewest wavefronts (1, 2, 4 or 8) that leave each lane at most two
+  // vectors (one when the inputs are summed from split-K partials, which
+  // costs more loads per vector); wider rows give each of 8 wavefronts'
+  // lanes more vectors, up to the register cache's max_vecs<VEC>().
+  const int per_lane = partials ? 1 : 2;
+  int threads = 64;
+  while (threads < kMaxNormThreads && threads * per_lane < nvec) threads *= 2;
   const int64_t plane = rows * static_cast<int64_t>(columns);
   if (!RESIDUAL && gather)
     hipLaunchKernelGGL((rms_norm_kernel<T, VEC, false, false, true>), dim3(static_cast<unsigned>(rows)),
@@ -252,11 +256,11 @@ int32_t dispatch_norm(const void *inputs, const void *residual, const void *weig
     align |= reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(residual_output);
   if (gather) align |= reinterpret_cast<uintptr_t>(residual_output);
   const bool vectorised = columns % kVec == 0 && align % 16 == 0 &&
-                          columns / kVec <= 1024 * max_vecs<kVec>();
+                          columns / kVec <= kMaxNormThreads * max_vecs<kVec>();
   if (vectorised) {
     launch_norm<T, kVec, RESIDUAL>(inputs, residual, weight, residual_output, output, rows,
                                    columns, eps, partials, splits, stream, gather);
-  } else if (columns <= 1024 * max_vecs<1>()) {
+  } else if (columns <= kMaxNormThreads * max_vecs<1>()) {
     launch_norm<T, 1, RESIDUAL>(inputs, residual, weight, residual_output, output, rows,
                                 columns, eps, partials, splits, stream, gather);
   } else {

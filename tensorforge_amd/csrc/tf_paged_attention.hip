@@ -221,13 +221,15 @@ __device__ __forceinline__ T *output_row(const AttnParams &p, int32_t b, int32_t
 //    log-sum-exp and resets the counter to zero, leaving it ready for the
 //    next call (no memset, so the call is graph-replay safe).
 //
-// Cross-workgroup visibility without cache maintenance: partials are written
-// with agent-scope atomic stores, which on gfx950 write through the per-XCD
-// L2 to the coherent memory side; the workgroup waits for those stores to
-// complete before its single counter increment (an agent-scope atomic), and
-// the last workgroup reads the partials back with agent-scope atomic loads,
-// which bypass the non-coherent caches.  No agent-scope fence is issued: on a
-// multi-XCD part such a fence writes back and invalidates the whole L2.
+// Cross-workgroup ordering follows the HIP memory model at agent scope:
+// every lane stores its partials (agent-scope atomic stores) and issues an
+// agent-scope release fence before the workgroup barrier, so those stores
+// happen before thread 0's counter increment, itself an acquire-release RMW
+// at agent scope; the last arrival's threads pass a barrier and an
+// agent-scope acquire fence before reading any other workgroup's partials.
+// The fences write back / invalidate the per-XCD L2 (the price of formal
+// ordering on a multi-XCD part); this mode is opt-in and the default path
+// merges in a second launch instead.
 template <typename T, int MAXK, typename F>
 __device__ __forceinline__ void finish(const AttnParams &p, int32_t b, int32_t qh0,
                                        int32_t nheads, int64_t counter, int32_t split,
@@ -270,17 +272,21 @@ __device__ __forceinline__ void finish(const AttnParams &p, int32_t b, int32_t q
   if (!counters || direct) return;
 
   __shared__ int32_t is_last;
-  __builtin_amdgcn_s_waitcnt(0);  // this lane's partial stores have completed
-  __syncthreads();                // ... and so have every other lane's
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // this lane's partials, published
+  __syncthreads();                                    // ... and every other lane's
   if (threadIdx.x == 0) {
     int32_t *slot = p.split_counters + counter;
     const int32_t prev =
-        __hip_atomic_fetch_add(slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(slot, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     is_last = prev == nvalid - 1;
     if (is_last) __hip_atomic_store(slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!is_last) return;
+  // The other workgroups' partials happen before this point (their release,
+  // the counter RMW, thread 0's acquire, the barrier); make them visible to
+  // every lane of this one.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   // Merge: all loads of an item (nvalid <= 8 at a time) are issued before
   // any is used, so the merge costs one round trip per 8 splits.
   constexpr int kBatch = 8;
@@ -675,8 +681,18 @@ paged_decode_mfma_kernel(AttnParams p) {
     // first K/V load.  Any cache line of the row that a wavefront later
     // reads (kv heads of 64 bytes or less share a line) then already holds
     // the token in L2 when it reads it, whichever wavefront of the compute
-    // unit brought the line into L1.  Pieces [0, Hkv D/8) rotate 8 key
-    // elements each, the next Hkv D/8 copy 8 value elements.
+    // unit brought the line into L1: no wavefront loads a line of any
+    // appended row before its own wait (stand-in loads read the QKV row,
+    // and the chunk deal reads a row's new token only in that row's own
+    // wavefronts), the vector L1 is write-through, and L1 holds nothing
+    // from before the launch.  Pieces [0, Hkv D/8) rotate 8 key elements
+    // each, the next Hkv D/8 copy 8 value elements.
+    //
+    // Issuing a wavefront's first K/V chunks before this store (when they
+    // do not hold the new token) gave wrong results at head_dim 32 although
+    // no such load touches an appended line (tests/
+    // test_fused_append_schedule.py restates the addresses); the cause is
+    // not known, so loads stay after the wait.
     const int32_t page = p.append_pages[b];
     const int32_t off = p.append_offsets[b];
     const bool append = p.append_active[b] != 0 && page >= 0 && page < p.num_blocks && off >= 0 &&
@@ -700,7 +716,12 @@ paged_decode_mfma_kernel(AttnParams p) {
         }
       }
     }
+    // vmcnt counts stores on gfx9-family parts: after the wait this
+    // wavefront's stores have reached L2.  The empty asm statements are
+    // compiler memory barriers, so no load below is scheduled above it.
+    __asm__ volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0);
+    __asm__ volatile("" ::: "memory");
   }
   const int32_t s1 = min(s0 + split_size, ctx);
   // Wavefronts of the head that take chunks of this row: all WPH, or with a
@@ -1152,16 +1173,21 @@ paged_decode_mfma_kernel(AttnParams p) {
     __asm__ volatile("" ::: "memory");
   }
   if (!counters) return;
-  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's partial stores have completed
+  // Publish this wavefront's partials at agent scope before its counter
+  // increment (an acquire-release RMW); the last arrival acquires at agent
+  // scope before reading the other wavefronts' partials (the ordering of
+  // `finish` above, with the wavefront as the unit).
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   int32_t last = 0;
   if (lane == 0) {
     int32_t *slot = p.split_counters + static_cast<int64_t>(b) * p.kv_heads + kvh;
     const int32_t prev =
-        __hip_atomic_fetch_add(slot, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(slot, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     last = prev == nvalid - 1;
     if (last) __hip_atomic_store(slot, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (__builtin_amdgcn_readfirstlane(last) == 0) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   merge_head_partials<T, D>(p, b, kvh, nvalid, reinterpret_cast<float *>(vt),
                             kChunk * kRow / static_cast<int>(sizeof(float)));
 }

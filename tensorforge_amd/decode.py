@@ -166,11 +166,13 @@ class DecoderWeights:
                          down=normal(h, f))
             for _ in range(config.num_hidden_layers)
         ]
-        # RoPE tables: angles in fp64, cos/sin rounded once to the model dtype
-        # (the reference computes them in fp32 and casts, layers.py:43-46).
+        # RoPE tables as the reference builds them (layers.py:38-46): inv_freq
+        # and the position/frequency outer product in fp32, cos/sin of those
+        # fp32 angles rounded once to the model dtype.
         inv_freq = 1.0 / (config.rope_theta ** (
-            torch.arange(0, d, 2, dtype=torch.float64) / d))
-        angles = torch.arange(config.max_position_embeddings, dtype=torch.float64)[:, None] * inv_freq
+            torch.arange(0, d, 2, dtype=torch.float32) / d))
+        angles = torch.outer(torch.arange(config.max_position_embeddings, dtype=torch.float32),
+                             inv_freq)
         angles = torch.cat((angles, angles), dim=-1)
         return cls(config=config, embedding=normal(config.vocab_size, h), layers=layers,
                    final_norm=ones(h), lm_head=normal(config.vocab_size, h),
@@ -852,6 +854,13 @@ class BucketedDecodeExecutor:
         self._metrics = _MutableMetrics()
         self.step_records: list[DecodeStepRecord] = []
         self._folded_weights: list[tuple[Tensor, Tensor]] | None = None
+        self._folded_sources: list[Tensor] = []
+        self._folded_version = 0
+        # Requests whose logits every pipelined step copies to the host
+        # (``watch_logits``), per ring slot: pinned rows and the lanes held.
+        self.watch_logits: set[str] = set()
+        self._watch_host: list[Tensor | None] = [None] * self._RING
+        self._watch_lanes: list[list[tuple[int, str]]] = [[] for _ in range(self._RING)]
         # fuse_norms=False keeps the RMSNorm launches between the
         # projections (the split-K partials path) in every bucket.
         self._fold = self._folded if fuse_norms else None
@@ -865,7 +874,32 @@ class BucketedDecodeExecutor:
             self._folded_weights = [(fold_norm_gain(layer.qkv, layer.input_norm),
                                      fold_norm_gain(layer.gate_up, layer.post_norm))
                                     for layer in self.weights.layers]
+            self._folded_sources = [tensor for layer in self.weights.layers
+                                    for tensor in (layer.qkv, layer.input_norm, layer.gate_up,
+                                                   layer.post_norm)]
+            self._folded_version = sum(t._version for t in self._folded_sources)
         return self._folded_weights
+
+    def refresh_weights(self) -> bool:
+        """Remake the folded qkv and gate|up copies, in place (the captured
+        graphs keep their addresses), if a weight or norm gain they come from
+        was changed in place since they were made (``layer.qkv.copy_(...)``,
+        a reload into the same tensors: torch counts such writes in each
+        tensor's version, which only grows).  Called by ``launch`` before
+        every step (about 8 us of host time at 22 layers); returns whether
+        the copies were remade.  Weights replaced by new tensors are not seen
+        by graphs captured before; build a new executor for them."""
+
+        if self._folded_weights is None:
+            return False
+        version = sum(t._version for t in self._folded_sources)
+        if version == self._folded_version:
+            return False
+        for (qkv, gate_up), layer in zip(self._folded_weights, self.weights.layers):
+            qkv.copy_(fold_norm_gain(layer.qkv, layer.input_norm))
+            gate_up.copy_(fold_norm_gain(layer.gate_up, layer.post_norm))
+        self._folded_version = version
+        return True
 
     @property
     def vocab_size(self) -> int:
@@ -963,6 +997,7 @@ class BucketedDecodeExecutor:
         tokens = tokens or {}
         if not request_ids:
             raise ValueError("launch requires at least one request")
+        self.refresh_weights()
         slot = self._next_slot
         if self._busy[slot]:
             raise RuntimeError("too many decode steps launched without collect()")
@@ -1030,6 +1065,18 @@ class BucketedDecodeExecutor:
         end.record()
         lanes = len(staged)
         self._readback[slot][:lanes].copy_(self.token_state[:lanes], non_blocking=True)
+        watched = [(lane, request_id) for lane, request_id in enumerate(staged)
+                   if request_id in self.watch_logits]
+        if watched:
+            host = self._watch_host[slot]
+            if host is None or host.shape[0] < len(watched) or host.dtype != bucket.logits.dtype:
+                host = torch.empty((max(len(watched), 8), self.vocab_size),
+                                   dtype=bucket.logits.dtype, pin_memory=True)
+                self._watch_host[slot] = host
+            # Ordered on the stream before any later step rewrites the rows.
+            for index, (lane, _) in enumerate(watched):
+                host[index].copy_(bucket.logits[lane], non_blocking=True)
+        self._watch_lanes[slot] = watched
         copied.record()
         # Host bookkeeping only: the step's device work is ordered before any
         # later reader of these pages on this stream.
@@ -1059,6 +1106,19 @@ class BucketedDecodeExecutor:
                                                   bucket is not None and bucket.graph))
         self._busy[ticket.slot] = False
         return sampled
+
+    def watched_logits(self, ticket: DecodeTicket) -> dict[str, Tensor]:
+        """Host copies (the model dtype) of the logits behind a collected
+        step's tokens for its requests in ``watch_logits`` -- valid in the
+        pipelined mode too, where the bucket's own buffer has moved on.
+        Call after ``collect`` of the ticket and before its slot is reused
+        (``_RING`` launches later)."""
+
+        if ticket.slot < 0 or self._busy[ticket.slot]:
+            return {}
+        host = self._watch_host[ticket.slot]
+        return {request_id: host[index].clone()
+                for index, (_, request_id) in enumerate(self._watch_lanes[ticket.slot])}
 
     def logits_of(self, ticket: DecodeTicket) -> dict[str, Tensor]:
         """The collected step's logits per request: views into its bucket's

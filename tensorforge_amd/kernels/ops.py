@@ -77,15 +77,22 @@ def _output_or_empty(output: Tensor | None, reference: Tensor, name: str) -> Ten
     return output
 
 
-def _norm_config(columns: int, dtype: torch.dtype, aligned: bool) -> dict[str, Any]:
+def _norm_config(columns: int, dtype: torch.dtype, aligned: bool,
+                 per_lane: int = 2) -> dict[str, Any]:
+    """The norm kernels' launch shape, as ``launch_norm`` in
+    csrc/tf_fused_ops.hip picks it: 16-byte vectors where the row and every
+    pointer allow, and the fewest of 1, 2, 4 or 8 wavefronts (the
+    reference's autotune set, triton_ops.py:28-33) that leave each lane at
+    most ``per_lane`` vectors (1 when summing split-K partials)."""
+
     vector = 16 // torch.empty((), dtype=dtype).element_size()
     vectorised = aligned and columns % vector == 0
     width = vector if vectorised else 1
-    per_lane = 8 if vectorised else 16
     units = columns // width
-    threads = max(((units + 1) // 2 + 63) // 64 * 64, ((units + per_lane - 1) // per_lane + 63) // 64 * 64, 64)
-    threads = min(threads, 1024)
-    return {"kwargs": {"VECTOR": width}, "num_warps": threads // 64, "wave_size": 64}
+    warps = 1
+    while warps < 8 and warps * 64 * per_lane < units:
+        warps *= 2
+    return {"kwargs": {"VECTOR": width}, "num_warps": warps, "wave_size": 64}
 
 
 def _record(operation: str, key: tuple[Any, ...], config: dict[str, Any]) -> None:

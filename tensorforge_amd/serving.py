@@ -104,16 +104,24 @@ class ContinuousServer:
 
     def __init__(self, executor: BucketedDecodeExecutor, *, max_batch: int = 64,
                  max_prefill_tokens: int = 8192, progress_s: float = 5.0,
-                 logits: dict[str, list] | None = None) -> None:
+                 logits: dict[str, list] | None = None,
+                 watch: dict[str, list] | None = None) -> None:
         """``logits`` (a dict to fill, for checkers): every step is read back
         before the next is launched and the fp32 logits row behind each
-        sampled token is appended per request; the schedule is unchanged."""
+        sampled token is appended per request; the schedule is unchanged.
+
+        ``watch`` (a dict keyed by request id, for checkers of the pipelined
+        mode): the logits row behind each token of those requests is copied
+        to the host as the steps run (``BucketedDecodeExecutor.watch_logits``)
+        and appended to ``watch[request_id]`` in the model dtype; one step
+        stays in flight as in serving."""
 
         self.executor = executor
         self.max_batch = max_batch
         self.max_prefill_tokens = max_prefill_tokens
         self.progress_s = progress_s
         self.logits = logits
+        self.watch = watch
 
     def run(self, requests: list[RequestSpec]) -> list[RequestTrace]:
         executor = self.executor
@@ -128,6 +136,9 @@ class ContinuousServer:
         in_flight: DecodeTicket | None = None
         done = 0
         last_report = t0
+        watch = self.watch
+        if watch is not None:
+            executor.watch_logits = set(watch)
 
         def finish(request_id: str, now: int, error: str | None = None) -> None:
             nonlocal done
@@ -164,7 +175,18 @@ class ContinuousServer:
                 budget -= len(spec.prompt)
             host_tokens: dict[str, int] = {}
             if admitted:
-                if self.logits is None:
+                if self.logits is None and watch is not None and any(r in watch for r in admitted):
+                    result = executor.prefill_prompts(admitted)
+                    failed = dict(result.errors)
+                    ids = list(result.logits)
+                    first = {}
+                    if ids:
+                        stacked = torch.stack([result.logits[r] for r in ids])
+                        first = dict(zip(ids, torch.argmax(stacked, dim=-1).tolist()))
+                        for request_id in ids:
+                            if request_id in watch:
+                                watch[request_id].append(result.logits[request_id].cpu().clone())
+                elif self.logits is None:
                     first, failed = executor.prefill_tokens(admitted)
                 else:
                     result = executor.prefill_prompts(admitted)
@@ -216,9 +238,12 @@ class ContinuousServer:
             if in_flight is not None:
                 sampled = executor.collect(in_flight)
                 stamp = clock()
+                rows = executor.watched_logits(in_flight) if watch is not None else {}
                 for request_id, token in zip(in_flight.request_ids, sampled):
                     if request_id not in running:
                         continue  # failed in the step launched since
+                    if request_id in rows:
+                        watch[request_id].append(rows[request_id])
                     trace = traces[request_id]
                     trace.generated.append(token)
                     trace.token_ns.append(stamp)
@@ -234,6 +259,8 @@ class ContinuousServer:
                 print(f"[serve] {done}/{len(requests)} done, {len(running)} running, "
                       f"{len(queue)} queued, t={(last_report - t0) / 1e9:.1f}s",
                       file=sys.stderr, flush=True)
+        if watch is not None:
+            executor.watch_logits = set()
         return [traces[r.request_id] for r in requests]
 
 

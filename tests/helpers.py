@@ -54,21 +54,38 @@ class GreedyParity:
     measured e is checked against the stated bound and a flip at a larger
     margin fails (it would mean the sampled token is not the argmax of the
     device's own logits).  Without recorded logits the stated bound stands
-    in for e.  Flips are counted and printed either way (``pytest -rP``
-    shows them).
+    in for e.  ``max_flip_rate`` caps the share of flipped tokens (0 makes
+    the check one of identity).  Flips are counted and printed either way
+    (``pytest -rP`` shows them), and every failure message carries the
+    counts.
     """
 
-    def __init__(self, weights, *, bound: float, device="cpu", dtype=torch.float32,
-                 name: str = "") -> None:
+    def __init__(self, weights, *, bound: float | None = None, device="cpu",
+                 dtype=torch.float32, name: str = "", max_flip_rate: float | None = None,
+                 tolerance: tuple[float, float] | None = None) -> None:
+        """``bound``: the stated largest |device logit - oracle logit|; or
+        ``tolerance=(atol, rtol)``: the bound is ``atol + rtol * L`` with L
+        the largest |oracle logit| of the checked rows (a reference-style
+        tolerance at the run's own logit magnitude)."""
+
+        if (bound is None) == (tolerance is None):
+            raise ValueError("give either bound or tolerance")
         self.weights = weights
-        self.bound = bound
+        self._bound = bound
+        self.tolerance = tolerance
+        self.max_logit = 0.0
         self.device = device
         self.dtype = dtype
         self.name = name
+        # Flip budget: at most this fraction of the checked tokens may
+        # differ from the oracle's argmax (None: no budget beyond the margin
+        # rule; 0: identity).
+        self.max_flip_rate = max_flip_rate
         self.flips: list[tuple] = []
         self.tokens = 0
         self.max_dlogit = 0.0
         self.min_margin = float("inf")
+        self.margins: list[float] = []  # the oracle's top-two margin at every token
 
     def check(self, request_id, prompt, generated, logits=None) -> None:
         from oracle.model import decoder_forward
@@ -77,6 +94,7 @@ class GreedyParity:
         expected = decoder_forward(self.weights, tokens, device=self.device, dtype=self.dtype)
         rows = expected[len(prompt) - 1:]
         assert rows.shape[0] == len(generated)
+        self.max_logit = max(self.max_logit, float(rows.abs().max()))
         if logits is not None:
             got = torch.stack([row.float().cpu() for row in logits])
             assert got.shape == rows.shape
@@ -85,20 +103,53 @@ class GreedyParity:
             row = rows[step]
             top = torch.topk(row, 2).values
             self.min_margin = min(self.min_margin, float(top[0] - top[1]))
+            self.margins.append(float(top[0] - top[1]))
             best = int(torch.argmax(row))
             self.tokens += 1
             if token != best:
                 self.flips.append((request_id, step, int(token), best, float(row[best] - row[token])))
 
-    def finish(self) -> None:
+    @property
+    def bound(self) -> float:
+        if self._bound is not None:
+            return self._bound
+        atol, rtol = self.tolerance
+        return atol + rtol * self.max_logit
+
+    def summary(self) -> dict:
+        """Counts of the run so far: tokens, flips, the flip rate, the
+        largest flip margin, the measured logit deviation, and how many
+        tokens had an oracle margin within twice it (the only places a flip
+        is allowed)."""
+
         measured = self.max_dlogit if self.max_dlogit > 0 else None
         e = measured if measured is not None else self.bound
-        print(f"[greedy parity] {self.name}: {self.tokens} tokens, {len(self.flips)} flips "
-              f"{[(r, s, round(m, 5)) for r, s, _, _, m in self.flips]}, max |dlogit| "
-              f"{measured if measured is None else round(measured, 5)} (stated bound "
-              f"{self.bound}), smallest oracle top-two margin {self.min_margin:.5f}")
+        return {
+            "tokens": self.tokens,
+            "flips": len(self.flips),
+            "flip_rate": round(len(self.flips) / max(self.tokens, 1), 5),
+            "largest_flip_margin": round(max((f[4] for f in self.flips), default=0.0), 5),
+            "max_dlogit": None if measured is None else round(measured, 5),
+            "near_ties": sum(1 for m in self.margins if m <= 2 * e),
+            "smallest_margin": round(self.min_margin, 6),
+            "max_abs_oracle_logit": round(self.max_logit, 4),
+            "logit_bound": round(self.bound, 5),
+        }
+
+    def finish(self) -> dict:
+        measured = self.max_dlogit if self.max_dlogit > 0 else None
+        e = measured if measured is not None else self.bound
+        summary = self.summary()
+        text = (f"[greedy parity] {self.name}: {summary} (stated logit bound {self.bound}, "
+                f"flip budget {self.max_flip_rate}); flips (request, step, margin): "
+                f"{[(r, s, round(m, 5)) for r, s, _, _, m in self.flips][:40]}")
+        print(text)
         if measured is not None:
             assert measured <= self.bound, (
-                f"{self.name}: max |dlogit| {measured:.4e} exceeds the stated bound {self.bound}")
+                f"max |dlogit| {measured:.4e} exceeds the stated bound {self.bound}: {text}")
         wide = [f for f in self.flips if f[4] > 2 * e]
-        assert not wide, f"{self.name}: flips at margins above 2 x {e:.4e}: {wide}"
+        assert not wide, f"flips at margins above 2 x {e:.4e}: {wide}: {text}"
+        if self.max_flip_rate is not None:
+            assert len(self.flips) <= self.max_flip_rate * self.tokens, (
+                f"flip rate above the budget {self.max_flip_rate}: {text}")
+        return summary

@@ -224,6 +224,59 @@ def test_autotune_hooks_reject_unknown_operations() -> None:
         assert autotune_cache_size(operation) >= 0
 
 
+def test_norm_launch_shapes_stay_in_the_reference_autotune_set() -> None:
+    """The recorded norm launch uses 1, 2, 4 or 8 wavefronts at every width
+    (triton_ops.py:28-33) and still holds the row in the register cache
+    (8 vectors per lane, 32 scalars)."""
+
+    from tensorforge_amd.kernels.ops import _norm_config
+
+    for dtype in (torch.float32, torch.float16, torch.bfloat16):
+        for aligned in (True, False):
+            for per_lane in (1, 2):
+                for columns in list(range(1, 1100, 7)) + [2048, 4096, 8192, 16383, 16384]:
+                    config = _norm_config(columns, dtype, aligned, per_lane)
+                    assert config["num_warps"] in {1, 2, 4, 8}, (columns, dtype)
+                    width = config["kwargs"]["VECTOR"]
+                    capacity = 32 if width == 1 else 8
+                    assert config["num_warps"] * 64 * capacity * width >= columns
+    assert _norm_config(513, torch.float16, True)["num_warps"] == 8
+    assert _norm_config(2048, torch.bfloat16, True)["num_warps"] == 2
+    assert _norm_config(4096, torch.bfloat16, True)["num_warps"] == 4
+
+
+def test_reference_module_paths_resolve_with_the_reference_names() -> None:
+    """A caller's `from tensorforge.kernels.<module> import <names>` keeps
+    working with only the package prefix changed (the names each reference
+    caller imports: runtime/decode_bucket.py:17-22, runtime/batched_decode.py:13,
+    runtime/triton_model.py:11, benchmark/attention_benchmark.py:23-27,
+    benchmark/kernel_benchmark.py:27-32)."""
+
+    import importlib
+
+    expected = {
+        "triton_attention": ("PagedAttentionWorkspace", "is_triton_attention_available",
+                             "paged_gqa_decode_attention", "selected_attention_autotune_config"),
+        "triton_ops": ("autotune_cache_size", "is_triton_available", "residual_rms_norm",
+                       "rms_norm", "selected_autotune_config", "swiglu"),
+        "triton_cache": ("paged_kv_write_token",),
+    }
+    from tensorforge_amd import kernels
+
+    for module_name, names in expected.items():
+        module = importlib.import_module(f"tensorforge_amd.kernels.{module_name}")
+        for name in names:
+            assert callable(getattr(module, name)), (module_name, name)
+            public = getattr(kernels, name, None)
+            if public is not None:
+                assert getattr(module, name) is public, (module_name, name)
+    from tensorforge_amd.kernels.triton_attention import is_triton_attention_available
+    from tensorforge_amd.kernels.triton_ops import is_triton_available
+
+    assert is_triton_available() is _native.is_available()
+    assert is_triton_attention_available() is _native.is_available()
+
+
 def test_split_size_setting_is_validated_and_restorable() -> None:
     previous = set_attention_split_size(512)
     try:

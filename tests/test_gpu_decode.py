@@ -122,11 +122,28 @@ def test_greedy_decode_matches_the_oracle(device):
     logits: dict[str, list[torch.Tensor]] = {}
     recorded = greedy_decode(recorder, prompts, steps=32, logits=logits)
     assert recorded == outputs
-    parity = GreedyParity(weights, bound=FP16_BOUND, name="cfg1 fp16 b4 x 32 steps")
+    # BASELINE config 1 is a gate of identity: against the fp32 oracle
+    # teacher-forced on the run's tokens, no flip at all ...
+    parity = GreedyParity(weights, bound=FP16_BOUND, name="cfg1 fp16 b4 x 32 steps",
+                          max_flip_rate=0.0)
     for rid, prompt in prompts.items():
         assert len(outputs[rid]) == 32
         parity.check(rid, prompt, outputs[rid], logits[rid])
     parity.finish()
+    # ... and the reference's own assertion form
+    # (tests/test_gpu_continuous_scheduler.py:60-72): an independent
+    # free-running greedy generation in the same precision (the model
+    # restated in fp16 torch math on the GPU, full prefix every step, its
+    # argmax fed back) gives the same token tuples.
+    for rid, prompt in prompts.items():
+        sequence = list(prompt)
+        expected = []
+        for _ in range(32):
+            row = decoder_forward(weights, torch.tensor(sequence), device=device,
+                                  dtype=torch.float16)[-1]
+            expected.append(int(torch.argmax(row)))
+            sequence.append(expected[-1])
+        assert tuple(outputs[rid]) == tuple(expected), (rid, outputs[rid], expected)
 
 
 def test_changing_batches_feed_tokens_back_by_lane(device):
@@ -358,3 +375,50 @@ def test_a_bad_token_or_an_exhausted_cache_fails_only_its_request(device):
     assert not ok.errors
     expected = decoder_forward(weights, torch.tensor(prompts["b"] + [first["b"]]))[-1]
     assert float((ok.logits["b"].float().cpu() - expected).abs().max()) <= FP16_BOUND
+
+
+def test_in_place_weight_updates_reach_the_folded_decode_weights(device):
+    """The default decode chain reads executor-held copies of the qkv and
+    gate|up weights with the norm gains folded in.  Weights and gains
+    changed in place after the first step (a reload into the same tensors)
+    are folded again before the next launch, in place, so the captured
+    graphs see them: the norm-fused executor then follows one that applies
+    the norms as launches (no copies) on the same weights, while a copy
+    left stale (refresh disabled) does not."""
+
+    config = small_config()
+    weights = DecoderWeights.random(config, seed=4, dtype=torch.float16, device=device)
+    prompts = {rid: p for rid, p in list(_prompts().items())[:2]}
+    runs = {}
+    for name in ("fused", "launches", "stale"):
+        _, executor = _executor(config, weights, device, batch_buckets=(2,),
+                                context_buckets=(512,))
+        if name == "launches":
+            executor = BucketedDecodeExecutor(weights, executor.cache, batch_buckets=(2,),
+                                              context_buckets=(512,), fuse_norms=False)
+        if name == "stale":
+            executor.refresh_weights = lambda: False
+        runs[name] = executor
+    assert runs["fused"].bucket(2, 512).fused_norms
+    assert not runs["launches"].bucket(2, 512).fused_norms
+    first = {name: _prefilled(executor, prompts) for name, executor in runs.items()}
+    assert first["fused"] == first["launches"] == first["stale"]
+    step1 = {name: executor.append_tokens(first[name]) for name, executor in runs.items()}
+    tokens = {rid: int(torch.argmax(step1["launches"].logits[rid])) for rid in prompts}
+    generator = torch.Generator().manual_seed(8)
+    with torch.no_grad():
+        for layer in weights.layers:
+            layer.input_norm.mul_(1.5)
+            layer.post_norm.copy_((1 + 0.3 * torch.randn(layer.post_norm.shape,
+                                                         generator=generator)).to(device))
+            layer.qkv.mul_(0.8)
+            layer.gate_up.add_((0.01 * torch.randn(layer.gate_up.shape,
+                                                   generator=generator)).to(device))
+    step2 = {name: executor.append_tokens(tokens) for name, executor in runs.items()}
+    assert not runs["fused"].refresh_weights()  # the launch already folded them again
+    for rid in prompts:
+        fused = step2["fused"].logits[rid].float().cpu()
+        launches = step2["launches"].logits[rid].float().cpu()
+        stale = step2["stale"].logits[rid].float().cpu()
+        assert float((fused - launches).abs().max()) <= FP16_BOUND, rid
+        assert float((stale - launches).abs().max()) > 10 * FP16_BOUND, rid

@@ -5,7 +5,8 @@ steps, read back step by step with their logits.
 Two gates (``tests.helpers.GreedyParity``):
 
 * the fp32 decoder oracle, teacher-forced on the run's own tokens: the
-  largest logit deviation must stay within the stated bf16 bound, and a
+  largest logit deviation must stay within the reference's bf16 tolerance
+  at the run's largest |logit| (3e-2 + 3e-2 L), and a
   token may differ from the oracle's argmax only where the oracle's top-two
   margin is within twice the measured deviation (the reference's margin
   rule, tests/test_triton_model.py:38-43);
@@ -13,8 +14,9 @@ Two gates (``tests.helpers.GreedyParity``):
   every operand and intermediate in bf16), the same rule against its own
   measured deviation.
 
-The flip counts, the measured deviations and the smallest margins are
-printed (``pytest -rP``).
+Each gate also caps the share of flipped tokens (``MAX_FLIP_RATE``).  The
+flip counts, the measured deviations and the smallest margins are printed
+(``pytest -rP``) and carried by every failure message.
 """
 
 from __future__ import annotations
@@ -35,10 +37,16 @@ from tests.helpers import GreedyParity
 
 pytestmark = pytest.mark.gpu
 
-# Largest |device logit - oracle logit| allowed over 22 bf16 layers, whose
-# logits reach |4|: the reference's bf16 tolerance, 3e-2 absolute plus 3e-2
-# relative (tests/test_triton_model.py:37), at that magnitude.
-BF16_22_LAYER_BOUND = 0.15
+# Largest |device logit - oracle logit| allowed over 22 bf16 layers: the
+# reference's bf16 tolerance, 3e-2 absolute plus 3e-2 relative
+# (tests/test_triton_model.py:37), at the largest |logit| of the checked
+# rows (about 4-5 for this random-init model: a bound near 0.15).
+BF16_22_LAYER_TOLERANCE = (3e-2, 3e-2)
+# Share of tokens that may differ from the oracle's argmax at 22 bf16
+# layers, each only at an oracle margin within twice the measured logit
+# deviation: random-init weights leave many near-ties (smallest top-two
+# margins 1e-4..7e-3), and the serving runs measured 5.7-5.9% such flips.
+MAX_FLIP_RATE = 0.08
 
 
 @pytest.mark.parametrize("fuse_norms", [True, False], ids=["fused-norms", "norm-launches"])
@@ -61,9 +69,11 @@ def test_tinyllama_geometry_greedy_tokens_follow_the_oracle(device, fuse_norms):
                "b": [rng.randrange(config.vocab_size) for _ in range(23)]}
     logits: dict[str, list[torch.Tensor]] = {}
     outputs = greedy_decode(executor, prompts, steps=8, logits=logits)
-    fp32 = GreedyParity(weights, bound=BF16_22_LAYER_BOUND, device=device,
+    fp32 = GreedyParity(weights, tolerance=BF16_22_LAYER_TOLERANCE, device=device,
+                        max_flip_rate=MAX_FLIP_RATE,
                         name=f"TinyLlama 22 layers bf16 ({'fused norms' if fuse_norms else 'norm launches'}) vs fp32 oracle")
-    same = GreedyParity(weights, bound=BF16_22_LAYER_BOUND, device=device, dtype=torch.bfloat16,
+    same = GreedyParity(weights, tolerance=BF16_22_LAYER_TOLERANCE, device=device, dtype=torch.bfloat16,
+                        max_flip_rate=MAX_FLIP_RATE,
                         name=f"TinyLlama 22 layers bf16 ({'fused norms' if fuse_norms else 'norm launches'}) vs bf16 restatement")
     for rid, prompt in prompts.items():
         assert len(outputs[rid]) == 8

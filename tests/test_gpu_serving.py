@@ -1,30 +1,39 @@
-"""Continuous batching of the config-5 model on the GPU, at reduced size.
+"""Continuous batching of the config-5 model on the GPU.
 
 The 22-layer TinyLlama-geometry decoder (random init, seed 0, bf16) serves
-40 requests through ``serving.ContinuousServer`` over the graph-bucketed
-executor: 36 arrive at once and 4 later (Poisson gaps), prompts of
-16..600 tokens, outputs of 8..30 tokens.  So the running batch passes
-through every batch bucket {1, 2, 4, 8, 16, 32, 64} and contexts cross
-from the 512- into the 1024-token bucket, with requests joining, leaving
-and changing lanes while one step stays in flight.
+requests through ``serving.ContinuousServer`` over the graph-bucketed
+executor, in two tests:
 
-Every request's tokens are checked against the fp32 decoder oracle,
-teacher-forced on the run's own tokens (the reference checks its
-scheduler's tokens against full-prefix greedy generation,
-tests/test_gpu_continuous_scheduler.py:20-77).  The run is made twice:
-pipelined (one step in flight, the serving mode), where a token may differ
-from the oracle's argmax only where the oracle's top-two margin is within
-twice the stated bf16 logit bound; and with every step read back with its
-logits, where the largest logit deviation of that same run is measured,
-must be within the stated bound, and a token may differ only where the
-margin is within twice that measured deviation.  At the end of each run
-every page and sequence slot is back in the pool.
+* BASELINE config 5 at its stated size: 512 requests, Poisson arrivals at
+  20 req/s, prompts lognormal (median 256) clipped to [16, 2048], outputs
+  uniform in [64, 512], at most 64 running, batch buckets 1..64 and context
+  buckets 512..4096 -- then the same 512 requests arriving at once (burst),
+  which fills the batch to 64 and drains it through every batch bucket.
+  Checked: every request completes with its token count and no error, no
+  step falls back to eager buffers, every page and sequence slot is back
+  in the pool, every bucket the run needs is captured once; and a seeded
+  subset of 32 requests (the longest prompt, the longest output and the
+  longest context among them) against the fp32 decoder oracle, with the
+  logits behind their tokens copied out of the pipelined run itself.
+* A reduced run (40 requests, prompts <= 600, outputs <= 30) checked in
+  full against the oracle, pipelined and with every step read back.
+
+Tokens are checked against the fp32 decoder oracle teacher-forced on the
+run's own tokens (the reference checks its scheduler's tokens against
+full-prefix greedy generation, tests/test_gpu_continuous_scheduler.py:20-77)
+with ``tests.helpers.GreedyParity``: the largest logit deviation must be
+within the reference's bf16 tolerance (3e-2 + 3e-2 x the run's largest
+|logit|), a token may differ from the oracle's argmax
+only where the oracle's top-two margin is within twice that measured
+deviation, and at most MAX_FLIP_RATE of the tokens may differ.
 """
 
 from __future__ import annotations
 
 import dataclasses
+import json
 import random
+import warnings
 
 import numpy as np
 import pytest
@@ -36,9 +45,15 @@ from tensorforge_amd.decode import (
     DecoderWeights,
     tinyllama_config,
 )
-from tensorforge_amd.serving import ContinuousServer, RequestSpec, summarize
+from tensorforge_amd.serving import (
+    ContinuousServer,
+    RequestSpec,
+    build_executor,
+    summarize,
+    synthetic_requests,
+)
 from tests.helpers import GreedyParity
-from tests.test_gpu_decode_tinyllama import BF16_22_LAYER_BOUND
+from tests.test_gpu_decode_tinyllama import BF16_22_LAYER_TOLERANCE, MAX_FLIP_RATE
 
 pytestmark = pytest.mark.gpu
 
@@ -60,7 +75,7 @@ def _requests(vocab: int) -> list[RequestSpec]:
             for i, (n, o, a) in enumerate(zip(prompts, outputs, arrivals))]
 
 
-def _serve(weights, device, requests, logits=None):
+def _serve(weights, device, requests, logits=None, watch=None):
     config = weights.config
     pages = 64 * (1024 // 16)
     order = list(range(pages))
@@ -73,7 +88,8 @@ def _serve(weights, device, requests, logits=None):
         page_order=order)
     executor = BucketedDecodeExecutor(weights, cache, batch_buckets=BATCH_BUCKETS,
                                       context_buckets=CONTEXT_BUCKETS)
-    traces = ContinuousServer(executor, max_batch=64, progress_s=0, logits=logits).run(requests)
+    traces = ContinuousServer(executor, max_batch=64, progress_s=0, logits=logits,
+                              watch=watch).run(requests)
     assert all(t.error is None for t in traces), [t.error for t in traces if t.error]
     stats = cache.stats()
     assert stats.active_sequences == 0 and stats.used_blocks == 0 and stats.reserved_tokens == 0
@@ -96,7 +112,8 @@ def test_continuous_batching_over_every_bucket_follows_the_oracle(device):
     config = tinyllama_config()
     weights = DecoderWeights.random(config, seed=0, dtype=torch.bfloat16, device=device)
     requests = _requests(config.vocab_size)
-    executor, traces = _serve(weights, device, requests)
+    watched: dict[str, list[torch.Tensor]] = {r.request_id: [] for r in requests}
+    executor, traces = _serve(weights, device, requests, watch=watched)
 
     # Every request served in full.
     for spec, trace in zip(requests, traces):
@@ -111,20 +128,95 @@ def test_continuous_batching_over_every_bucket_follows_the_oracle(device):
     print(f"[serving] {summary['requests']} requests, {summary['generated_tokens']} tokens, "
           f"{summary['decode_steps']} decode steps, buckets {sorted(used)}")
 
-    # Tokens against the fp32 oracle (run on the GPU; weights converted once).
+    # Tokens against the fp32 oracle (run on the GPU; weights converted once),
+    # with the logits of the pipelined run copied out as it ran.
     fp32 = _fp32(weights)
-    parity = GreedyParity(fp32, bound=BF16_22_LAYER_BOUND, device=device,
+    parity = GreedyParity(fp32, tolerance=BF16_22_LAYER_TOLERANCE, device=device,
+                          max_flip_rate=MAX_FLIP_RATE,
                           name="cfg5 serving (pipelined), 40 requests, buckets 1..64")
     for spec, trace in zip(requests, traces):
-        parity.check(spec.request_id, spec.prompt, trace.generated)
+        rows = watched[spec.request_id]
+        assert len(rows) == len(trace.generated) == spec.max_new_tokens
+        parity.check(spec.request_id, spec.prompt, trace.generated, rows)
     parity.finish()
 
     # The same requests with every step read back with its logits.
     logits: dict[str, list[torch.Tensor]] = {}
     _, recorded = _serve(weights, device, requests, logits=logits)
-    measured = GreedyParity(fp32, bound=BF16_22_LAYER_BOUND, device=device,
+    measured = GreedyParity(fp32, tolerance=BF16_22_LAYER_TOLERANCE, device=device,
+                            max_flip_rate=MAX_FLIP_RATE,
                             name="cfg5 serving (logits recorded), 40 requests")
     for spec, trace in zip(requests, recorded):
         assert len(trace.generated) == spec.max_new_tokens == len(logits[spec.request_id])
         measured.check(spec.request_id, spec.prompt, trace.generated, logits[spec.request_id])
     measured.finish()
+
+
+def _subset(requests: list[RequestSpec], count: int = 32) -> list[str]:
+    """A seeded subset of ``count`` requests that holds the longest prompt,
+    the longest output and the longest context of the run."""
+
+    chosen = {max(requests, key=lambda r: len(r.prompt)).request_id,
+              max(requests, key=lambda r: r.max_new_tokens).request_id,
+              max(requests, key=lambda r: len(r.prompt) + r.max_new_tokens).request_id}
+    rng = random.Random(0)
+    others = [r.request_id for r in requests if r.request_id not in chosen]
+    chosen.update(rng.sample(others, count - len(chosen)))
+    return sorted(chosen)
+
+
+def test_config5_at_its_stated_size_poisson_then_burst(device):
+    config = tinyllama_config()
+    executor = build_executor(config, max_batch=64, seed=0)
+    requests = synthetic_requests(512, rate=20.0, vocab_size=config.vocab_size, seed=0)
+    assert len(requests) == 512
+    assert max(len(r.prompt) for r in requests) <= 2048
+    assert {r.max_new_tokens for r in requests} <= set(range(64, 513))
+    subset = _subset(requests)
+    fp32 = _fp32(executor.weights)
+    cache = executor.cache
+    reports = {}
+    used_batches: set[int] = set()
+    used_contexts: set[int] = set()
+    for mode, burst in (("poisson 20 req/s", False), ("burst", True)):
+        specs = synthetic_requests(512, rate=20.0, vocab_size=config.vocab_size, seed=0,
+                                   burst=burst)
+        executor.step_records.clear()
+        watched: dict[str, list[torch.Tensor]] = {rid: [] for rid in subset}
+        print(f"[cfg5 full] {mode}: serving 512 requests", flush=True)
+        traces = ContinuousServer(executor, max_batch=64, progress_s=10,
+                                  watch=watched).run(specs)
+        failed = [(t.request_id, t.error) for t in traces if t.error is not None]
+        assert not failed, failed[:5]
+        for spec, trace in zip(specs, traces):
+            assert len(trace.generated) == spec.max_new_tokens, spec.request_id
+        stats = cache.stats()
+        assert stats.active_sequences == 0 and stats.used_blocks == 0
+        assert stats.reserved_tokens == 0
+        metrics = executor.metrics()
+        assert metrics.shape_fallbacks == 0 and metrics.eager_fallback_calls == 0
+        used = {record.bucket for record in executor.step_records}
+        used_batches |= {b for b, _ in used}
+        used_contexts |= {c for _, c in used}
+        summary = summarize(traces, executor)
+        print(f"[cfg5 full] {mode}: " + json.dumps(summary), flush=True)
+        parity = GreedyParity(fp32, tolerance=BF16_22_LAYER_TOLERANCE, device=device,
+                              max_flip_rate=MAX_FLIP_RATE,
+                              name=f"cfg5 at size, {mode}, {len(subset)} of 512 requests")
+        by_id = {t.request_id: t for t in traces}
+        for request_id in subset:
+            spec = next(r for r in specs if r.request_id == request_id)
+            rows = watched[request_id]
+            assert len(rows) == len(by_id[request_id].generated) == spec.max_new_tokens
+            parity.check(request_id, spec.prompt, by_id[request_id].generated, rows)
+            watched[request_id] = []
+        reports[mode] = {"serving": summary, "greedy_parity": parity.finish()}
+    # Burst fills the batch to 64 and drains it: every batch bucket ran, and
+    # the contexts reach past 2048 tokens (the 4096-token bucket).
+    assert used_batches == {1, 2, 4, 8, 16, 32, 64}, sorted(used_batches)
+    assert used_contexts == {512, 1024, 2048, 4096}, sorted(used_contexts)
+    assert executor.metrics().capture_count == len(executor.buffer_addresses())
+    line = json.dumps({"workload": "BASELINE config 5 at its stated size", **reports})
+    print(line, flush=True)
+    warnings.warn(f"[cfg5 full] greedy parity: "
+                  + json.dumps({m: r["greedy_parity"] for m, r in reports.items()}))

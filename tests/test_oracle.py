@@ -299,9 +299,17 @@ def test_residual_oracles() -> None:
         torch.bfloat16))
     fused_sum, fused_norm = residual_rms_norm_fused_reference(x, r, w, 1e-5)
     assert_bit_exact(fused_sum, (x.float() + r.float()).to(torch.bfloat16), "fused sum")
-    s = x.double() + r.double()
-    expected = s * torch.rsqrt(s.square().mean(-1, keepdim=True) + 1e-5) * w.double()
-    torch.testing.assert_close(fused_norm.float(), expected.float(), rtol=8e-3, atol=1e-6)
+    # The norm output against a library routine: F.rms_norm over the fp32
+    # sum (not the rounded one), one rounding -- within one bf16 ulp, and it
+    # must differ from the normalised rounded sum somewhere (the two
+    # semantics the reference distinguishes, docs/kernel-design.md:33-39).
+    s = x.float() + r.float()
+    library = F.rms_norm(s.double(), (256,), w.double(), 1e-5).to(torch.bfloat16)
+    ulp = (library.float().abs() * 2.0 ** -7).clamp_min(2.0 ** -133)
+    assert bool(((fused_norm.float() - library.float()).abs() <= ulp).all())
+    assert bool((fused_norm.float() == library.float()).float().mean() > 0.95)
+    rounded_sum_norm = F.rms_norm(summed.double(), (256,), w.double(), 1e-5).to(torch.bfloat16)
+    assert not torch.equal(fused_norm, rounded_sum_norm)
     # Cancellation (reference tests/test_triton_kernels.py:113-127): x + (-x) = 0 -> 0.
     zero_sum, zero_norm = residual_rms_norm_fused_reference(x, -x, w, 1e-5)
     assert not bool(zero_sum.float().abs().max()) and not bool(zero_norm.float().abs().max())

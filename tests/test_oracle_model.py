@@ -50,6 +50,32 @@ def test_rope_closed_forms() -> None:
     assert torch.equal(rotate_half(torch.arange(4.0)), torch.tensor([-2.0, -3.0, 0.0, 1.0]))
 
 
+def test_rope_tables_carry_the_references_fp32_angle_rounding() -> None:
+    """The tables are built in fp32 as the reference builds them
+    (layers.py:38-46), not from exact angles: against exact fp64 angles
+    p * theta^(-2i/D) every entry is within the error that fp32 rounding of
+    the frequency and of the product explains (and well outside a table of
+    some other frequency law), while at large positions the rounding shows
+    (entries differ from the exact-angle table by more than fp32 cos/sin
+    rounding alone would)."""
+
+    d, theta = 64, 10000.0
+    positions = torch.arange(4096)
+    cos, sin = rope_tables(d, theta, positions)
+    assert cos.dtype == torch.float32 and cos.shape == (4096, d)
+    exponent = torch.arange(0, d, 2, dtype=torch.float64) / d
+    exact = positions.double()[:, None] * theta ** (-exponent)[None, :]
+    exact = torch.cat((exact, exact), dim=-1)
+    # fp32 inv_freq (pow and division: a few ulps) and the fp32 product.
+    bound = exact.abs() * 6 * 2.0 ** -24 + 1e-6
+    assert bool(((cos.double() - exact.cos()).abs() <= bound).all())
+    assert bool(((sin.double() - exact.sin()).abs() <= bound).all())
+    assert float((cos.double() - exact.cos()).abs().max()) > 1e-5
+    # Identity at position 0, unit norm everywhere.
+    assert torch.equal(cos[0], torch.ones(d)) and torch.equal(sin[0], torch.zeros(d))
+    assert float((cos.double() ** 2 + sin.double() ** 2 - 1).abs().max()) < 1e-6
+
+
 def _brute_force_logits(weights: DecoderWeights, tokens: list[int]) -> torch.Tensor:
     """The same decoder written as explicit per-position loops over heads
     and keys (math.exp softmax), fp64."""

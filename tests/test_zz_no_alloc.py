@@ -4,7 +4,8 @@ The no-allocation call keeps its split partials in the library's fixed
 device array instead of a caller workspace; it runs the same kernels, so
 its output must equal the workspace call's bit for bit.  Two split-KV calls
 in a row (the second smaller, so stale partials of the first sit in the
-array), a one-pass call, and the size limit are checked.  Collected last
+array), a call captured in a HIP graph and replayed, a one-pass call, and
+the size limit are checked.  Collected last
 (``test_zz_``): it must pass alone in a fresh process and after the rest.
 """
 
@@ -46,6 +47,44 @@ def _noalloc_call(lib, gpu, output, split_size, num_splits, stream):
         batch, query_heads, kv_heads, head_dim, num_blocks, block_size,
         gpu.block_tables.shape[1], split_size, num_splits, gpu.scale,
         _native.dtype_code(gpu.query.dtype), 0, stream)
+
+
+def test_noalloc_under_graph_capture_replays_like_the_workspace_call(device):
+    """The callers the entry point is for: the call captured in a HIP graph
+    (torch.cuda.graph).  Collected first in this file, so in a process that
+    has made no no-allocation call yet (this file alone, or the whole suite,
+    where nothing else calls it) the scratch address is taken inside the
+    capture.  The graph is replayed three times, with the query changed in
+    place and eager work and synchronisations between replays; every replay
+    must equal an eager workspace call on the same inputs bit for bit."""
+
+    lib = _native.library()
+    case = make_decode_attention_case(
+        [1500, 3, 0, 640, 2048, 96], query_heads=32, kv_heads=4, head_dim=64, block_size=16,
+        dtype=torch.bfloat16, seed=21, table_width=128).to(device)
+    stream = torch.cuda.Stream(device)
+    expected = torch.empty_like(case.query)
+    captured = torch.full_like(case.query, float("nan"))
+    with torch.cuda.stream(stream):
+        _workspace_call(lib, case, expected, 256, 8, stream.cuda_stream)  # module loaded
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        status = _noalloc_call(lib, case, captured, 256, 8,
+                               torch.cuda.current_stream(device).cuda_stream)
+    _native.check(status, "no-allocation call under capture")
+    generator = torch.Generator().manual_seed(22)
+    for replay in range(3):
+        fresh = torch.randn(case.query.shape, generator=generator).to(torch.bfloat16)
+        case.query.copy_(fresh.to(device))
+        torch.cuda.synchronize(device)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        _workspace_call(lib, case, expected, 256, 8,
+                        torch.cuda.current_stream(device).cuda_stream)
+        torch.cuda.synchronize(device)
+        assert_bit_exact(captured, expected, f"graph replay {replay}")
+        assert bool(torch.isfinite(captured.float()).all())
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
