@@ -5,8 +5,9 @@ geometry -- 64 rows with context U[128, 2048] plus 8 zero-length rows,
 32 query / 4 KV heads, head_dim 64, 16-token pages on a seeded permutation,
 bf16, N(0,1) inputs, scale 1/8.  A step is one attention call over one
 batch as the Python entry point plans it: at this batch one pass, one
-workgroup per (row, kv head) whose three wavefronts share the row and
-combine in LDS (no partials, no merge launch); ``--split-size`` forces the
+workgroup per (row, kv head) whose wavefronts (up to four, one per 576
+tokens of the row) share the row and combine in LDS (no partials, no merge
+launch); ``--split-size`` forces the
 split-KV form (split stage + log-sum-exp merge launch).  To keep
 the 256 MB Infinity Cache from serving the K/V pages, steps rotate over
 several independent copies of the page pool (``--pools``), so every step
@@ -25,8 +26,10 @@ graph of K split-stage launches alone.
 ``decode_step`` is the metric's "decode tokens/s" part: a whole
 graph-captured decode step of the 22-layer TinyLlama-geometry model (random
 init, bf16) for the same 64 rows, with prompts of the rows' context lengths,
-and beside it the oracle's fp32 incremental decode step on 4 rows on the
-host cores.
+with its own ``roofline`` (the step's algorithmic bytes -- every layer's
+weights, the rows' K/V at their contexts, LM head -- over the device step
+time), and beside it the oracle's fp32 incremental decode step on all 64
+rows on the host cores.
 """
 
 from __future__ import annotations
@@ -272,6 +275,7 @@ def decode_step(lengths: list[int], cpu_seconds: float, with_cpu: bool) -> dict:
 
     from tensorforge_amd.decode import DecoderWeights, tinyllama_config
     from tensorforge_amd.kernel_bench import measure_decode_step
+    from tensorforge_amd.workloads import decode_step_bytes
 
     device = torch.device("cuda", 0)
     config = tinyllama_config()
@@ -280,6 +284,8 @@ def decode_step(lengths: list[int], cpu_seconds: float, with_cpu: bool) -> dict:
     steps = 40
     prompts = [max(1, min(n, 2048 - steps - 8)) for n in active]
     gpu = measure_decode_step(weights, len(active), 2048, steps=steps, prompt_lengths=prompts)
+    step_bytes = decode_step_bytes(config, gpu["sum_context_mean"], len(active), 2)
+    rate = step_bytes["total"] / (gpu["device_ms_p50"] * 1e-3) / 1e9
     result = {
         "model": "TinyLlama-1.1B geometry, 22 layers, random init (seed 0), bf16",
         "batch": len(active),
@@ -289,6 +295,13 @@ def decode_step(lengths: list[int], cpu_seconds: float, with_cpu: bool) -> dict:
         "steps": gpu["steps"],
         "timing": "HIP events around each graph replay; host-inclusive = pipelined "
                   "launch/collect loop wall time per step",
+        "roofline": {"bound": "hbm", "achieved": round(rate, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(rate / HBM_PEAK_GBS, 4),
+                     "algorithmic_bytes_per_step": step_bytes,
+                     "sum_context_mean": gpu["sum_context_mean"],
+                     "model": "workloads.decode_step_bytes: every layer's weights once, the "
+                              "rows' K/V read at their contexts and the new K/V written, LM "
+                              "head, embedding rows and logits; over the device p50 step time"},
     }
     if with_cpu:
         result["cpu_baseline"] = decode_step_cpu_baseline(weights, prompts, cpu_seconds)

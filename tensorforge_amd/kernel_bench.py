@@ -21,6 +21,10 @@
   probe alone, and the page-gather probe over config 2's own pages;
 * valu (only with ``--only valu``) -- the attention kernel's products on
   MFMA against its VALU form, at config 2's lengths with group 8 and 4;
+* step_projections (only with ``--only step_projections``) -- the four
+  projections of a 64-row decode step in the forms the executor launches
+  (norm and residual epilogues, gate|up + SwiGLU), for their rates and
+  their HBM counters;
 * projections -- the decode step's projections at TinyLlama shapes and 1 /
   16 / 64 rows (weights rotated through HBM): hipBLASLt against the paths
   the decode bucket takes (linear_kstream for qkv, linear_stream partials
@@ -501,6 +505,8 @@ def measure_decode_step(weights: DecoderWeights, batch: int, context: int, *,
     p50 = times[len(times) // 2]
     return {
         "steps": timed, "prompt_tokens": sum(prompt_lengths),
+        # Contexts of the timed steps, on average (new token included).
+        "sum_context_mean": sum(prompt_lengths) + batch * (warm + (timed + 1) // 2),
         "device_ms_p50": round(p50, 4),
         "device_ms_p95": round(times[int(0.95 * (len(times) - 1))], 4),
         "host_inclusive_ms_per_step": round(host_ms, 4),
@@ -597,11 +603,58 @@ def projections(device: torch.device, calls: int) -> list[dict]:
     return results
 
 
+def step_projections(device: torch.device, calls: int) -> list[dict]:
+    """The four projections of a 64-row TinyLlama decode step in the forms
+    the executor's default chain launches (decode._forward): qkv with the
+    input RMSNorm, o and down added to the residual stream, gate|up with the
+    post-attention RMSNorm and SwiGLU.  Weights rotated through enough
+    copies (>= 600 MB) that each call reads its weight from HBM; bytes are
+    the weight, x and the output (and the residual) once."""
+
+    from tensorforge_amd.kernels import linear_swiglu
+
+    m, h, f, eps = 64, 2048, 5632, 1e-5
+    generator = torch.Generator().manual_seed(0)
+
+    def randn(*shape: int, scale: float = 1.0) -> torch.Tensor:
+        return (torch.randn(*shape, generator=generator) * scale).to(torch.bfloat16).to(device)
+
+    x_h, residual, attn, act = randn(m, h), randn(m, h), randn(m, h), randn(m, f)
+    y_qkv = torch.empty(m, 2560, dtype=torch.bfloat16, device=device)
+    y_h = torch.empty(m, h, dtype=torch.bfloat16, device=device)
+    y_act = torch.empty(m, f, dtype=torch.bfloat16, device=device)
+    e = 2
+    cases = {
+        "qkv + input norm (linear_kstream norm)": (
+            (2560, h), lambda w: linear_kstream(x_h, w, output=y_qkv, norm_eps=eps),
+            (m * h + m * 2560) * e),
+        "o + residual (linear_kstream residual)": (
+            (h, h), lambda w: linear_kstream(attn, w, output=y_h, residual=residual),
+            (2 * m * h + m * h) * e),
+        "gate|up + post norm + SwiGLU (linear_swiglu k_split norm)": (
+            (2 * f, h), lambda w: linear_swiglu(x_h, w, output=y_act, k_split=True, norm_eps=eps),
+            (m * h + m * f) * e),
+        "down + residual (linear_kstream residual)": (
+            (h, f), lambda w: linear_kstream(act, w, output=y_h, residual=residual),
+            (m * f + 2 * m * h) * e),
+    }
+    results = []
+    for name, ((n, k), run, io_bytes) in cases.items():
+        copies = max(2, int(600e6 // (n * k * e)))
+        weights = [randn(n, k, scale=0.02) for _ in range(copies)]
+        us = graph_time_us(lambda i: run(weights[i % copies]), calls, device)
+        results.append(report(f"b64 step projection: {name} [{m}x{k}]x[{k}x{n}]", us,
+                              n * k * e + io_bytes, weight_bytes=n * k * e,
+                              weight_copies=copies))
+        del weights
+    return results
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--calls", type=int, default=100)
     parser.add_argument("--only", choices=("cfg3", "cfg4", "decode", "decode22", "ceiling", "valu",
-                                           "projections"), default=None)
+                                           "projections", "step_projections"), default=None)
     args = parser.parse_args()
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -625,6 +678,9 @@ def main() -> int:
             print(json.dumps(result), flush=True)
     if args.only in (None, "projections"):
         for result in projections(device, args.calls):
+            print(json.dumps(result), flush=True)
+    if args.only == "step_projections":
+        for result in step_projections(device, args.calls):
             print(json.dumps(result), flush=True)
     return 0
 

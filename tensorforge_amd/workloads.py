@@ -169,3 +169,27 @@ def kv_append_bytes(tokens: int, kv_heads: int, head_dim: int, element_size: int
     """K and V rows read and written plus 12 bytes of control per token."""
 
     return 2 * (2 * tokens * kv_heads * head_dim * element_size) + 12 * tokens
+
+
+def decode_step_bytes(config, sum_context: int, batch: int, element_size: int) -> dict:
+    """Algorithmic HBM bytes of one decode step of a Llama-style decoder
+    (``tensorforge_amd.decode.DecoderConfig``) over ``batch`` rows whose
+    contexts sum to ``sum_context`` tokens (the new token included): every
+    layer's weights once (qkv, o, gate|up, down and the two norm gains), the
+    rows' cached K and V read and the new token's K and V written, the LM
+    head and final norm once, the embedding rows read and the logits
+    written.  Activations passed between kernels are not counted (a fused
+    step need not write them)."""
+
+    e = element_size
+    h, f, d = config.hidden_size, config.intermediate_size, config.head_dim
+    hq, hkv = config.num_attention_heads, config.num_key_value_heads
+    layers = config.num_hidden_layers
+    weights = ((hq + 2 * hkv) * d * h + h * hq * d + 2 * f * h + h * f + 2 * h) * e
+    kv_read = sum_context * hkv * d * 2 * e
+    kv_write = batch * hkv * d * 2 * e
+    head = (config.vocab_size * h + h) * e
+    io = batch * h * e + batch * config.vocab_size * e
+    return {"layer_weights": layers * weights, "kv_read": layers * kv_read,
+            "kv_write": layers * kv_write, "lm_head": head, "embedding_and_logits": io,
+            "total": layers * (weights + kv_read + kv_write) + head + io}

@@ -431,6 +431,26 @@ def test_elementwise_byte_models() -> None:
     assert kv_append_bytes(64, 4, 64, 2) > 0
 
 
+def test_decode_step_byte_model_closed_form() -> None:
+    """TinyLlama geometry: 44,040,192 weight elements per layer plus two
+    2048-element gains (qkv 2560 x 2048, o 2048 x 2048, gate|up 11264 x
+    2048, down 2048 x 5632), 22 layers, 1.94 GB in bf16; K/V 512 bytes per
+    token and layer for each of K and V."""
+
+    from tensorforge_amd.decode import tinyllama_config
+    from tensorforge_amd.workloads import decode_step_bytes
+
+    config = tinyllama_config()
+    parts = decode_step_bytes(config, sum_context=1000, batch=2, element_size=2)
+    assert parts["layer_weights"] == 22 * (44_040_192 + 2 * 2048) * 2
+    assert parts["kv_read"] == 22 * 1000 * 4 * 64 * 2 * 2
+    assert parts["kv_write"] == 22 * 2 * 4 * 64 * 2 * 2
+    assert parts["lm_head"] == (32000 * 2048 + 2048) * 2
+    assert parts["embedding_and_logits"] == 2 * 2048 * 2 + 2 * 32000 * 2
+    assert parts["total"] == sum(v for key, v in parts.items() if key != "total")
+    assert abs(parts["layer_weights"] / 1e9 - 1.938) < 0.001
+
+
 def test_bench_refuses_more_than_one_gpu() -> None:
     result = subprocess.run(
         [sys.executable, str(REPO_ROOT / "bench.py"), "--gpus", "2"],
