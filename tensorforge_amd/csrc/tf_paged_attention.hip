@@ -1320,22 +1320,30 @@ size_t generic_lds_bytes(int D, int G) {
 // Log-sum-exp merge of split partials
 // ===========================================================================
 template <typename T>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(256)
 merge_partials_kernel(const float *__restrict__ partial_max, const float *__restrict__ partial_sum,
                       const float *__restrict__ partial_acc,
                       const int32_t *__restrict__ context_lengths, T *__restrict__ output,
                       int32_t query_heads, int32_t head_dim, int32_t split_size,
                       int32_t num_splits, int32_t partial_stride, int32_t max_tokens,
                       int32_t balanced) {
-  // One wavefront per (row, query head).  Lane s holds the max and sum of
-  // split s (64 splits per pass); lanes over head_dim accumulate the
-  // weighted rows, kBatch splits of loads in flight.  The first batch is
+  // One workgroup of W wavefronts per (row, query head).  Lane s holds the
+  // max and sum of split s (64 splits per pass); lanes over head_dim
+  // accumulate the weighted rows in batches of kBatch splits, every load of
+  // a batch in flight together.  Wavefront w takes batches w, w + W, ...;
+  // each batch's weighted sum starts from zero and the batch sums are
+  // added in batch order (by wavefront 0 through LDS when W > 1), so the
+  // result does not depend on W, and a row of <= kBatch splits gives
+  // exactly the one batch's sum.  The first batch of each wavefront is
   // issued together with the max/sum loads (before the row length is
-  // known), so a row with <= kBatch splits costs one memory round trip;
+  // known), so a row with <= W kBatch splits costs one memory round trip;
   // loads of splits past the row's last one are discarded by a select.
   constexpr int kBatch = 16;
   constexpr int kDims = 4;  // head_dim <= 256 = 4 x 64 lanes
-  const int lane = threadIdx.x;
+  extern __shared__ float batch_sums[];  // [batches][kDims][64] when W > 1
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int W = blockDim.x >> 6;
   const int32_t qh = blockIdx.x;
   const int32_t b = blockIdx.y;
   const int64_t base = (static_cast<int64_t>(b) * query_heads + qh) * num_splits;
@@ -1356,7 +1364,7 @@ merge_partials_kernel(const float *__restrict__ partial_max, const float *__rest
   const int32_t first = min(lane, num_splits - 1);
   float m = partial_max[base + first];
   float l = partial_sum[base + first];
-  load_batch(0);
+  load_batch(kBatch * wave);
   int32_t ctx = context_lengths[b];
   ctx = ctx < 0 ? 0 : (ctx > max_tokens ? max_tokens : ctx);
   if (balanced) {
@@ -1383,9 +1391,12 @@ merge_partials_kernel(const float *__restrict__ partial_max, const float *__rest
   }
   den = wave_sum(den);
   const float inv = den > 0.f ? 1.f / den : 0.f;
-  float num[kDims] = {0.f, 0.f, 0.f, 0.f};
-  for (int32_t s0 = 0; s0 < nvalid; s0 += kBatch) {
-    if (s0 > 0) load_batch(s0);
+  const int32_t batches = (nvalid + kBatch - 1) / kBatch;
+  float total[kDims] = {0.f, 0.f, 0.f, 0.f};
+  for (int32_t bi = wave; bi < batches; bi += W) {
+    const int32_t s0 = bi * kBatch;
+    if (bi != wave) load_batch(s0);
+    float num[kDims] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       const int32_t sj = s0 + j;
@@ -1397,11 +1408,25 @@ merge_partials_kernel(const float *__restrict__ partial_max, const float *__rest
 #pragma unroll
       for (int k = 0; k < kDims; ++k) num[k] += w * v[j][k];
     }
+    if (W == 1) {
+#pragma unroll
+      for (int k = 0; k < kDims; ++k) total[k] += num[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < kDims; ++k) batch_sums[(bi * kDims + k) * 64 + lane] = num[k];
+    }
+  }
+  if (W > 1) {  // workgroup-uniform
+    __syncthreads();
+    if (wave != 0) return;
+    for (int32_t bi = 0; bi < batches; ++bi)
+#pragma unroll
+      for (int k = 0; k < kDims; ++k) total[k] += batch_sums[(bi * kDims + k) * 64 + lane];
   }
 #pragma unroll
   for (int k = 0; k < kDims; ++k) {
     const int d = lane + 64 * k;
-    if (k < ndim && d < head_dim) out[d] = from_float<T>(num[k]);
+    if (k < ndim && d < head_dim) out[d] = from_float<T>(total[k]);
   }
 }
 
@@ -1648,21 +1673,29 @@ int32_t launch_merge(const float *partial_max, const float *partial_sum, const f
   const int32_t bal = balanced ? 1 : 0;
   if (batch == 0) return TF_SUCCESS;
   const dim3 grid(static_cast<unsigned>(query_heads), static_cast<unsigned>(batch));
+  // Up to four wavefronts per (row, head) when a row may have more than one
+  // 16-split batch, so the batches' loads are in flight together (cfg3's
+  // 64 partitions of 512 tokens: 14.2 -> a few us); their batch sums meet
+  // in LDS (4 KB per batch), so beyond 16 batches one wavefront walks them.
+  const int32_t batches = (num_splits + 15) / 16;
+  const int waves = batches <= 1 || batches > 16 ? 1 : (batches < 4 ? batches : 4);
+  const dim3 block(64u * static_cast<unsigned>(waves));
+  const size_t lds = waves > 1 ? static_cast<size_t>(batches) * 4 * 64 * sizeof(float) : 0;
   switch (dtype) {
     case TF_DTYPE_FLOAT32:
-      hipLaunchKernelGGL(merge_partials_kernel<float>, grid, dim3(64), 0, stream, partial_max,
+      hipLaunchKernelGGL(merge_partials_kernel<float>, grid, block, lds, stream, partial_max,
                          partial_sum, partial_acc, context_lengths, static_cast<float *>(output),
                          query_heads, head_dim, split_size, num_splits, partial_stride, max_tokens,
                          bal);
       break;
     case TF_DTYPE_FLOAT16:
-      hipLaunchKernelGGL(merge_partials_kernel<_Float16>, grid, dim3(64), 0, stream, partial_max,
+      hipLaunchKernelGGL(merge_partials_kernel<_Float16>, grid, block, lds, stream, partial_max,
                          partial_sum, partial_acc, context_lengths,
                          static_cast<_Float16 *>(output), query_heads, head_dim, split_size,
                          num_splits, partial_stride, max_tokens, bal);
       break;
     default:
-      hipLaunchKernelGGL(merge_partials_kernel<__bf16>, grid, dim3(64), 0, stream, partial_max,
+      hipLaunchKernelGGL(merge_partials_kernel<__bf16>, grid, block, lds, stream, partial_max,
                          partial_sum, partial_acc, context_lengths, static_cast<__bf16 *>(output),
                          query_heads, head_dim, split_size, num_splits, partial_stride, max_tokens,
                          bal);

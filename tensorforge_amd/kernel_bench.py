@@ -162,14 +162,15 @@ def config4(device: torch.device, calls: int) -> list[dict]:
 
 
 def config3(device: torch.device, calls: int) -> list[dict]:
-    """Config 3 (4 rows of 8k..32k at Llama-3-8B geometry) five ways: the
+    """Config 3 (4 rows of 8k..32k at Llama-3-8B geometry) six ways: the
     entry point's plan (balanced partitions sized on the device from the
     rows' lengths, two wavefronts each, merge launch); the BASELINE's form,
     512-token partitions and a separate log-sum-exp merge launch (the entry
     point with the partition size fixed at 512, as the reference's
-    split_size argument fixes it) and the same partitions with the in-kernel
-    merge (the C ABI with the workspace's arrival counters: the last
-    partition of each (row, kv head) merges); and fixed 4096-token
+    split_size argument fixes it, two wavefronts per partition), the same
+    partitions with one wavefront each, and with the in-kernel merge (the
+    C ABI with the workspace's arrival counters: the last partition of each
+    (row, kv head) merges); and fixed 4096-token
     partitions with four wavefronts each (the plan before the balanced
     partitions) with the merge launch and with the in-kernel merge."""
 
@@ -205,7 +206,9 @@ def config3(device: torch.device, calls: int) -> list[dict]:
     previous = set_attention_split_size(512)
     try:
         us = graph_time_us(entry, calls, device)
-        results.append(report(f"{name}, 512-token partitions, merge launch (BASELINE form)", us,
+        launch = selected_attention_launch() or {}
+        results.append(report(f"{name}, 512-token partitions ({launch.get('waves_per_head')} "
+                              f"wavefronts each), merge launch (BASELINE form)", us,
                               nbytes, record=dict(selected_attention_autotune_config() or {})))
     finally:
         set_attention_split_size(previous)
@@ -214,8 +217,11 @@ def config3(device: torch.device, calls: int) -> list[dict]:
     fixed_flags = ((1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
                    | (4 << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
                    | (1 << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
+    two_waves = ((1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
+                 | (2 << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT))
     for split, flags, in_kernel, label in (
-            (512, 0, True, "512-token partitions, 1 wavefront each, in-kernel merge"),
+            (512, 0, False, "512-token partitions, 1 wavefront each, merge launch"),
+            (512, two_waves, True, "512-token partitions, 2 wavefronts each, in-kernel merge"),
             (4096, fixed_flags, False, "fixed 4096-token partitions, 4 wavefronts each, "
                                        "merge launch"),
             (4096, fixed_flags, True, "fixed 4096-token partitions, 4 wavefronts each, "

@@ -162,6 +162,16 @@ NARROW_TOKENS_PER_WAVE = 64
 # partitions with 4: 70.8-71.9).
 BALANCED_MIN_CONTEXT = 8192
 BALANCED_WAVES = 2
+# Partitions of a caller-fixed size (set_attention_split_size, or
+# attention_path="split_kv") are streamed by two wavefronts each, four
+# above 768 tokens, all of them on every partition (measured on MI355X
+# against one wavefront per partition, merge launch included: config 3 in
+# the BASELINE's 512-token partitions 119.7 -> 85.1 us; config 2 at 256 /
+# 512 / 1024 tokens 32.6 / 33.3 / 34.0 -> 27.0 / 25.1 / 24.3 us (2) and
+# 25.9 (4 at 1024); 16 x 4096 and 4 x 2048 rows 10-30% faster).
+FIXED_SPLIT_WAVES = 2
+FIXED_SPLIT_WAVES_WIDE = 4
+FIXED_SPLIT_WIDE = 768
 COMPUTE_UNITS = 256  # MI355X
 
 
@@ -270,8 +280,9 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
       two wavefronts each (config 3: 64.5 against 70.8-71.9 us for fixed
       4096-token partitions);
     * a partition size fixed by the caller (set_attention_split_size) or
-      ``attention_path="split_kv"``: split-KV with one wavefront per split
-      and attention_split_size_for; ``"one_pass"`` forces one pass.
+      ``attention_path="split_kv"``: split-KV (size attention_split_size_for
+      unless fixed) with two wavefronts per partition, four above 768
+      tokens; ``"one_pass"`` forces one pass.
     """
 
     fixed = _SPLIT_SIZE is not None
@@ -283,7 +294,9 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
         if attention_path == "one_pass" or (attention_path == "auto"
                                             and launch_context <= split_size):
             return AttentionPlan(True, capacity32, 1, 1)
-        return AttentionPlan(False, split_size, (launch_context + split_size - 1) // split_size, 1)
+        waves = FIXED_SPLIT_WAVES if split_size <= FIXED_SPLIT_WIDE else FIXED_SPLIT_WAVES_WIDE
+        return AttentionPlan(False, split_size, (launch_context + split_size - 1) // split_size,
+                             waves, 0)
     if workgroups >= ONE_PASS_MIN_WORKGROUPS:
         tokens = wide_tokens_per_wave(launch_context)
         waves = max(1, min(8, -(-launch_context // tokens)))

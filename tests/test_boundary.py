@@ -358,13 +358,17 @@ def test_attention_plan() -> None:
     assert attention_plan(100, 64, 4, 128).flags == 0  # one wavefront
     assert attention_plan(32768, 64, 4, 32768).waves_per_head == 8
     forced = attention_plan(2048, 72, 4, 2048, "split_kv")
-    assert (forced.one_pass, forced.split_size, forced.waves_per_head) == (False, 576, 1)
+    assert (forced.one_pass, forced.split_size, forced.waves_per_head) == (False, 576, 2)
+    assert forced.tokens_per_wave == 0  # every wavefront streams its share of the partition
     previous = set_attention_split_size(512)
     try:
         fixed = attention_plan(2048, 72, 4, 2048)
         assert (fixed.one_pass, fixed.split_size, fixed.num_splits) == (False, 512, 4)
-        assert fixed.flags == 0
-        assert attention_plan(400, 2, 4, 2048).waves_per_head == 1
+        assert fixed.flags == ((1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
+                               | (2 << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT))
+        assert attention_plan(400, 2, 4, 2048).waves_per_head == 1  # one pass
+        set_attention_split_size(1024)
+        assert attention_plan(32768, 4, 8, 32768).waves_per_head == 4
     finally:
         set_attention_split_size(previous)
 
