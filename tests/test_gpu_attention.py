@@ -470,3 +470,59 @@ def test_in_kernel_merge_is_fresh_on_every_call(device):
     assert int(workspace.split_counters.sum()) == 0
     case.query = queries[-1].cpu()
     _check_against_oracle(case, fused_out[-1].cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, "last call")
+
+
+def test_merge_result_does_not_depend_on_its_wavefront_count(device):
+    """The merge launch gives each (row, head) one wavefront per batch of 16
+    partitions (up to four; one beyond 16 batches) and adds the batch sums
+    in batch order, so the same partials merge to the same bits whatever
+    the partition count the launch declares: here the partials of a call
+    with 20 partitions of 64 tokens (two batches: two wavefronts), laid out
+    again for 70 declared partitions (four wavefronts) and for 300 (one
+    wavefront walking the batches), with NaN in every slot past the rows'
+    own partitions (read ahead, never used)."""
+
+    lengths = [1280, 1, 0, 700, 1279, 64, 65, 1024]
+    case = make_decode_attention_case(lengths, query_heads=8, kv_heads=2, head_dim=64,
+                                      block_size=16, dtype=torch.bfloat16, seed=31)
+    gpu = case.to(device)
+    lib = _native.library()
+    batch, hq, d = gpu.query.shape
+    blocks, page, hkv, _ = gpu.key_cache.shape
+    split, used = 64, 20
+    stream = _native.current_stream(device)
+    partials = {}
+    for declared in (used, 70, 300):
+        rows = batch * hq * declared
+        partials[declared] = (torch.full((rows,), float("nan"), device=device),
+                              torch.full((rows,), float("nan"), device=device),
+                              torch.full((rows, d), float("nan"), device=device))
+    pm, ps, pa = partials[used]
+    _native.check(lib.tf_paged_gqa_decode_partials(
+        gpu.query.data_ptr(), gpu.key_cache.data_ptr(), gpu.value_cache.data_ptr(),
+        gpu.block_tables.data_ptr(), gpu.context_lengths.data_ptr(), pm.data_ptr(),
+        ps.data_ptr(), pa.data_ptr(), pm.numel(), d, batch, hq, hkv, d, blocks, page,
+        gpu.block_tables.shape[1], split, used, gpu.scale, _native.dtype_code(torch.bfloat16), 0,
+        stream), "partials")
+    for declared in (70, 300):
+        qm, qs, qa = partials[declared]
+        qm.view(batch, hq, declared)[:, :, :used] = pm.view(batch, hq, used)
+        qs.view(batch, hq, declared)[:, :, :used] = ps.view(batch, hq, used)
+        qa.view(batch, hq, declared, d)[:, :, :used] = pa.view(batch, hq, used, d)
+    outputs = {}
+    for declared, (qm, qs, qa) in partials.items():
+        out = torch.full_like(gpu.query, float("nan"))
+        _native.check(lib.tf_paged_gqa_decode_merge(
+            qm.data_ptr(), qs.data_ptr(), qa.data_ptr(), gpu.context_lengths.data_ptr(),
+            out.data_ptr(), qm.numel(), d, batch, hq, d, split, declared, used * split,
+            _native.dtype_code(torch.bfloat16), stream), f"merge of {declared}")
+        outputs[declared] = out
+    torch.cuda.synchronize()
+    assert torch.equal(outputs[used].view(torch.int16), outputs[70].view(torch.int16))
+    assert torch.equal(outputs[used].view(torch.int16), outputs[300].view(torch.int16))
+    live = [r for r, c in enumerate(lengths) if c > 0]
+    want = paged_gqa_decode_reference(case.query[live], case.key_cache, case.value_cache,
+                                      case.block_tables[live], case.context_lengths[live],
+                                      scale=case.scale)
+    assert_close(outputs[used].cpu()[live], want, NORTH_STAR_ATOL, NORTH_STAR_RTOL, "merged")
+    assert bool((outputs[used].cpu()[[2]] == 0).all())
