@@ -223,9 +223,10 @@ class DecodeGraphBucket:
     length, the append page/offset and the active flag.  The host keeps a
     master copy and rewrites only what changed: a lane that decodes the same
     request as last time gets just its newly appended pages.  Each step
-    copies the master into one of two pinned slabs and from there, with one
-    asynchronous copy per slab, to the device; a slab is reused only after
-    its previous copy has completed.
+    copies the master into one of two pinned byte slabs (the int64 rows and
+    the int32 segments back to back) and from there, with one asynchronous
+    copy, to the device; a slab is reused only after its previous copy has
+    completed.
     """
 
     def __init__(self, weights: DecoderWeights, cache: PagedKVCache, *, batch_capacity: int,
@@ -256,14 +257,21 @@ class DecodeGraphBucket:
         self._host_views = (self._ctl_int[:cuts[0]].reshape(b, width), self._ctl_int[cuts[0]:cuts[1]],
                             self._ctl_int[cuts[1]:cuts[2]], self._ctl_int[cuts[2]:cuts[3]],
                             self._ctl_int[cuts[3]:])
-        self._pinned = [(torch.zeros((3, b), dtype=torch.long, pin_memory=True),
-                         torch.zeros(self._ctl_int.size, dtype=torch.int32, pin_memory=True))
-                        for _ in range(2)]
+        # One byte slab holds both segments (the int64 rows first), so a step
+        # stages its controls with a single host-to-device copy.
+        long_bytes = 3 * b * 8
+        slab_bytes = long_bytes + self._ctl_int.size * 4
+        self._pinned = []
+        for _ in range(2):
+            slab = torch.zeros(slab_bytes, dtype=torch.uint8, pin_memory=True)
+            self._pinned.append((slab, slab.numpy()[:long_bytes].view(np.int64).reshape(3, b),
+                                 slab.numpy()[long_bytes:].view(np.int32)))
         self._copied = [torch.cuda.Event(), torch.cuda.Event()]
         self._copy_recorded = [False, False]
         self._flip = 0
-        self._long = torch.zeros((3, b), dtype=torch.long, device=device)
-        self._int = torch.zeros(self._ctl_int.size, dtype=torch.int32, device=device)
+        self._slab = torch.zeros(slab_bytes, dtype=torch.uint8, device=device)
+        self._long = self._slab[:long_bytes].view(torch.int64).view(3, b)
+        self._int = self._slab[long_bytes:].view(torch.int32)
         self.host_tokens = self._long[0]
         self.positions = self._long[1]
         self.source_lanes = self._long[2]
@@ -417,11 +425,10 @@ class DecodeGraphBucket:
         self._flip ^= 1
         if self._copy_recorded[k]:
             self._copied[k].synchronize()  # the slab's previous copy has landed
-        pinned_long, pinned_int = self._pinned[k]
-        np.copyto(pinned_long.numpy(), self._ctl_long)
-        np.copyto(pinned_int.numpy(), self._ctl_int)
-        self._long.copy_(pinned_long, non_blocking=True)
-        self._int.copy_(pinned_int, non_blocking=True)
+        slab, host_long, host_int = self._pinned[k]
+        np.copyto(host_long, self._ctl_long)
+        np.copyto(host_int, self._ctl_int)
+        self._slab.copy_(slab, non_blocking=True)
         self._copied[k].record()
         self._copy_recorded[k] = True
 
