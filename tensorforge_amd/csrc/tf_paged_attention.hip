@@ -602,6 +602,25 @@ paged_decode_mfma_kernel(AttnParams p) {
     const int32_t logical = p.page_shift >= 0 ? (t >> p.page_shift) : (t / p.block_size);
     return logical < p.table_width ? table[logical] : -1;
   };
+  // Byte offsets of the same tiles' K / V head slices from the cache bases
+  // (lane i: tile first + i), -1 where the tile has no valid page: computed
+  // once per window on the vector lanes, so a tile's loads need only two
+  // lane reads and a few scalar adds (the scalar unit, one instruction per
+  // cycle for the whole compute unit, was the long rows' bound).
+  const uint32_t token_bytes = static_cast<uint32_t>(p.kv_heads) * D * sizeof(T);
+  const int64_t head_bytes = static_cast<int64_t>(kvh) * D * sizeof(T);
+  auto window_offsets = [&](int32_t first, int32_t page, uint32_t &lo, int32_t &hi) {
+    const int32_t t = s0 + 16 * (first + lane);
+    const int32_t in_page = p.page_shift >= 0 ? (t & (p.block_size - 1))
+                                              : (t - (t / p.block_size) * p.block_size);
+    const int64_t off = page >= 0 && page < p.num_blocks
+                            ? (static_cast<int64_t>(page) * p.block_size + in_page) * token_bytes + head_bytes
+                            : int64_t{-1};
+    lo = static_cast<uint32_t>(off);
+    hi = static_cast<int32_t>(off >> 32);
+  };
+  uint32_t win_lo = 0;  // the current segment's window_offsets
+  int32_t win_hi = -1;
 
   // Independent start-up loads: row length, query group, first page window
   // (the window first when the query group is rotated, whose arithmetic
@@ -734,10 +753,8 @@ paged_decode_mfma_kernel(AttnParams p) {
     active = active < 1 ? 1 : (active > WPH ? WPH : active);
   }
 
-  const uint32_t token_bytes = static_cast<uint32_t>(p.kv_heads) * D * sizeof(T);
   const unsigned char *kbytes = static_cast<const unsigned char *>(p.key_cache);
   const unsigned char *vbytes = static_cast<const unsigned char *>(p.value_cache);
-  const int64_t head_bytes = static_cast<int64_t>(kvh) * D * sizeof(T);
   // Stand-in row of absent tokens (read, masked out): this row's query
   // input, at least D elements long.
   const unsigned char *stand_in =
@@ -784,26 +801,24 @@ paged_decode_mfma_kernel(AttnParams p) {
   // tokens and chunks past the end read a stand-in row, so every load is
   // unconditional and the wait counts stay exact).  Bit t of valid[j]
   // marks token 16j + t present.
-  auto load_kv = [&](int32_t seg_first_tile, int32_t seg_s0, int32_t seg_s1, int32_t c,
-                     vec8(&kf)[2][KS], vec8(&vf)[2][KS], uint32_t(&valid)[2]) {
+  auto load_kv = [&](int32_t seg_s0, int32_t seg_s1, int32_t c, vec8(&kf)[2][KS], vec8(&vf)[2][KS],
+                     uint32_t(&valid)[2]) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int32_t t0 = seg_s0 + c * kChunk + 16 * j;
-      const int32_t tile = (t0 - s0) >> 4;
-      const int32_t slot = min(tile - seg_first_tile, kSegmentTiles - 1);
-      const int32_t page = __builtin_amdgcn_readlane(page_win, slot);
-      const bool tile_ok = t0 < seg_s1 && page >= 0 && page < p.num_blocks;
+      // Tile 2c + j of the segment's window (past the segment's end the
+      // tile is absent whatever the slot holds).
+      const int32_t slot = min(2 * c + j, kSegmentTiles - 1);
+      const uint32_t off_lo = __builtin_amdgcn_readlane(win_lo, slot);
+      const int32_t off_hi = __builtin_amdgcn_readlane(win_hi, slot);
+      const bool tile_ok = t0 < seg_s1 && off_hi >= 0;
       const int32_t ntok = tile_ok ? min(16, seg_s1 - t0) : 0;
       valid[j] = ntok >= 16 ? 0xffffu : ((1u << ntok) - 1u);
-      const int32_t in_page = p.page_shift >= 0 ? (t0 & (p.block_size - 1))
-                                                : (t0 - (t0 / p.block_size) * p.block_size);
       // Absent tiles read a stand-in row: the row's query (or QKV) input,
       // which nothing writes while the kernel runs, so that a stand-in load
       // never brings a cache page's line into L1 while another workgroup
       // on this compute unit may be appending to it.
-      const int64_t tile_off =
-          tile_ok ? (static_cast<int64_t>(page) * p.block_size + in_page) * token_bytes + head_bytes
-                  : 0;
+      const int64_t tile_off = static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(off_hi)) << 32) | off_lo);
       const unsigned char *kp = tile_ok ? kbytes + tile_off : stand_in;
       const unsigned char *vp = tile_ok ? vbytes + tile_off : stand_in;
       const uint32_t lane_off = l16 < ntok ? lane_full : lane_first;
@@ -1026,7 +1041,9 @@ paged_decode_mfma_kernel(AttnParams p) {
 
   // Segments of up to 1024 tokens share one page window; inside a segment
   // two register sets alternate so the next chunk's K/V are in flight while
-  // the current one is computed.
+  // the current one is computed (a third set, two chunks ahead, measured
+  // slower: 16 KB more in flight per wavefront lowers a compute unit's
+  // read rate).
   vec8 ka[2][KS], va[2][KS], kb[2][KS], vb[2][KS];
   uint32_t vala[2], valb[2];
   for (int32_t seg_s0 = s0; seg_s0 < s1; seg_s0 += 16 * kSegmentTiles) {
@@ -1037,13 +1054,14 @@ paged_decode_mfma_kernel(AttnParams p) {
     const int32_t mine =
         sub < active && seg_chunks > sub ? (seg_chunks - sub + active - 1) / active : 0;
     if (mine == 0) continue;
+    window_offsets(seg_first_tile, page_win, win_lo, win_hi);
     auto chunk = [&](int32_t i) { return i < mine ? sub + i * active : seg_chunks; };
-    load_kv(seg_first_tile, seg_s0, seg_s1, chunk(0), ka, va, vala);
+    load_kv(seg_s0, seg_s1, chunk(0), ka, va, vala);
     for (int32_t i = 0; i < mine; i += 2) {
-      load_kv(seg_first_tile, seg_s0, seg_s1, chunk(i + 1), kb, vb, valb);
+      load_kv(seg_s0, seg_s1, chunk(i + 1), kb, vb, valb);
       compute(ka, va, vala);
       if (i + 1 >= mine) break;
-      load_kv(seg_first_tile, seg_s0, seg_s1, chunk(i + 2), ka, va, vala);
+      load_kv(seg_s0, seg_s1, chunk(i + 2), ka, va, vala);
       compute(kb, vb, valb);
     }
   }
