@@ -708,10 +708,14 @@ paged_decode_mfma_kernel(AttnParams p) {
     // each, the next Hkv D/8 copy 8 value elements.
     //
     // Issuing a wavefront's first K/V chunks before this store (when they
-    // do not hold the new token) gave wrong results at head_dim 32 although
-    // no such load touches an appended line (tests/
-    // test_fused_append_schedule.py restates the addresses); the cause is
-    // not known, so loads stay after the wait.
+    // do not hold the new token) once gave results that differed from the
+    // two launches at head_dim 32, although no such load touches an
+    // appended line (tests/test_fused_append_schedule.py restates the
+    // addresses).  The same symptom -- a few last-bit differences, both
+    // forms deterministic -- came back with another change of this
+    // prologue and went away when the wavefronts' combine below was written
+    // with explicit fused multiply-adds: the compiler had fused a different
+    // product of `x * a + y * c` in the two instantiations.
     const int32_t page = p.append_pages[b];
     const int32_t off = p.append_offsets[b];
     const bool append = p.append_active[b] != 0 && page >= 0 && page < p.num_blocks && off >= 0 &&
@@ -1126,9 +1130,15 @@ paged_decode_mfma_kernel(AttnParams p) {
         const float a = m_run == kNegInf ? 0.f : fast_exp2(m_run - mn);
         const float c = mo == kNegInf ? 0.f : fast_exp2(mo - mn);
         m_run = mn;
-        l_run = l_run * a + lo * c;
+        // Explicit fused multiply-adds: `x * a + y * c` leaves the compiler
+        // free to fuse either product, and its choice differed between
+        // instantiations of this kernel (the fused RoPE launch and the plain
+        // one, which must give the same bits) once their other code differed.
+        l_run = __builtin_fmaf(lo, c, l_run * a);
 #pragma unroll
-        for (int n = 0; n < NB; ++n) acc[n] = acc[n] * a + ao[n] * c;
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[n][r] = __builtin_fmaf(ao[n][r], c, acc[n][r] * a);
       }
     }
     __syncthreads();

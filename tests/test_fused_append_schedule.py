@@ -15,8 +15,12 @@ case where two kv heads share a cache line.
 It also checks a variant that was tried and is not shipped: issuing each
 wavefront's first two chunks before the append when neither holds the new
 token.  The emulation shows that those early loads touch no appended line in
-any of these geometries, so an address overlap does not explain the wrong
-results that variant gave; see the module-level note in the kernel source.
+any of these geometries, so an address overlap does not explain the
+differing results that variant gave.  (The same last-bit symptom came back
+with another change of the launch's prologue and went away when the
+wavefronts' combine was written with explicit fused multiply-adds: the
+compiler had fused a different product of `x * a + y * c` in the fused and
+the plain kernel; see the note in the kernel source.)
 """
 
 from __future__ import annotations
