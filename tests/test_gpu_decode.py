@@ -42,11 +42,12 @@ FP16_BOUND = 1e-2
 BF16_BOUND = 6e-2
 
 
-def _cache(config, device, pages=128, sequences=4):
+def _cache(config, device, pages=128, sequences=4, block_size=16):
     order = list(range(pages))
     random.Random(0).shuffle(order)
     return PagedKVCache(
-        PagedKVCacheConfig(num_layers=config.num_hidden_layers, num_blocks=pages, block_size=16,
+        PagedKVCacheConfig(num_layers=config.num_hidden_layers, num_blocks=pages,
+                           block_size=block_size,
                            num_kv_heads=config.num_key_value_heads, head_dim=config.head_dim,
                            max_sequences=sequences, max_sequence_length=512,
                            dtype=torch.float16, device=device),
@@ -101,6 +102,31 @@ def test_batched_prefill_matches_the_oracle_and_single_prefill(device):
             torch.testing.assert_close(k_batched.float(), k_alone.float(), rtol=1e-2, atol=1e-2)
             torch.testing.assert_close(v_batched.float(), v_alone.float(), rtol=1e-2, atol=1e-2)
         assert together.sequence_layout(rid).context_length == len(prompt)
+
+
+@pytest.mark.parametrize("block_size", [32, 48])
+def test_greedy_decode_does_not_depend_on_the_page_size(device, block_size):
+    """The config-1 run on 32- and 48-token pages (48: the division form of the
+    page indices in every kernel that walks pages) gives the 16-token run's
+    tokens and bit-identical logits at every step: the page size changes
+    addresses, not arithmetic."""
+
+    config = small_config()
+    weights = DecoderWeights.random(config, seed=0, dtype=torch.float16, device=device)
+    prompts = _prompts()
+    runs = {}
+    for size in (16, block_size):
+        cache = _cache(config, device, pages=128 * 16 // size + 8, block_size=size)
+        executor = BucketedDecodeExecutor(weights, cache, batch_buckets=(1, 2, 4),
+                                          context_buckets=(256, 512))
+        logits: dict[str, list[torch.Tensor]] = {}
+        runs[size] = (greedy_decode(executor, prompts, steps=32, logits=logits), logits)
+    (tokens16, logits16), (tokens_b, logits_b) = runs[16], runs[block_size]
+    assert tokens_b == tokens16
+    for rid in prompts:
+        assert len(logits_b[rid]) == len(logits16[rid]) == 32
+        for step, (a, b) in enumerate(zip(logits_b[rid], logits16[rid])):
+            assert torch.equal(a, b), f"{rid} step {step}: pages of {block_size} differ"
 
 
 def test_greedy_decode_matches_the_oracle(device):
