@@ -493,20 +493,25 @@ def measure_decode_step(weights: DecoderWeights, batch: int, context: int, *,
         raise RuntimeError(f"prefill failed: {errors}")
     budget = context - prompt_length
     warm = min(4, budget // 4)
-    timed = min(steps, budget - warm - 1)
+    timed = min(steps, budget - warm - 2)
     pending = executor.launch(rids, tokens)
-    for _ in range(warm - 1):
+    for _ in range(warm):
         ticket = executor.launch(rids)
         executor.collect(pending)
         pending = ticket
+    # The clock starts when a step has just been collected, with the next
+    # one already queued, and stops when the timed-th step after it has been
+    # collected: exactly `timed` step completions with the pipeline full.
+    # (Starting it with a step in flight would count that step's remainder
+    # too: about one step more than `timed`.)
     executor.step_records.clear()
     begin = time.perf_counter()
     for _ in range(timed):
         ticket = executor.launch(rids)
         executor.collect(pending)
         pending = ticket
-    executor.collect(pending)
     host_ms = (time.perf_counter() - begin) * 1e3 / timed
+    executor.collect(pending)
     times = sorted(r.device_ms for r in executor.step_records[1:])
     p50 = times[len(times) // 2]
     return {
