@@ -200,6 +200,7 @@ def config3(device: torch.device, calls: int) -> list[dict]:
     tuned = dict(selected_attention_autotune_config() or {})
     launch = selected_attention_launch() or {}
     results.append(report(f"{name}, entry point plan (balanced partitions, "
+                          f"{launch.get('heads_per_workgroup')} kv heads per workgroup, "
                           f"{launch.get('waves_per_head')} wavefronts each), merge launch", us,
                           nbytes, record=tuned))
 
@@ -207,7 +208,8 @@ def config3(device: torch.device, calls: int) -> list[dict]:
     try:
         us = graph_time_us(entry, calls, device)
         launch = selected_attention_launch() or {}
-        results.append(report(f"{name}, 512-token partitions ({launch.get('waves_per_head')} "
+        results.append(report(f"{name}, 512-token partitions ({launch.get('heads_per_workgroup')} "
+                              f"kv heads per workgroup, {launch.get('waves_per_head')} "
                               f"wavefronts each), merge launch (BASELINE form)", us,
                               nbytes, record=dict(selected_attention_autotune_config() or {})))
     finally:

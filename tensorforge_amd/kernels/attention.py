@@ -155,23 +155,35 @@ NARROW_WAVES = 8
 NARROW_SPLIT_WAVES = 4
 NARROW_TOKENS_PER_WAVE = 64
 # Narrow split-KV calls of at least this context and 2..64 rows size their
-# partitions on the device from the rows' lengths (balanced_slots_for); the
+# partitions on the device from the rows' lengths (balanced_geometry); the
 # compact grid holds one workgroup per compute unit, each partition streamed
-# by BALANCED_WAVES wavefronts (config 3 on MI355X: 64.4-64.6 us with 2,
-# 65.4-65.7 with 4, 67.7-68.2 with 6 or 8, 92.5 with 1; fixed 4096-token
-# partitions with 4: 70.8-71.9).
+# by BALANCED_WAVES wavefronts per kv head (config 3 on MI355X, one kv head
+# per workgroup: 64.4-64.6 us with 2, 65.4-65.7 with 4, 67.7-68.2 with 6 or
+# 8, 92.5 with 1; fixed 4096-token partitions with 4: 70.8-71.9).  A
+# workgroup serves up to BALANCED_MAX_HEADS_PER_WG kv heads of a partition
+# at once, so its wavefronts read whole token rows (one kv head's slice is
+# a quarter or less of a row) and the partitions are that many times
+# shorter (MI355X, graph-timed: config 3 64.4 -> 62.7 -> 61.8 us with 1, 2,
+# 4 kv heads per workgroup; 8 x 16k 99.6 -> 91.5 with 2; 4 x 32k at 32/4
+# heads, D 64 36.5 -> 31.1 with 2; 6 ragged rows of 8k-31k 75.9 -> 72.5).
 BALANCED_MIN_CONTEXT = 8192
 BALANCED_WAVES = 2
+BALANCED_MAX_HEADS_PER_WG = 4
 # Partitions of a caller-fixed size (set_attention_split_size, or
 # attention_path="split_kv") are streamed by two wavefronts each, four
 # above 768 tokens, all of them on every partition (measured on MI355X
 # against one wavefront per partition, merge launch included: config 3 in
 # the BASELINE's 512-token partitions 119.7 -> 85.1 us; config 2 at 256 /
 # 512 / 1024 tokens 32.6 / 33.3 / 34.0 -> 27.0 / 25.1 / 24.3 us (2) and
-# 25.9 (4 at 1024); 16 x 4096 and 4 x 2048 rows 10-30% faster).
+# 25.9 (4 at 1024); 16 x 4096 and 4 x 2048 rows 10-30% faster).  Partitions
+# of 512-768 tokens go to workgroups of two kv heads, so their wavefronts
+# read whole token rows (config 3 at 512 tokens 76.1 -> 71.6 us, config 2
+# 25.4 -> 24.5; at 256 tokens config 2 is 26.4 against 26.9, so shorter
+# partitions keep one kv head per workgroup).
 FIXED_SPLIT_WAVES = 2
 FIXED_SPLIT_WAVES_WIDE = 4
 FIXED_SPLIT_WIDE = 768
+FIXED_SPLIT_PAIRED = 512
 COMPUTE_UNITS = 256  # MI355X
 
 
@@ -189,18 +201,22 @@ class AttentionPlan:
     tokens_per_wave: int = ONE_PASS_TOKENS_PER_WAVE
     # Split-KV with partitions sized on the device from the rows' lengths
     # (TF_ATTENTION_FLAG_BALANCED): split_size is then the smallest partition
-    # and num_splits the slots per kv head over all rows together.
+    # and num_splits the slots per group of heads_per_wg kv heads over all
+    # rows together.
     balanced: bool = False
+    # kv heads one workgroup serves (its wavefronts: heads_per_wg x
+    # waves_per_head).
+    heads_per_wg: int = 1
 
     @property
     def flags(self) -> int:
         """The C ABI's launch flags: several wavefronts per kv head (none for
-        one) and the balanced partitions."""
+        one), several kv heads per workgroup and the balanced partitions."""
 
         flags = _native.TF_ATTENTION_FLAG_BALANCED if self.balanced else 0
-        if self.waves_per_head <= 1:
+        if self.waves_per_head <= 1 and self.heads_per_wg <= 1:
             return flags
-        return (flags | (1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
+        return (flags | (self.heads_per_wg << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
                 | (self.waves_per_head << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
                 | ((self.tokens_per_wave // 64) << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
 
@@ -234,24 +250,41 @@ def narrow_split_size_for(max_context_length: int, batch: int, kv_heads: int) ->
     )
 
 
-def balanced_slots_for(max_context_length: int, batch: int, kv_heads: int) -> int:
-    """Slots per kv head of a balanced split-KV call, or 0 where the call
-    keeps fixed partitions: one slot per compute unit and kv head
-    (``COMPUTE_UNITS // kv_heads``), so the compact grid is one workgroup
-    per compute unit.  Only for 2..64 rows of at least BALANCED_MIN_CONTEXT
-    tokens, where rows of unequal length leave fixed partitions unevenly
-    spread (config 3: rows of 8k..32k in 4096-token partitions give 160 of
-    256 workgroups work); the slots must outnumber the rows (the device-side
-    partition size needs it) and fit one per 256 tokens of the context, so
-    the workspace the reference sizes for 256-token partitions holds the
-    partials ([row][query head][slot], as for fixed partitions)."""
+def balanced_geometry(max_context_length: int, batch: int, kv_heads: int) -> tuple[int, int]:
+    """Slots and kv heads per workgroup of a balanced split-KV call, or
+    (0, 1) where the call keeps fixed partitions.
+
+    A workgroup serves ``heads_per_wg`` kv heads of one partition (the
+    largest of BALANCED_MAX_HEADS_PER_WG, ..., 2, 1 that divides kv_heads
+    and fits), and there is one slot per compute unit and group of kv heads
+    (``COMPUTE_UNITS * heads_per_wg // kv_heads``), so the compact grid is
+    one workgroup per compute unit.  Only for 2..64 rows of at least
+    BALANCED_MIN_CONTEXT tokens, where rows of unequal length leave fixed
+    partitions unevenly spread (config 3: rows of 8k..32k in 4096-token
+    partitions give 160 of 256 workgroups work); the slots must outnumber
+    the rows (the device-side partition size needs it) and fit one per 256
+    tokens of the context, so the workspace the reference sizes for
+    256-token partitions holds the partials ([row][query head][slot], as
+    for fixed partitions)."""
 
     if batch < 2 or batch > 64 or max_context_length < BALANCED_MIN_CONTEXT:
-        return 0
-    slots = COMPUTE_UNITS // max(kv_heads, 1)
-    if slots <= batch or slots > -(-max_context_length // REFERENCE_SPLIT_SIZE):
-        return 0
-    return slots
+        return 0, 1
+    limit = -(-max_context_length // REFERENCE_SPLIT_SIZE)
+    heads = BALANCED_MAX_HEADS_PER_WG
+    while heads >= 1:
+        if kv_heads % heads == 0:
+            slots = COMPUTE_UNITS * heads // max(kv_heads, 1)
+            if batch < slots <= limit:
+                return slots, heads
+        heads //= 2
+    return 0, 1
+
+
+def balanced_slots_for(max_context_length: int, batch: int, kv_heads: int) -> int:
+    """Slots per group of kv heads of a balanced split-KV call, or 0 where
+    the call keeps fixed partitions (balanced_geometry)."""
+
+    return balanced_geometry(max_context_length, batch, kv_heads)[0]
 
 
 def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capacity: int,
@@ -276,9 +309,10 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
       size of narrow_split_size_for (1 x 4k: 11.9 against 13.5 us; 8 x 4k:
       14.2 against 15.5; config 3, 4 x 8-32k x 8 kv heads at D 128: 74.7
       against 78.4), or for 2..64 rows of >= 8k the balanced partitions of
-      balanced_slots_for, sized on the device from the rows' lengths, with
-      two wavefronts each (config 3: 64.5 against 70.8-71.9 us for fixed
-      4096-token partitions);
+      balanced_geometry, sized on the device from the rows' lengths, with
+      up to four kv heads per workgroup and two wavefronts per kv head
+      (config 3: 61.8 us with four kv heads per workgroup, 64.5 with one,
+      against 70.8-71.9 us for fixed 4096-token partitions);
     * a partition size fixed by the caller (set_attention_split_size) or
       ``attention_path="split_kv"``: split-KV (size attention_split_size_for
       unless fixed) with two wavefronts per partition, four above 768
@@ -295,8 +329,9 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
                                             and launch_context <= split_size):
             return AttentionPlan(True, capacity32, 1, 1)
         waves = FIXED_SPLIT_WAVES if split_size <= FIXED_SPLIT_WIDE else FIXED_SPLIT_WAVES_WIDE
+        heads = 2 if FIXED_SPLIT_PAIRED <= split_size <= FIXED_SPLIT_WIDE and kv_heads % 2 == 0 else 1
         return AttentionPlan(False, split_size, (launch_context + split_size - 1) // split_size,
-                             waves, 0)
+                             waves, 0, heads_per_wg=heads)
     if workgroups >= ONE_PASS_MIN_WORKGROUPS:
         tokens = wide_tokens_per_wave(launch_context)
         waves = max(1, min(8, -(-launch_context // tokens)))
@@ -304,11 +339,11 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
     if (attention_path == "one_pass" or launch_context <= NARROW_ONE_PASS_CONTEXT
             or (workgroups >= NARROW_ONE_PASS_MIN_WORKGROUPS and launch_context <= 2048)):
         return AttentionPlan(True, capacity32, 1, NARROW_WAVES, NARROW_TOKENS_PER_WAVE)
-    slots = balanced_slots_for(launch_context, batch, kv_heads)
+    slots, heads = balanced_geometry(launch_context, batch, kv_heads)
     if slots:
         smallest = (-(-launch_context // slots) + 63) // 64 * 64
         return AttentionPlan(False, smallest, slots, BALANCED_WAVES, NARROW_TOKENS_PER_WAVE,
-                             balanced=True)
+                             balanced=True, heads_per_wg=heads)
     narrow = narrow_split_size_for(launch_context, batch, kv_heads)
     return AttentionPlan(False, narrow, (launch_context + narrow - 1) // narrow,
                          NARROW_SPLIT_WAVES, NARROW_TOKENS_PER_WAVE)
@@ -405,7 +440,7 @@ def paged_gqa_decode_attention(
     if plan.balanced and kernel != "mfma":
         # The generic kernel takes fixed partitions: the same slots of the
         # smallest size still cover the context.
-        plan = dataclasses.replace(plan, balanced=False)
+        plan = dataclasses.replace(plan, balanced=False, heads_per_wg=1)
     device = query.device
     stream = _native.current_stream(device)
     counters_ptr = None
@@ -524,11 +559,13 @@ def paged_gqa_decode_attention(
             "kernel": kernel,
             "workgroup": "sequence x kv_head",
         }
+    heads = plan.heads_per_wg if kernel == "mfma" else 1
     _LAST_ATTENTION_LAUNCH = {
         "kernel": kernel,
         "waves_per_head": plan.waves_per_head if kernel == "mfma" else 1,
-        "grid": ((kv_heads * num_splits, 1) if use_split_kv and plan.balanced
-                 else (batch * kv_heads, num_splits)),
+        "grid": ((kv_heads // heads * num_splits, 1) if use_split_kv and plan.balanced
+                 else (batch * kv_heads // heads, num_splits)),
+        "heads_per_workgroup": heads,
         "in_kernel_merge": bool(use_split_kv and counters_ptr is not None),
         "balanced_partitions": bool(use_split_kv and plan.balanced),
         "group_size": group,

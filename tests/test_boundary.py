@@ -314,12 +314,18 @@ def test_attention_plan() -> None:
     with up to 8 wavefronts (one per 64 tokens) at short contexts and
     split-KV with up to 4 wavefronts per split at long ones (the reference's
     own 1 x 8 case keeps its 256-token partitions), with balanced
-    partitions -- one slot per compute unit and kv head, the size set on the
-    device -- for 2..64 rows of >= 8k when the slots fit one per 256 tokens
-    (cfg3: 32 slots of >= 1024 tokens); one wavefront per split when the
-    caller fixes the partition size or forces split-KV."""
+    partitions -- up to four kv heads per workgroup, one slot per compute
+    unit and group of kv heads, the size set on the device -- for 2..64
+    rows of >= 8k when the slots fit one per 256 tokens (cfg3: four kv
+    heads per workgroup, 128 slots of >= 256 tokens); two wavefronts per
+    split when the caller fixes the partition size or forces split-KV (four
+    above 768 tokens), with two kv heads per workgroup for 512-768 tokens."""
 
-    from tensorforge_amd.kernels.attention import balanced_slots_for, narrow_split_size_for
+    from tensorforge_amd.kernels.attention import (
+        balanced_geometry,
+        balanced_slots_for,
+        narrow_split_size_for,
+    )
 
     cfg2 = attention_plan(2048, 72, 4, 2048)
     assert (cfg2.one_pass, cfg2.num_splits, cfg2.waves_per_head) == (True, 1, 4)
@@ -339,9 +345,16 @@ def test_attention_plan() -> None:
     long8 = attention_plan(4000, 8, 4, 4096)
     assert (long8.one_pass, long8.split_size, long8.num_splits) == (False, 512, 8)
     cfg3 = attention_plan(32768, 4, 8, 32768)
-    assert (cfg3.one_pass, cfg3.split_size, cfg3.num_splits, cfg3.balanced) == (False, 1024, 32,
+    assert (cfg3.one_pass, cfg3.split_size, cfg3.num_splits, cfg3.balanced) == (False, 256, 128,
                                                                                 True)
-    assert cfg3.flags == 32 | (1 << 24) | (1 << 20) | (2 << 8)
+    assert cfg3.heads_per_wg == 4
+    assert cfg3.flags == 32 | (1 << 24) | (4 << 20) | (2 << 8)
+    assert balanced_geometry(32768, 4, 8) == (128, 4)
+    assert balanced_geometry(16384, 8, 8) == (64, 2)   # 128 slots > 16384 / 256
+    assert balanced_geometry(12032, 16, 8) == (32, 1)
+    assert balanced_geometry(32768, 4, 4) == (128, 2)  # 256 slots > 32768 / 256
+    assert balanced_geometry(32768, 4, 6) == (85, 2)     # 3 groups of 2 kv heads x 85
+    assert balanced_geometry(65536, 4, 2) == (256, 2)
     assert balanced_slots_for(32768, 1, 8) == 0      # one row: fixed partitions
     assert balanced_slots_for(8191, 4, 8) == 0       # below 8k
     assert balanced_slots_for(8192, 8, 4) == 0       # 64 slots > 8192 / 256
@@ -359,13 +372,19 @@ def test_attention_plan() -> None:
     assert attention_plan(32768, 64, 4, 32768).waves_per_head == 8
     forced = attention_plan(2048, 72, 4, 2048, "split_kv")
     assert (forced.one_pass, forced.split_size, forced.waves_per_head) == (False, 576, 2)
+    assert forced.heads_per_wg == 2
     assert forced.tokens_per_wave == 0  # every wavefront streams its share of the partition
     previous = set_attention_split_size(512)
     try:
         fixed = attention_plan(2048, 72, 4, 2048)
         assert (fixed.one_pass, fixed.split_size, fixed.num_splits) == (False, 512, 4)
-        assert fixed.flags == ((1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
+        # 512-768-token partitions: two kv heads per workgroup
+        assert fixed.flags == ((2 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
                                | (2 << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT))
+        set_attention_split_size(256)
+        assert attention_plan(2048, 72, 4, 2048).heads_per_wg == 1
+        assert attention_plan(2048, 72, 3, 2048).heads_per_wg == 1  # odd kv heads
+        set_attention_split_size(512)
         assert attention_plan(400, 2, 4, 2048).waves_per_head == 1  # one pass
         set_attention_split_size(1024)
         assert attention_plan(32768, 4, 8, 32768).waves_per_head == 4

@@ -237,9 +237,9 @@ def test_llama3_long_context_split_kv(device):
 
 def test_llama3_long_context_auto_plan(device):
     """BASELINE config 3 under the entry point's own plan: partitions sized
-    on the device from the rows' lengths (at least 1024 tokens, 32 slots per
-    kv head) with two wavefronts each (whole-row loads at D 128), then the
-    merge launch."""
+    on the device from the rows' lengths (at least 256 tokens, 128 slots per
+    group of four kv heads) with two wavefronts per kv head (whole-row loads
+    at D 128), then the merge launch."""
 
     case = llama3_long_context_case(seed=1)
     gpu = case.to(device)
@@ -248,9 +248,10 @@ def test_llama3_long_context_auto_plan(device):
         max_context_length=32768,
     )
     assert selected_attention_autotune_config() == {
-        "path": "split_kv", "split_size": 1024, "num_splits": 32,
+        "path": "split_kv", "split_size": 256, "num_splits": 128,
     }
     assert selected_attention_launch()["waves_per_head"] == 2
+    assert selected_attention_launch()["heads_per_workgroup"] == 4
     assert selected_attention_launch()["balanced_partitions"]
     _check_against_oracle(case, output.cpu(), NORTH_STAR_ATOL, NORTH_STAR_RTOL, "cfg3 auto")
 

@@ -39,10 +39,10 @@ pytestmark = pytest.mark.gpu
 UNSUPPORTED = 2  # TF_ERROR_UNSUPPORTED
 
 
-def _wave_flags(waves_per_head: int, tokens_per_wave: int = 64) -> int:
-    if waves_per_head <= 1:
+def _wave_flags(waves_per_head: int, tokens_per_wave: int = 64, heads_per_wg: int = 1) -> int:
+    if waves_per_head <= 1 and heads_per_wg <= 1:
         return 0
-    return ((1 << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
+    return ((heads_per_wg << _native.TF_ATTENTION_HEADS_PER_WG_SHIFT)
             | (waves_per_head << _native.TF_ATTENTION_WAVES_PER_CU_SHIFT)
             | ((tokens_per_wave // 64) << _native.TF_ATTENTION_TOKENS_PER_WAVE_SHIFT))
 
@@ -107,21 +107,36 @@ CASES = {
 }
 
 
+@pytest.mark.parametrize("heads_per_wg", [1, 2, 4])
 @pytest.mark.parametrize("name", sorted(CASES))
-def test_balanced_partitions_match_oracle_and_fixed_partitions(device, name):
+def test_balanced_partitions_match_oracle_and_fixed_partitions(device, name, heads_per_wg):
+    """Also with 2 and 4 kv heads per workgroup (the slots then count
+    groups of kv heads): bit-identical to one kv head per workgroup, since a
+    kv head's partition is dealt over its own wavefronts the same way."""
+
     lengths, hq, hkv, d, page, dtype, slots, smallest, waves = CASES[name]
+    if hkv % heads_per_wg or heads_per_wg * waves > 8:
+        pytest.skip("kv heads per workgroup must divide the kv heads and fit 8 wavefronts")
     assert max(lengths) <= slots * smallest
     width = max((max(lengths) + page - 1) // page, 1) + 2
     case = make_decode_attention_case(lengths, query_heads=hq, kv_heads=hkv, head_dim=d,
                                       block_size=page, dtype=dtype, seed=len(lengths) + d,
                                       table_width=width)
     gpu = case.to(device)
-    flags = _wave_flags(waves)
+    flags = _wave_flags(waves, heads_per_wg=heads_per_wg)
     out = torch.full_like(gpu.query, float("nan"))
     status, _ = _call(gpu, out, flags | _native.TF_ATTENTION_FLAG_BALANCED, smallest, slots)
     assert status == 0, _native.library().tf_last_error()
     torch.cuda.synchronize()
     _check(case, out, f"balanced {name}")
+    if heads_per_wg > 1:
+        one = torch.full_like(gpu.query, float("nan"))
+        status, _ = _call(gpu, one, _wave_flags(waves) | _native.TF_ATTENTION_FLAG_BALANCED,
+                          smallest, slots)
+        assert status == 0, _native.library().tf_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), one.view(torch.int16)), (
+            f"{name}: {heads_per_wg} kv heads per workgroup differ from one")
 
     size = _partition_size(lengths, smallest, slots, width * page)
     fixed_splits = max(1, -(-min(slots * smallest, width * page) // size))
@@ -156,7 +171,8 @@ def test_sixty_four_rows(device):
 
 def test_config3_entry_point_plan(device):
     """BASELINE config 3 through the entry point: 2..64 rows of >= 8k take
-    balanced partitions (32 slots per kv head on 256 compute units)."""
+    balanced partitions (four kv heads per workgroup, 128 slots per group of
+    four on 256 compute units)."""
 
     case = llama3_long_context_case(seed=2)
     gpu = case.to(device)
@@ -164,11 +180,12 @@ def test_config3_entry_point_plan(device):
                                         gpu.block_tables, gpu.context_lengths,
                                         max_context_length=32768)
     assert selected_attention_autotune_config() == {
-        "path": "split_kv", "split_size": 1024, "num_splits": 32,
+        "path": "split_kv", "split_size": 256, "num_splits": 128,
     }
     launch = selected_attention_launch()
     assert launch["balanced_partitions"] and launch["waves_per_head"] == 2
-    assert launch["grid"] == (8 * 32, 1)
+    assert launch["heads_per_workgroup"] == 4
+    assert launch["grid"] == (2 * 128, 1)
     _check(case, output, "cfg3 balanced")
 
 
