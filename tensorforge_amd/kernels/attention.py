@@ -250,7 +250,8 @@ def narrow_split_size_for(max_context_length: int, batch: int, kv_heads: int) ->
     )
 
 
-def balanced_geometry(max_context_length: int, batch: int, kv_heads: int) -> tuple[int, int]:
+def balanced_geometry(max_context_length: int, batch: int, kv_heads: int,
+                      slot_limit: int | None = None) -> tuple[int, int]:
     """Slots and kv heads per workgroup of a balanced split-KV call, or
     (0, 1) where the call keeps fixed partitions.
 
@@ -262,14 +263,16 @@ def balanced_geometry(max_context_length: int, batch: int, kv_heads: int) -> tup
     BALANCED_MIN_CONTEXT tokens, where rows of unequal length leave fixed
     partitions unevenly spread (config 3: rows of 8k..32k in 4096-token
     partitions give 160 of 256 workgroups work); the slots must outnumber
-    the rows (the device-side partition size needs it) and fit one per 256
-    tokens of the context, so the workspace the reference sizes for
-    256-token partitions holds the partials ([row][query head][slot], as
-    for fixed partitions)."""
+    the rows (the device-side partition size needs it) and fit the
+    workspace, whose partials keep the fixed-partition layout ([row][query
+    head][slot]): ``slot_limit`` slots per (row, query head), by default one
+    per 256 tokens of the context, what the workspace the reference sizes
+    for 256-token partitions holds."""
 
     if batch < 2 or batch > 64 or max_context_length < BALANCED_MIN_CONTEXT:
         return 0, 1
-    limit = -(-max_context_length // REFERENCE_SPLIT_SIZE)
+    limit = (-(-max_context_length // REFERENCE_SPLIT_SIZE) if slot_limit is None
+             else slot_limit)
     heads = BALANCED_MAX_HEADS_PER_WG
     while heads >= 1:
         if kv_heads % heads == 0:
@@ -288,7 +291,7 @@ def balanced_slots_for(max_context_length: int, batch: int, kv_heads: int) -> in
 
 
 def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capacity: int,
-                   attention_path: str = "auto") -> AttentionPlan:
+                   attention_path: str = "auto", slot_limit: int | None = None) -> AttentionPlan:
     """The launch of a call from host-known sizes only.
 
     The reference runs one pass unless the batch has few programs
@@ -339,7 +342,7 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
     if (attention_path == "one_pass" or launch_context <= NARROW_ONE_PASS_CONTEXT
             or (workgroups >= NARROW_ONE_PASS_MIN_WORKGROUPS and launch_context <= 2048)):
         return AttentionPlan(True, capacity32, 1, NARROW_WAVES, NARROW_TOKENS_PER_WAVE)
-    slots, heads = balanced_geometry(launch_context, batch, kv_heads)
+    slots, heads = balanced_geometry(launch_context, batch, kv_heads, slot_limit)
     if slots:
         smallest = (-(-launch_context // slots) + 63) // 64 * 64
         return AttentionPlan(False, smallest, slots, BALANCED_WAVES, NARROW_TOKENS_PER_WAVE,
@@ -430,7 +433,15 @@ def paged_gqa_decode_attention(
         raise ValueError("output must be contiguous and share query shape, dtype, and device")
     attention_scale = head_dim**-0.5 if scale is None else scale
 
-    plan = attention_plan(launch_context, batch, kv_heads, context_capacity, attention_path)
+    # Balanced partitions may take as many slots as the partials' workspace
+    # holds per (row, query head): the caller's, or the one allocated below.
+    if workspace is not None:
+        slot_limit = min(workspace.partial_max.numel(), workspace.partial_sum.numel(),
+                         workspace.partial_accumulator.shape[0]) // max(batch * query_heads, 1)
+    else:
+        slot_limit = COMPUTE_UNITS * BALANCED_MAX_HEADS_PER_WG
+    plan = attention_plan(launch_context, batch, kv_heads, context_capacity, attention_path,
+                          slot_limit)
     use_split_kv = not plan.one_pass
     split_size = plan.split_size
     dtype = _native.dtype_code(query.dtype)
@@ -644,11 +655,12 @@ def paged_gqa_decode_attention_rope_append(
     context_capacity = table_width * block_size
     if max_context_length <= 0 or max_context_length > context_capacity:
         raise ValueError("max_context_length must be positive and within table capacity")
-    plan = attention_plan(max_context_length, batch, kv_heads, context_capacity)
-    head_bucket = _next_power_of_2(head_dim)
-    partial_programs = batch * query_heads * plan.num_splits
     capacity = min(workspace.partial_max.numel(), workspace.partial_sum.numel(),
                    workspace.partial_accumulator.shape[0])
+    plan = attention_plan(max_context_length, batch, kv_heads, context_capacity,
+                          slot_limit=capacity // max(batch * query_heads, 1))
+    head_bucket = _next_power_of_2(head_dim)
+    partial_programs = batch * query_heads * plan.num_splits
     if not plan.one_pass and (capacity < partial_programs
                               or workspace.partial_accumulator.shape[1] != head_bucket):
         raise ValueError("split-KV workspace has insufficient or incompatible capacity")

@@ -189,6 +189,35 @@ def test_config3_entry_point_plan(device):
     _check(case, output, "cfg3 balanced")
 
 
+def test_many_long_rows_take_the_slots_their_workspace_holds(device):
+    """16 rows of 8k-9k: with the entry point's own workspace the plan takes
+    four kv heads per workgroup and 128 slots; a workspace sized as the
+    reference sizes it (one partial per 256 tokens of a row) holds only 36
+    slots per row, so the plan drops to 32 slots of one kv head.  Both
+    match the oracle."""
+
+    lengths = [8192 + 64 * i for i in range(16)]
+    case = make_decode_attention_case(lengths, query_heads=32, kv_heads=8, head_dim=128,
+                                      block_size=16, dtype=torch.bfloat16, seed=16)
+    gpu = case.to(device)
+    output = paged_gqa_decode_attention(gpu.query, gpu.key_cache, gpu.value_cache,
+                                        gpu.block_tables, gpu.context_lengths)
+    launch = selected_attention_launch()
+    assert launch["balanced_partitions"] and launch["heads_per_workgroup"] == 4
+    assert launch["grid"] == (2 * 128, 1)
+    _check(case, output, "16 long rows, own workspace")
+    workspace = PagedAttentionWorkspace.allocate(batch_capacity=16, query_heads=32,
+                                                 head_dim=128, max_context_length=max(lengths),
+                                                 device=device)
+    output = paged_gqa_decode_attention(gpu.query, gpu.key_cache, gpu.value_cache,
+                                        gpu.block_tables, gpu.context_lengths,
+                                        workspace=workspace)
+    launch = selected_attention_launch()
+    assert launch["balanced_partitions"] and launch["heads_per_workgroup"] == 1
+    assert launch["grid"] == (8 * 32, 1)
+    _check(case, output, "16 long rows, reference-sized workspace")
+
+
 def test_graph_replay_follows_device_lengths(device):
     """The partition size is recomputed from the device lengths on every
     replay: shrink and grow the rows between replays of one graph."""
