@@ -107,16 +107,19 @@ CASES = {
 }
 
 
-@pytest.mark.parametrize("heads_per_wg", [1, 2, 4])
-@pytest.mark.parametrize("name", sorted(CASES))
+# Each case with 1, 2 and 4 kv heads per workgroup where they divide its kv
+# heads and fit 8 wavefronts.
+HEADS_CASES = [(name, heads) for name in sorted(CASES) for heads in (1, 2, 4)
+               if CASES[name][2] % heads == 0 and heads * CASES[name][8] <= 8]
+
+
+@pytest.mark.parametrize(("name", "heads_per_wg"), HEADS_CASES)
 def test_balanced_partitions_match_oracle_and_fixed_partitions(device, name, heads_per_wg):
     """Also with 2 and 4 kv heads per workgroup (the slots then count
     groups of kv heads): bit-identical to one kv head per workgroup, since a
     kv head's partition is dealt over its own wavefronts the same way."""
 
     lengths, hq, hkv, d, page, dtype, slots, smallest, waves = CASES[name]
-    if hkv % heads_per_wg or heads_per_wg * waves > 8:
-        pytest.skip("kv heads per workgroup must divide the kv heads and fit 8 wavefronts")
     assert max(lengths) <= slots * smallest
     width = max((max(lengths) + page - 1) // page, 1) + 2
     case = make_decode_attention_case(lengths, query_heads=hq, kv_heads=hkv, head_dim=d,
