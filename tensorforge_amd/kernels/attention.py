@@ -688,6 +688,11 @@ def selected_attention_autotune_config() -> dict[str, Any] | None:
 
 
 def selected_attention_launch() -> dict[str, Any] | None:
-    """Kernel family and grid of the last call (no reference counterpart)."""
+    """Launch details of the last call (no reference counterpart): the
+    kernel family ("mfma" or "generic"), ``waves_per_head`` (wavefronts per
+    kv head), ``heads_per_workgroup`` (kv heads one workgroup serves),
+    ``grid`` (workgroups as (x, y)), ``balanced_partitions`` (partition
+    size set on the device), ``in_kernel_merge``, ``group_size`` and
+    ``launch_context``."""
 
     return _LAST_ATTENTION_LAUNCH
