@@ -91,8 +91,9 @@ enum tf_attention_variant {
 
 /* tf_paged_gqa_decode* flags.  FORCE_GENERIC selects the generic family.
  * Tuning fields of the MFMA grid kernel (0 selects the defaults):
- *   bits 8-15   wavefronts per kv head (heads x this <= 8)
- *   bits 20-23  kv heads per workgroup (must divide kv_heads)
+ *   bits 8-15   wavefronts per kv head (heads x this <= 8, else 1)
+ *   bits 20-23  kv heads per workgroup, which read the same token rows
+ *               together (must divide kv_heads and be <= 8, else 1)
  *   bits 24-30  tokens per wavefront / 64; a row then uses ceil(its tokens
  *               / that) of the head's wavefronts (0: all)
  * Other bits (2, 4, 8, 64, 128 and bits 16-19) are rejected with
@@ -106,9 +107,10 @@ enum tf_attention_variant {
  * rows' lengths on the device instead of using split_size for every row:
  * with total = the sum of the (clamped) lengths, every row is cut into
  * partitions of max(split_size, ceil32(ceil(total / (num_splits - batch))))
- * tokens, at most num_splits per kv head over all rows together, and the
- * launch is one compact grid of (kv_heads / heads per workgroup) x
- * num_splits workgroups that take those partitions in row order.  Ragged
+ * tokens, at most num_splits per group of kv heads (heads per workgroup)
+ * over all rows together, and the launch is one compact grid of
+ * (kv_heads / heads per workgroup) x num_splits workgroups that take those
+ * partitions in row order.  Ragged
  * long rows then spread over the grid evenly where fixed partitions leave
  * most of it without work.  Partials land in slot j < ceil(len / partition)
  * of their row, as with fixed partitions; the merge recomputes the size. */
