@@ -46,6 +46,7 @@
 //   reduce kernel     triton_attention.py:268-316 (LSE merge :288-316)
 //   oracle            kernels/reference.py:46-93
 #include <mutex>
+#include <type_traits>
 
 #include "tf_common.hpp"
 
@@ -112,6 +113,37 @@ __device__ __forceinline__ int32_t clamp_context(const AttnParams &p, int32_t b)
   return ctx;
 }
 
+// Integer wavefront reductions by DPP lane moves within each 16-lane row and
+// lane reads across the four rows (no LDS-routed shuffles; the whole
+// wavefront must be active).  A DPP source lane outside the row reads 0.
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_int(int32_t v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
+}
+// Sum over the 64 lanes (every lane gets it): quad_perm [1,0,3,2] and
+// [2,3,0,1], row_half_mirror and row_mirror give each lane its row's sum.
+__device__ __forceinline__ int32_t wave64_isum(int32_t v) {
+  v += dpp_int<0xb1>(v);
+  v += dpp_int<0x4e>(v);
+  v += dpp_int<0x141>(v);
+  v += dpp_int<0x140>(v);
+  return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
+}
+// Inclusive prefix sum over lanes 0..63: row_shr 1, 2, 4, 8 within each row
+// (Hillis-Steele), then the earlier rows' totals added.
+__device__ __forceinline__ int32_t wave64_iscan(int32_t v) {
+  v += dpp_int<0x111>(v);
+  v += dpp_int<0x112>(v);
+  v += dpp_int<0x114>(v);
+  v += dpp_int<0x118>(v);
+  const int32_t r0 = __builtin_amdgcn_readlane(v, 15);
+  const int32_t r01 = r0 + __builtin_amdgcn_readlane(v, 31);
+  const int32_t r012 = r01 + __builtin_amdgcn_readlane(v, 47);
+  const int row = (threadIdx.x & 63) >> 4;
+  return v + (row == 0 ? 0 : (row == 1 ? r0 : (row == 2 ? r01 : r012)));
+}
+
 // Partition size of a balanced split-KV call (TF_ATTENTION_FLAG_BALANCED),
 // the same in every workgroup and in the merge: with total = the sum of the
 // batch's clamped lengths, max(split_size, ceil32(ceil(total / (num_splits
@@ -127,9 +159,9 @@ __device__ __forceinline__ int32_t balanced_partition(const int32_t *lengths, in
   int32_t v = lane < batch ? lengths[lane] : 0;
   v = v < 0 ? 0 : (v > max_tokens ? max_tokens : v);
   len = v;
-  int64_t total = v;
-#pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) total += __shfl_xor(total, offset, 64);
+  // The lengths' sum in two 16-bit halves (each half's sum over 64 lanes
+  // fits in 32 bits), reduced with DPP moves and lane reads.
+  const int64_t total = (static_cast<int64_t>(wave64_isum(v >> 16)) << 16) + wave64_isum(v & 0xffff);
   const int64_t spare = num_splits - batch;
   int64_t size = ((total + spare - 1) / spare + 31) / 32 * 32;
   const int64_t longest = (static_cast<int64_t>(max_tokens) + 31) / 32 * 32;
@@ -144,17 +176,11 @@ __device__ __forceinline__ int32_t balanced_partition(const int32_t *lengths, in
 // results are wavefront-uniform.
 __device__ __forceinline__ void balanced_slot(const AttnParams &p, int32_t slot, int32_t &size,
                                               int32_t &row, int32_t &part) {
-  const int lane = threadIdx.x & 63;
   int32_t len;
   size = balanced_partition(p.context_lengths, p.batch, p.max_tokens, p.split_size,
                             p.num_splits, len);
   const int32_t n = (len + size - 1) / size;
-  int32_t incl = n;  // inclusive prefix sum of the partition counts over rows (lanes)
-#pragma unroll
-  for (int offset = 1; offset < 64; offset <<= 1) {
-    const int32_t below = __shfl_up(incl, offset, 64);
-    if (lane >= offset) incl += below;
-  }
+  const int32_t incl = wave64_iscan(n);  // inclusive prefix sum of the partition counts over rows (lanes)
   const int32_t excl = incl - n;
   const unsigned long long hit = __ballot(slot >= excl && slot < incl);
   row = -1;
@@ -162,7 +188,7 @@ __device__ __forceinline__ void balanced_slot(const AttnParams &p, int32_t slot,
   if (hit != 0) {
     const int r = __builtin_ctzll(hit);
     row = r;
-    part = slot - __shfl(excl, r, 64);
+    part = slot - __builtin_amdgcn_readlane(excl, r);
   }
   row = __builtin_amdgcn_readfirstlane(row);
   part = __builtin_amdgcn_readfirstlane(part);
@@ -529,6 +555,20 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += dpp_move<0x4e>(v);
   v += dpp_move<0x141>(v);
   return v + dpp_move<0x140>(v);
+}
+// Lane `l` of v (l wavefront-uniform).
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+// Max / sum over the 64 lanes: the rows' results combined by lane reads
+// (the same value on every lane).
+__device__ __forceinline__ float wave64_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+__device__ __forceinline__ float wave64_sum(float v) {
+  v = row16_sum(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
 // Wave-level layout of one 32-token chunk (tiles j = 0, 1 of 16 tokens):
@@ -1347,7 +1387,7 @@ size_t generic_lds_bytes(int D, int G) {
 // ===========================================================================
 // Log-sum-exp merge of split partials
 // ===========================================================================
-template <typename T>
+template <typename T, int NDIM>
 __global__ void __launch_bounds__(256)
 merge_partials_kernel(const float *__restrict__ partial_max, const float *__restrict__ partial_sum,
                       const float *__restrict__ partial_acc,
@@ -1355,43 +1395,45 @@ merge_partials_kernel(const float *__restrict__ partial_max, const float *__rest
                       int32_t query_heads, int32_t head_dim, int32_t split_size,
                       int32_t num_splits, int32_t partial_stride, int32_t max_tokens,
                       int32_t balanced) {
-  // One workgroup of W wavefronts per (row, query head).  Lane s holds the
-  // max and sum of split s (64 splits per pass); lanes over head_dim
-  // accumulate the weighted rows in batches of kBatch splits, every load of
-  // a batch in flight together.  Wavefront w takes batches w, w + W, ...;
-  // each batch's weighted sum starts from zero and the batch sums are
-  // added in batch order (by wavefront 0 through LDS when W > 1), so the
-  // result does not depend on W, and a row of <= kBatch splits gives
-  // exactly the one batch's sum.  The first batch of each wavefront is
-  // issued together with the max/sum loads (before the row length is
-  // known), so a row with <= W kBatch splits costs one memory round trip;
-  // loads of splits past the row's last one are discarded by a select.
+  // One workgroup of W wavefronts per (row, query head); NDIM = ceil(head_dim
+  // / 64) accumulator elements per lane (dims lane + 64 k).  Lane s holds the
+  // max and sum of split s (64 splits per pass) and, once the row's max and
+  // denominator are known, the weight of split s; the weighted rows are
+  // summed in batches of kBatch splits, every load of a batch in flight
+  // together, each split's weight taken from its lane with a lane read.
+  // Wavefront w takes batches w, w + W, ...; each batch's weighted sum
+  // starts from zero and the batch sums are added in batch order (by
+  // wavefront 0 through LDS when W > 1), so the result does not depend on W,
+  // and a row of <= kBatch splits gives exactly the one batch's sum.  The
+  // first batch of each wavefront is issued together with the max/sum loads
+  // (before the row length is known), so a row with <= W kBatch splits costs
+  // one memory round trip; loads of splits past the row's last one (clamped
+  // to the last slot) are never used.
   constexpr int kBatch = 16;
-  constexpr int kDims = 4;  // head_dim <= 256 = 4 x 64 lanes
-  extern __shared__ float batch_sums[];  // [batches][kDims][64] when W > 1
+  extern __shared__ float batch_sums[];  // [batches][NDIM][64] when W > 1
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int W = blockDim.x >> 6;
   const int32_t qh = blockIdx.x;
   const int32_t b = blockIdx.y;
   const int64_t base = (static_cast<int64_t>(b) * query_heads + qh) * num_splits;
   T *out = output + (static_cast<int64_t>(b) * query_heads + qh) * head_dim;
-  const int ndim = (head_dim + 63) / 64;
-  float v[kBatch][kDims];
+  const float *acc_rows = partial_acc + base * partial_stride;
+  int dim[NDIM];
+#pragma unroll
+  for (int k = 0; k < NDIM; ++k) dim[k] = min(lane + 64 * k, head_dim - 1);
+  float v[kBatch][NDIM];
   auto load_batch = [&](int32_t s0) {
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
-      const int32_t sj = min(s0 + j, num_splits - 1);
+      const float *row = acc_rows + static_cast<int64_t>(min(s0 + j, num_splits - 1)) * partial_stride;
 #pragma unroll
-      for (int k = 0; k < kDims; ++k) {
-        const int d = min(lane + 64 * k, head_dim - 1);
-        v[j][k] = k < ndim ? partial_acc[(base + sj) * partial_stride + d] : 0.f;
-      }
+      for (int k = 0; k < NDIM; ++k) v[j][k] = row[dim[k]];
     }
   };
   const int32_t first = min(lane, num_splits - 1);
-  float m = partial_max[base + first];
-  float l = partial_sum[base + first];
+  const float m0 = partial_max[base + first];
+  const float l0 = partial_sum[base + first];
   load_batch(kBatch * wave);
   int32_t ctx = context_lengths[b];
   ctx = ctx < 0 ? 0 : (ctx > max_tokens ? max_tokens : ctx);
@@ -1404,44 +1446,55 @@ merge_partials_kernel(const float *__restrict__ partial_max, const float *__rest
   // Max and sum over the valid splits (lanes beyond 64 splits in later passes).
   float gmax = kNegInf;
   for (int32_t s0 = 0; s0 < nvalid; s0 += 64) {
-    const float ms = s0 == 0 ? m : partial_max[base + min(s0 + lane, num_splits - 1)];
+    const float ms = s0 == 0 ? m0 : partial_max[base + min(s0 + lane, num_splits - 1)];
     gmax = fmaxf(gmax, s0 + lane < nvalid ? ms : kNegInf);
   }
-  gmax = wave_max(gmax);
+  gmax = wave64_max(gmax);
   float den = 0.f;
   if (gmax != kNegInf) {
     for (int32_t s0 = 0; s0 < nvalid; s0 += 64) {
       const int32_t sl = min(s0 + lane, num_splits - 1);
-      const float ms = s0 == 0 ? m : partial_max[base + sl];
-      const float ls = s0 == 0 ? l : partial_sum[base + sl];
+      const float ms = s0 == 0 ? m0 : partial_max[base + sl];
+      const float ls = s0 == 0 ? l0 : partial_sum[base + sl];
       if (s0 + lane < nvalid && ms != kNegInf) den += ls * fast_exp2(ms - gmax);
     }
   }
-  den = wave_sum(den);
+  den = wave64_sum(den);
   const float inv = den > 0.f ? 1.f / den : 0.f;
+  // Lane s's weight of split 64 pass + s (0 for a partial with no tokens).
+  auto pass_weight = [&](int32_t pass) -> float {
+    const float ms = pass == 0 ? m0 : partial_max[base + min(64 * pass + lane, num_splits - 1)];
+    return ms == kNegInf ? 0.f : fast_exp2(ms - gmax) * inv;
+  };
+  int32_t pass = 0;
+  float weight = pass_weight(0);
   const int32_t batches = (nvalid + kBatch - 1) / kBatch;
-  float total[kDims] = {0.f, 0.f, 0.f, 0.f};
+  float total[NDIM];
+#pragma unroll
+  for (int k = 0; k < NDIM; ++k) total[k] = 0.f;
   for (int32_t bi = wave; bi < batches; bi += W) {
     const int32_t s0 = bi * kBatch;
     if (bi != wave) load_batch(s0);
-    float num[kDims] = {0.f, 0.f, 0.f, 0.f};
+    if (s0 / 64 != pass) {
+      pass = s0 / 64;
+      weight = pass_weight(pass);
+    }
+    float num[NDIM];
+#pragma unroll
+    for (int k = 0; k < NDIM; ++k) num[k] = 0.f;
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
-      const int32_t sj = s0 + j;
-      if (sj >= nvalid) break;
-      // Weight of split sj: its max comes from lane sj % 64 of the pass
-      // holding it (the first pass's values are in registers).
-      const float msj = sj < 64 ? __shfl(m, sj, 64) : partial_max[base + sj];
-      const float w = msj == kNegInf ? 0.f : fast_exp2(msj - gmax) * inv;
+      if (s0 + j >= nvalid) break;
+      const float w = lane_value(weight, (s0 + j) & 63);
 #pragma unroll
-      for (int k = 0; k < kDims; ++k) num[k] += w * v[j][k];
+      for (int k = 0; k < NDIM; ++k) num[k] = fmaf(w, v[j][k], num[k]);
     }
     if (W == 1) {
 #pragma unroll
-      for (int k = 0; k < kDims; ++k) total[k] += num[k];
+      for (int k = 0; k < NDIM; ++k) total[k] += num[k];
     } else {
 #pragma unroll
-      for (int k = 0; k < kDims; ++k) batch_sums[(bi * kDims + k) * 64 + lane] = num[k];
+      for (int k = 0; k < NDIM; ++k) batch_sums[(bi * NDIM + k) * 64 + lane] = num[k];
     }
   }
   if (W > 1) {  // workgroup-uniform
@@ -1449,12 +1502,12 @@ merge_partials_kernel(const float *__restrict__ partial_max, const float *__rest
     if (wave != 0) return;
     for (int32_t bi = 0; bi < batches; ++bi)
 #pragma unroll
-      for (int k = 0; k < kDims; ++k) total[k] += batch_sums[(bi * kDims + k) * 64 + lane];
+      for (int k = 0; k < NDIM; ++k) total[k] += batch_sums[(bi * NDIM + k) * 64 + lane];
   }
 #pragma unroll
-  for (int k = 0; k < kDims; ++k) {
+  for (int k = 0; k < NDIM; ++k) {
     const int d = lane + 64 * k;
-    if (k < ndim && d < head_dim) out[d] = from_float<T>(total[k]);
+    if (d < head_dim) out[d] = from_float<T>(total[k]);
   }
 }
 
@@ -1702,32 +1755,33 @@ int32_t launch_merge(const float *partial_max, const float *partial_sum, const f
   if (batch == 0) return TF_SUCCESS;
   const dim3 grid(static_cast<unsigned>(query_heads), static_cast<unsigned>(batch));
   // Up to four wavefronts per (row, head) when a row may have more than one
-  // 16-split batch, so the batches' loads are in flight together (cfg3's
-  // 64 partitions of 512 tokens: 14.2 -> a few us); their batch sums meet
-  // in LDS (4 KB per batch), so beyond 16 batches one wavefront walks them.
+  // 16-split batch, so the batches' loads are in flight together; their
+  // batch sums meet in LDS (1 KB per batch and 64 dims), so beyond 16
+  // batches one wavefront walks them.
   const int32_t batches = (num_splits + 15) / 16;
   const int waves = batches <= 1 || batches > 16 ? 1 : (batches < 4 ? batches : 4);
   const dim3 block(64u * static_cast<unsigned>(waves));
-  const size_t lds = waves > 1 ? static_cast<size_t>(batches) * 4 * 64 * sizeof(float) : 0;
+  const int ndim = (head_dim + 63) / 64;  // accumulator elements per lane
+  if (ndim < 1 || ndim > 4) return fail(TF_ERROR_INVALID_ARGUMENT, "merge: head_dim must be in [1, 256]");
+  const size_t lds = waves > 1 ? static_cast<size_t>(batches) * ndim * 64 * sizeof(float) : 0;
+  auto launch = [&](auto kernel, auto *out) {
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream, partial_max, partial_sum, partial_acc,
+                       context_lengths, out, query_heads, head_dim, split_size, num_splits,
+                       partial_stride, max_tokens, bal);
+  };
+  auto by_width = [&](auto *out) {
+    using T = std::remove_pointer_t<decltype(out)>;
+    switch (ndim) {
+      case 1: launch(merge_partials_kernel<T, 1>, out); break;
+      case 2: launch(merge_partials_kernel<T, 2>, out); break;
+      case 3: launch(merge_partials_kernel<T, 3>, out); break;
+      default: launch(merge_partials_kernel<T, 4>, out); break;
+    }
+  };
   switch (dtype) {
-    case TF_DTYPE_FLOAT32:
-      hipLaunchKernelGGL(merge_partials_kernel<float>, grid, block, lds, stream, partial_max,
-                         partial_sum, partial_acc, context_lengths, static_cast<float *>(output),
-                         query_heads, head_dim, split_size, num_splits, partial_stride, max_tokens,
-                         bal);
-      break;
-    case TF_DTYPE_FLOAT16:
-      hipLaunchKernelGGL(merge_partials_kernel<_Float16>, grid, block, lds, stream, partial_max,
-                         partial_sum, partial_acc, context_lengths,
-                         static_cast<_Float16 *>(output), query_heads, head_dim, split_size,
-                         num_splits, partial_stride, max_tokens, bal);
-      break;
-    default:
-      hipLaunchKernelGGL(merge_partials_kernel<__bf16>, grid, block, lds, stream, partial_max,
-                         partial_sum, partial_acc, context_lengths, static_cast<__bf16 *>(output),
-                         query_heads, head_dim, split_size, num_splits, partial_stride, max_tokens,
-                         bal);
-      break;
+    case TF_DTYPE_FLOAT32: by_width(static_cast<float *>(output)); break;
+    case TF_DTYPE_FLOAT16: by_width(static_cast<_Float16 *>(output)); break;
+    default: by_width(static_cast<__bf16 *>(output)); break;
   }
   return check_launch("paged_gqa_decode merge");
 }
