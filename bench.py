@@ -478,7 +478,8 @@ def main() -> int:
         path = "split_kv"
     else:
         path = "auto"
-    plan = attention_plan(max_context, batch, kv_heads, table_width * block_size, path)
+    plan = attention_plan(max_context, batch, kv_heads, table_width * block_size, path,
+                          head_dim=head_dim)
     split_size, num_splits, flags = plan.split_size, plan.num_splits, plan.flags
     one_pass = plan.one_pass
     workspace = PagedAttentionWorkspace.allocate(

@@ -288,8 +288,11 @@ class DecodeGraphBucket:
             raise ValueError("token_state must be an int64 tensor of at least batch_capacity")
         self.token_state = token_state
         hq, hkv, d = config.num_attention_heads, config.num_key_value_heads, config.head_dim
+        # Partials for one partition per 128 tokens of the context (twice the
+        # reference's sizing), so narrow buckets can take the 128-token
+        # partitions of the attention plan.
         self.workspace = PagedAttentionWorkspace.allocate(
-            batch_capacity=b, query_heads=hq, head_dim=d, max_context_length=context_capacity,
+            batch_capacity=b, query_heads=hq, head_dim=d, max_context_length=2 * context_capacity,
             device=device)
         self.query = torch.empty((b, hq, d), dtype=dtype, device=device)
         self.attention_output = torch.empty((b, hq, d), dtype=dtype, device=device)

@@ -144,15 +144,35 @@ ONE_PASS_MIN_WORKGROUPS = 192
 # on MI355X at config 2, three seeds: 576 with up to 4 wavefronts per 2k row
 # beats 448 / 512 / 640 and the 768 / 3 of the operand-layout loads).
 ONE_PASS_TOKENS_PER_WAVE = 576
-# Narrow calls (fewer workgroups than ONE_PASS_MIN_WORKGROUPS) are latency-
-# bound: one pass with up to 8 wavefronts per kv head, a row using one per
-# 64 of its tokens, when the context is short (<= 1024 tokens, or <= 2048
-# with >= 128 workgroups); otherwise split-KV with up to 4 wavefronts per
-# (row, kv head, split) -- see attention_plan for the measurements.
-NARROW_ONE_PASS_CONTEXT = 1024
-NARROW_ONE_PASS_MIN_WORKGROUPS = 128
-NARROW_WAVES = 8
-NARROW_SPLIT_WAVES = 4
+# Narrow calls (fewer workgroups than ONE_PASS_MIN_WORKGROUPS).  Measured on
+# MI355X with the K/V read from HBM (one 1 GB page pool, tables rotated over
+# disjoint pages; TinyLlama 32/4 heads at D 64 and Llama-3 32/8 at D 128,
+# 1-47 rows of 64-32768 tokens), graph-timed through the C ABI:
+# * split-KV (narrow_split_plan) wins once a (row, kv head) holds >=
+#   NARROW_SPLIT_MIN_BYTES of K and V (NARROW_SPLIT_MIN_BYTES_WIDE above
+#   NARROW_SPLIT_WIDE_GRID one-pass workgroups), in partitions of equal size
+#   that put about one workgroup on each compute unit, two wavefronts each,
+#   kv heads paired in a workgroup (256-byte slices of each token row) where
+#   one head's slice is narrower.  1 x 1000 at D 64: 7.7 us against 10.4 for
+#   one pass with eight wavefronts of 64 tokens; 8 x 1000 8.6 against 11.3;
+#   32 x 2048 15.3 against 19.7; 32 x 3000 20.0 (four partitions of pairs)
+#   against 22.7 for two partitions of one kv head and 27.6 for one pass;
+#   47 x 3000 23.9 (three of pairs) against 28.3; 4 x 1000 at D 128 10.7
+#   against 19.0; 1 x 32k at D 128 29.1 against 38.5 for 2048-token
+#   partitions of four wavefronts.  Below the byte floor one pass is as
+#   fast or faster (1 x 256 at D 64: 5.3 against 7.2 us with two partitions;
+#   32 x 800: 9.6 against 10.2);
+# * otherwise one pass with up to NARROW_WAVES wavefronts per kv head, a row
+#   using one per max(64, head_dim, ceil64(context / 4)) of its tokens (1-47
+#   rows x 64 / 200 / 512 tokens at D 64: 3.7-3.9 / 5.1-5.7 / 6.9-7.5 us,
+#   against 4.5-4.8 / 5.3-6.0 / 7.6-8.4 with eight wavefronts of 64 tokens).
+NARROW_WAVES = 4
+NARROW_SPLIT_WAVES = 2
+NARROW_SPLIT_WAVES_SMALL_GRID = 4  # partitions of >= 256 tokens on <= 128 workgroups
+NARROW_SPLIT_MIN_SIZE = 128
+NARROW_SPLIT_MIN_BYTES = 192 * 1024
+NARROW_SPLIT_MIN_BYTES_WIDE = 256 * 1024
+NARROW_SPLIT_WIDE_GRID = 64
 NARROW_TOKENS_PER_WAVE = 64
 # Narrow split-KV calls of at least this context and 2..64 rows size their
 # partitions on the device from the rows' lengths (balanced_geometry); the
@@ -234,20 +254,52 @@ def wide_tokens_per_wave(max_context_length: int) -> int:
     return max(128, (-(-max_context_length // 4) + 63) // 64 * 64)
 
 
-def narrow_split_size_for(max_context_length: int, batch: int, kv_heads: int) -> int:
-    """Partition size of a narrow split-KV call with several wavefronts per
-    split: the smallest size >= 256 that keeps the grid near 256 (row, kv
-    head, split) workgroups, and at most 16 splits per row --
-    ``max(256, ceil64(L * B * Hkv / 256), ceil64(L / 16))``."""
+def narrow_one_pass_tokens(max_context_length: int, head_dim: int) -> int:
+    """Token budget per wavefront of a narrow one-pass call: a row gets up to
+    NARROW_WAVES wavefronts of max(64, head_dim, ceil64(context / 4))
+    tokens."""
 
-    def ceil64(value: int) -> int:
-        return (value + 63) // 64 * 64
+    quarter = (-(-max_context_length // NARROW_WAVES) + 63) // 64 * 64
+    return max(NARROW_TOKENS_PER_WAVE, head_dim, quarter)
 
-    return max(
-        REFERENCE_SPLIT_SIZE,
-        ceil64(max_context_length * max(batch, 1) * kv_heads // 256),
-        ceil64((max_context_length + 15) // 16),
-    )
+
+def narrow_split_plan(max_context_length: int, batch: int, kv_heads: int, head_dim: int,
+                      element_bytes: int, slot_limit: int | None = None) -> AttentionPlan | None:
+    """Split-KV launch of a narrow call, or None where one pass is faster.
+
+    With R = rows x kv heads one-pass workgroups, the partitions aim at
+    about COMPUTE_UNITS workgroups: round(COMPUTE_UNITS x pair / R) per row,
+    where pair = 2 when kv heads can pair up (an even count whose slice of a
+    token row is narrower than 256 bytes) and a workgroup then serves two kv
+    heads of its partition once the unpaired grid would exceed the compute
+    units.  Partitions are of equal size (a multiple of 32 tokens, at least
+    NARROW_SPLIT_MIN_SIZE), as many per row as the workspace's partials per
+    (row, query head) allow (``slot_limit``).  Two wavefronts per partition,
+    four for partitions of >= 256 tokens on at most 128 workgroups.  One
+    pass instead when a (row, kv head) holds less than NARROW_SPLIT_MIN_BYTES
+    of K and V (NARROW_SPLIT_MIN_BYTES_WIDE above 64 one-pass workgroups), or
+    when a row would not take two partitions."""
+
+    rows_heads = max(batch, 1) * kv_heads
+    row_bytes = 2 * max_context_length * head_dim * element_bytes
+    floor_bytes = (NARROW_SPLIT_MIN_BYTES if rows_heads <= NARROW_SPLIT_WIDE_GRID
+                   else NARROW_SPLIT_MIN_BYTES_WIDE)
+    if row_bytes < floor_bytes:
+        return None
+    pair = 2 if kv_heads % 2 == 0 and head_dim * element_bytes < 256 else 1
+    target = max(1, round(COMPUTE_UNITS * pair / rows_heads))
+    if slot_limit is not None:
+        target = min(target, slot_limit)
+    size = max(NARROW_SPLIT_MIN_SIZE, (-(-max_context_length // max(target, 1)) + 31) // 32 * 32)
+    splits = -(-max_context_length // size)
+    if splits < 2:
+        return None
+    units = rows_heads * splits
+    heads = pair if units > COMPUTE_UNITS else 1
+    waves = (NARROW_SPLIT_WAVES_SMALL_GRID if units <= COMPUTE_UNITS // 2 and size >= 256
+             else NARROW_SPLIT_WAVES)
+    return AttentionPlan(False, size, splits, waves, NARROW_TOKENS_PER_WAVE,
+                         heads_per_wg=heads)
 
 
 def balanced_geometry(max_context_length: int, batch: int, kv_heads: int,
@@ -291,7 +343,8 @@ def balanced_slots_for(max_context_length: int, batch: int, kv_heads: int) -> in
 
 
 def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capacity: int,
-                   attention_path: str = "auto", slot_limit: int | None = None) -> AttentionPlan:
+                   attention_path: str = "auto", slot_limit: int | None = None, *,
+                   head_dim: int = 64, element_bytes: int = 2) -> AttentionPlan:
     """The launch of a call from host-known sizes only.
 
     The reference runs one pass unless the batch has few programs
@@ -304,22 +357,21 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
       wavefronts (one per wide_tokens_per_wave tokens of the row) that
       combine in LDS -- no partials, no merge launch (72 rows x 4 kv heads
       x 2k: 21.3 us against 26.0 us for split 576 plus merge);
-    * fewer workgroups, context <= 1024 (or <= 2048 with >= 128 workgroups):
-      one pass with up to 8 wavefronts per kv head, one per 64 tokens of a
-      row (1-16 rows x 1k: 9.8-10.1 us against 12.5-12.9 for 256-token
-      splits with one wavefront each; 32 x 2k: 17.9 against 20.9);
-    * otherwise split-KV with up to 4 wavefronts per split and the partition
-      size of narrow_split_size_for (1 x 4k: 11.9 against 13.5 us; 8 x 4k:
-      14.2 against 15.5; config 3, 4 x 8-32k x 8 kv heads at D 128: 74.7
-      against 78.4), or for 2..64 rows of >= 8k the balanced partitions of
+    * fewer workgroups: for 2..64 rows of >= 8k the balanced partitions of
       balanced_geometry, sized on the device from the rows' lengths, with
       up to four kv heads per workgroup and two wavefronts per kv head
-      (config 3: 61.8 us with four kv heads per workgroup, 64.5 with one,
-      against 70.8-71.9 us for fixed 4096-token partitions);
+      (config 3: 58.7 us, against 70.8 for fixed 4096-token partitions);
+      otherwise split-KV by narrow_split_plan where a row's K and V are
+      large enough to pay for the merge launch, else one pass with up to
+      four wavefronts per kv head (narrow_one_pass_tokens);
     * a partition size fixed by the caller (set_attention_split_size) or
       ``attention_path="split_kv"``: split-KV (size attention_split_size_for
       unless fixed) with two wavefronts per partition, four above 768
       tokens; ``"one_pass"`` forces one pass.
+
+    ``slot_limit`` is the number of partials per (row, query head) the
+    workspace holds (None: no limit beyond the plan's own); ``head_dim`` and
+    ``element_bytes`` size a token row's slice per kv head.
     """
 
     fixed = _SPLIT_SIZE is not None
@@ -339,17 +391,19 @@ def attention_plan(launch_context: int, batch: int, kv_heads: int, context_capac
         tokens = wide_tokens_per_wave(launch_context)
         waves = max(1, min(8, -(-launch_context // tokens)))
         return AttentionPlan(True, capacity32, 1, waves, tokens)
-    if (attention_path == "one_pass" or launch_context <= NARROW_ONE_PASS_CONTEXT
-            or (workgroups >= NARROW_ONE_PASS_MIN_WORKGROUPS and launch_context <= 2048)):
-        return AttentionPlan(True, capacity32, 1, NARROW_WAVES, NARROW_TOKENS_PER_WAVE)
+    narrow_tokens = narrow_one_pass_tokens(launch_context, head_dim)
+    one_pass = AttentionPlan(True, capacity32, 1,
+                             max(1, min(NARROW_WAVES, -(-launch_context // narrow_tokens))),
+                             narrow_tokens)
+    if attention_path == "one_pass":
+        return one_pass
     slots, heads = balanced_geometry(launch_context, batch, kv_heads, slot_limit)
     if slots:
         smallest = (-(-launch_context // slots) + 63) // 64 * 64
         return AttentionPlan(False, smallest, slots, BALANCED_WAVES, NARROW_TOKENS_PER_WAVE,
                              balanced=True, heads_per_wg=heads)
-    narrow = narrow_split_size_for(launch_context, batch, kv_heads)
-    return AttentionPlan(False, narrow, (launch_context + narrow - 1) // narrow,
-                         NARROW_SPLIT_WAVES, NARROW_TOKENS_PER_WAVE)
+    split = narrow_split_plan(launch_context, batch, kv_heads, head_dim, element_bytes, slot_limit)
+    return split if split is not None else one_pass
 
 
 def paged_gqa_decode_attention(
@@ -441,7 +495,7 @@ def paged_gqa_decode_attention(
     else:
         slot_limit = COMPUTE_UNITS * BALANCED_MAX_HEADS_PER_WG
     plan = attention_plan(launch_context, batch, kv_heads, context_capacity, attention_path,
-                          slot_limit)
+                          slot_limit, head_dim=head_dim, element_bytes=query.element_size())
     use_split_kv = not plan.one_pass
     split_size = plan.split_size
     dtype = _native.dtype_code(query.dtype)
@@ -658,7 +712,8 @@ def paged_gqa_decode_attention_rope_append(
     capacity = min(workspace.partial_max.numel(), workspace.partial_sum.numel(),
                    workspace.partial_accumulator.shape[0])
     plan = attention_plan(max_context_length, batch, kv_heads, context_capacity,
-                          slot_limit=capacity // max(batch * query_heads, 1))
+                          slot_limit=capacity // max(batch * query_heads, 1), head_dim=head_dim,
+                          element_bytes=qkv.element_size())
     head_bucket = _next_power_of_2(head_dim)
     partial_programs = batch * query_heads * plan.num_splits
     if not plan.one_pass and (capacity < partial_programs

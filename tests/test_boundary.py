@@ -310,40 +310,57 @@ def test_automatic_split_size() -> None:
 
 def test_attention_plan() -> None:
     """One pass for wide batches (cfg2: 72 rows x 4 kv heads at 2k, four
-    wavefronts per kv head, one per 576 tokens); for narrow calls one pass
-    with up to 8 wavefronts (one per 64 tokens) at short contexts and
-    split-KV with up to 4 wavefronts per split at long ones (the reference's
-    own 1 x 8 case keeps its 256-token partitions), with balanced
-    partitions -- up to four kv heads per workgroup, one slot per compute
-    unit and group of kv heads, the size set on the device -- for 2..64
-    rows of >= 8k when the slots fit one per 256 tokens (cfg3: four kv
-    heads per workgroup, 128 slots of >= 256 tokens); two wavefronts per
+    wavefronts per kv head, one per 576 tokens); for narrow calls split-KV
+    in partitions of the smallest power of two >= 128 tokens that keeps the
+    grid within the compute units (twice that with two kv heads per
+    workgroup at D 64) and the workspace's partials, where a row's K and V
+    pay for the merge (the reference's own 1 x 8 case with its workspace
+    keeps its 256-token partitions), else one pass with up to 4 wavefronts;
+    balanced partitions -- up to four kv heads per workgroup, one slot per
+    compute unit and group of kv heads, the size set on the device -- for
+    2..64 rows of >= 8k when the slots fit one per 256 tokens (cfg3: four
+    kv heads per workgroup, 128 slots of >= 256 tokens); two wavefronts per
     split when the caller fixes the partition size or forces split-KV (four
     above 768 tokens), with two kv heads per workgroup for 512-768 tokens."""
 
     from tensorforge_amd.kernels.attention import (
         balanced_geometry,
         balanced_slots_for,
-        narrow_split_size_for,
+        narrow_split_plan,
     )
 
     cfg2 = attention_plan(2048, 72, 4, 2048)
     assert (cfg2.one_pass, cfg2.num_splits, cfg2.waves_per_head) == (True, 1, 4)
     assert cfg2.flags == (9 << 24) | (1 << 20) | (4 << 8)
-    short = attention_plan(200, 2, 4, 2048)
-    assert short.one_pass and short.waves_per_head == 8
-    assert short.flags == (1 << 24) | (1 << 20) | (8 << 8)
+    short = attention_plan(200, 2, 4, 2048)  # 51 KB of K and V per (row, kv head): one pass
+    assert short.one_pass and short.waves_per_head == 4 and short.tokens_per_wave == 64
+    assert short.flags == (1 << 24) | (1 << 20) | (4 << 8)
     assert short.split_size == 2048  # the whole table in one partition
-    assert attention_plan(1000, 16, 4, 1024).one_pass
+    d128 = attention_plan(256, 4, 8, 256, head_dim=128)  # two wavefronts of 128 tokens
+    assert d128.one_pass and (d128.waves_per_head, d128.tokens_per_wave) == (2, 128)
+    mid16 = attention_plan(1000, 16, 4, 1024)
+    assert (mid16.one_pass, mid16.split_size, mid16.num_splits) == (False, 128, 8)
+    assert (mid16.heads_per_wg, mid16.waves_per_head) == (2, 2)  # 512 partitions in pairs
     few = attention_plan(2048, 1, 4, 2048)
-    assert (few.one_pass, few.split_size, few.num_splits, few.waves_per_head) == (False, 256, 8, 4)
-    assert few.flags == (1 << 24) | (1 << 20) | (4 << 8)
+    assert (few.one_pass, few.split_size, few.num_splits, few.waves_per_head) == (False, 128, 16, 2)
+    assert few.flags == (1 << 24) | (1 << 20) | (2 << 8)
+    # The reference's 1 x 8 case with its workspace (8 partials per row and head).
+    ref = attention_plan(2048, 1, 4, 2048, slot_limit=8)
+    assert (ref.one_pass, ref.split_size, ref.num_splits, ref.waves_per_head) == (False, 256, 8, 4)
     assert attention_plan(2048, 48, 4, 2048).one_pass  # 192 workgroups: wide
-    narrow32 = attention_plan(2048, 32, 4, 2048)        # 128 workgroups, <= 2k
-    assert narrow32.one_pass and narrow32.waves_per_head == 8
-    assert not attention_plan(2100, 32, 4, 2112).one_pass
+    narrow32 = attention_plan(2048, 32, 4, 2048)        # 128 workgroups
+    assert (narrow32.split_size, narrow32.num_splits, narrow32.heads_per_wg) == (512, 4, 2)
+    # Partitions of equal size, about one workgroup per compute unit.
+    even = attention_plan(2100, 32, 4, 2112)
+    assert (even.split_size, even.num_splits, even.heads_per_wg) == (544, 4, 2)
+    assert attention_plan(1000, 32, 4, 1024).one_pass  # 250 KB per (row, kv head), 128 of them
+    forty = attention_plan(3000, 40, 4, 3008)  # round(512 / 160) = 3 partitions of pairs
+    assert (forty.split_size, forty.num_splits, forty.heads_per_wg) == (1024, 3, 2)
+    assert attention_plan(4096, 23, 8, 4096, head_dim=128).one_pass  # 184 workgroups
     long8 = attention_plan(4000, 8, 4, 4096)
-    assert (long8.one_pass, long8.split_size, long8.num_splits) == (False, 512, 8)
+    assert (long8.one_pass, long8.split_size, long8.num_splits) == (False, 256, 16)
+    d128_8 = attention_plan(1000, 8, 8, 1024, head_dim=128)  # 256-byte slices: no pairs
+    assert (d128_8.split_size, d128_8.num_splits, d128_8.heads_per_wg) == (256, 4, 1)
     cfg3 = attention_plan(32768, 4, 8, 32768)
     assert (cfg3.one_pass, cfg3.split_size, cfg3.num_splits, cfg3.balanced) == (False, 256, 128,
                                                                                 True)
@@ -362,8 +379,13 @@ def test_attention_plan() -> None:
     assert balanced_slots_for(16384, 64, 4) == 0     # slots must outnumber rows
     assert balanced_slots_for(65536, 65, 1) == 0     # at most 64 rows
     assert not attention_plan(8192, 8, 4, 8192).balanced
-    assert narrow_split_size_for(32768, 1, 4) == 2048  # at most 16 splits per row
-    assert narrow_split_size_for(4000, 1, 4) == 256
+    one_row = narrow_split_plan(32768, 1, 4, 64, 2)
+    assert (one_row.split_size, one_row.num_splits, one_row.heads_per_wg) == (256, 128, 2)
+    assert narrow_split_plan(32768, 1, 4, 64, 2, slot_limit=64).split_size == 512
+    assert narrow_split_plan(4000, 1, 4, 64, 2).split_size == 128
+    assert narrow_split_plan(4000, 1, 4, 64, 2, slot_limit=0) is None
+    assert narrow_split_plan(512, 4, 4, 64, 2) is None  # 128 KB per (row, kv head)
+    assert narrow_split_plan(512, 4, 8, 128, 2) is not None  # 256 KB
     assert attention_plan(4096, 64, 4, 4096).waves_per_head == 8
     mid = attention_plan(1024, 64, 4, 1024)  # ~4 wavefronts per row below 1.5k
     assert (mid.waves_per_head, mid.tokens_per_wave) == (4, 256)
