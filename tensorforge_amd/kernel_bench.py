@@ -592,8 +592,9 @@ def projections(device: torch.device, calls: int) -> list[dict]:
             dtype=torch.bfloat16, seed=batch + context)
         gpu = case.to(device)
         width = gpu.block_tables.shape[1]
+        # Partials for one partition per 128 tokens, as the decode executor sizes them.
         workspace = PagedAttentionWorkspace.allocate(
-            batch_capacity=batch, query_heads=32, head_dim=64, max_context_length=width * 16,
+            batch_capacity=batch, query_heads=32, head_dim=64, max_context_length=2 * width * 16,
             device=device)
         output = torch.empty_like(gpu.query)
 
@@ -605,14 +606,17 @@ def projections(device: torch.device, calls: int) -> list[dict]:
 
         planned = graph_time_us(run, calls, device)
         record = selected_attention_autotune_config()
+        launch = selected_attention_launch()
         previous = set_attention_split_size(256)
         try:
-            one_wave = graph_time_us(run, calls, device)
+            fixed = graph_time_us(run, calls, device)
         finally:
             set_attention_split_size(previous)
         results.append({"case": f"attention {batch} rows x {context} (TinyLlama geometry)",
                         "plan_us": round(planned, 2), "plan": record,
-                        "one_wavefront_per_256_partition_us": round(one_wave, 2)})
+                        "waves_per_head": launch["waves_per_head"],
+                        "heads_per_workgroup": launch["heads_per_workgroup"],
+                        "fixed_256_partitions_us": round(fixed, 2)})
     return results
 
 
