@@ -662,11 +662,11 @@ paged_decode_mfma_kernel(AttnParams p) {
   uint32_t win_lo = 0;  // the current segment's window_offsets
   int32_t win_hi = -1;
 
-  // Independent start-up loads: row length, query group, first page window
-  // (the window first when the query group is rotated, whose arithmetic
-  // waits for its loads).
-  const int32_t ctx = clamp_context(p, b);
-  int32_t page_win = ROPE ? load_window(0) : 0;
+  // Independent start-up loads, all issued before anything waits for one:
+  // the first page window, the query group, then the row length (below;
+  // with RoPE the length is read together with the row's position).
+  int32_t page_win = load_window(0);
+  int32_t length = 0;
   vec8 qf[KS];  // B operand of the score MFMA: q[head l16][32ks + 8q4 .. +8]
   constexpr int kHalf = D / 2;
   // RoPE inputs of this row: the QKV row and the cos / sin rows of its position.
@@ -675,7 +675,11 @@ paged_decode_mfma_kernel(AttnParams p) {
   const T *rope_sn = nullptr;
   if constexpr (ROPE) {
     rope_row = static_cast<const T *>(p.rope_qkv) + static_cast<int64_t>(b) * p.rope_row_stride;
+    length = p.context_lengths[b];
     int64_t pos = p.rope_positions[b];
+    // Both reads issued before either is waited for (the empty-row test on
+    // the length would otherwise be placed between them).
+    __asm__ volatile("" ::: "memory");
     pos = pos < 0 ? 0 : (pos >= p.rope_table_rows ? p.rope_table_rows - 1 : pos);
     rope_cs = static_cast<const T *>(p.rope_cos) + pos * D;
     rope_sn = static_cast<const T *>(p.rope_sin) + pos * D;
@@ -698,12 +702,16 @@ paged_decode_mfma_kernel(AttnParams p) {
     return out;
   };
   {
-    const int64_t head = static_cast<int64_t>(kvh) * p.group + l16;
+    // Lanes past the group (l16 >= group) take the group's last head: their
+    // score and output columns are never stored, and their maxima follow
+    // that head's, so the wavefront's rescale decisions and every stored
+    // bit are unchanged.  Loads with no branch around them leave the
+    // compiler no reason to wait for them here (a branch's phi copy did, and
+    // with it the window and row-length loads behind them lost a round trip).
+    const int64_t head = static_cast<int64_t>(kvh) * p.group + min(l16, p.group - 1);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      if (l16 >= p.group) {
-        qf[ks] = vec8{};
-      } else if constexpr (ROPE) {
+      if constexpr (ROPE) {
         qf[ks] = rotate8(rope_row + head * D, 32 * ks + 8 * q4);
       } else {
         const T *qrow = static_cast<const T *>(p.query) +
@@ -712,7 +720,14 @@ paged_decode_mfma_kernel(AttnParams p) {
       }
     }
   }
-  if constexpr (!ROPE) page_win = load_window(0);
+  // The row length is read after the loads above are issued: its test (an
+  // empty partition returns) would otherwise be placed first, holding the
+  // query loads behind the length's round trip.
+  if constexpr (!ROPE) {
+    __asm__ volatile("" ::: "memory");
+    length = p.context_lengths[b];
+  }
+  const int32_t ctx = length < 0 ? 0 : (length > p.max_tokens ? p.max_tokens : length);
   // VALU form (head_dim 64, group <= 8): lane (t16, qd) holds dims
   // [16 qd, 16 qd + 16) of every query head of the group (zeros past it).
   constexpr int kValuHeads = 8;
