@@ -557,6 +557,269 @@ linear_kstream_kernel(const T *__restrict__ x, int64_t x_stride, const T *__rest
   }
 }
 
+// Activation-resident form of the K-split kernel (the SwiGLU + RMSNorm
+// launch at 49-64 rows with K = 2048; launch_kstream_mt picks it): each
+// wavefront copies its K quarter of the workgroup's 16 MT rows of x into
+// LDS once, then streams only weights over the column tiles blockIdx.x,
+// blockIdx.x + groups, ... (INFL chunks of 64 k in flight), so a workgroup
+// reads x once instead of once per 64-k chunk of every tile.  Per lane and
+// k-step the MFMA operands, the order of the k-steps, the sums of squares
+// and the epilogue are those of linear_kstream_kernel, so both forms give
+// the same bits.  The outputs of a workgroup's tiles wait in LDS and are
+// stored after the stream (a store inside it would leave the loads' wait
+// counts unknown at the loop head).
+template <typename T, int MT, int NT, bool SWIGLU, int EPI, int INFL, int KQ, int MAXT>
+__global__ void __launch_bounds__(256)
+linear_xres_kernel(const T *__restrict__ x, int64_t x_stride, const T *__restrict__ w,
+                   int64_t w_stride, T *__restrict__ y, int64_t y_stride, int32_t m, int32_t n,
+                   int32_t k, int32_t groups, KstreamExtra<T> extra) {
+  using M = SplitMma<T>;
+  using vec8 = typename M::vec8;
+  constexpr int KC = 64;
+  constexpr int XR = 16 * MT;
+  constexpr int CW = 16 * NT;
+  constexpr int kSteps = KC / 32;
+  constexpr int kItems = MT * 4 * 64;
+  constexpr int kTiles = SWIGLU ? 2 : 1;
+  const int32_t r0 = static_cast<int32_t>(blockIdx.y) * XR;
+  x += static_cast<int64_t>(r0) * x_stride;
+  y += static_cast<int64_t>(r0) * y_stride;
+  if constexpr (EPI == kEpiResidual) extra.residual += static_cast<int64_t>(r0) * extra.residual_stride;
+  m = min(m - r0, XR);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l16 = lane & 15;
+  const int q4 = lane >> 4;
+  constexpr int32_t kq = KQ;          // K quarter (the host checks k == 4 KQ)
+  constexpr int32_t xs = kq + 8;      // padded LDS row: rows 16 B apart in the banks
+  constexpr int32_t nch = kq / KC;    // chunks per tile per wavefront
+  static_assert(nch % INFL == 0, "a group of INFL chunks lies in one tile");
+  constexpr int XL = XR * kq / 512;   // x loads per lane
+  const int32_t k0 = wave * kq;
+  const int32_t ntiles = (n + CW - 1) / CW;
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char xres_smem[];
+  // LDS: x quarters [4][XR][xs] | weight staging [4][WR][KC] (its space
+  // holds the tile sums [4][kTiles][NT][kItems] in the epilogue) | row sums
+  // of squares [4][XR] | rounded outputs [MAXT][XR][CW].
+  constexpr int kStageBytes = 4 * (SWIGLU ? 2 * CW : CW) * KC * static_cast<int>(sizeof(T));
+  constexpr int kTileBytes = 4 * kTiles * NT * kItems * 4;
+  constexpr int kRegion = kStageBytes > kTileBytes ? kStageBytes : kTileBytes;
+  T *xq = reinterpret_cast<T *>(xres_smem) + wave * XR * xs;
+  unsigned char *region = xres_smem + 4 * XR * xs * sizeof(T);
+  T *wl = reinterpret_cast<T *>(region) + wave * (SWIGLU ? 2 * CW : CW) * KC;
+  float *tiles = reinterpret_cast<float *>(region);
+  float *ssq_rows = reinterpret_cast<float *>(region + kRegion);
+  T *outs = reinterpret_cast<T *>(ssq_rows + 4 * XR);
+
+  // Weight loads of stream position i (clamped to the last): tile
+  // blockIdx.x + (i / nch) groups, chunk i % nch; lane (l16, q4) of group g,
+  // k-step s holds w[row][kk + 32 s + 8 q4 .. +8].
+  // Weight chunks are loaded as whole 128-byte row pieces (8 lanes per row,
+  // 8 rows per load) and staged in a per-wavefront LDS region before the
+  // MFMA operand reads, as linear_kstream_kernel stages them.  The host
+  // checks nch % INFL == 0, so a group of INFL positions lies in one tile:
+  // load_w(p, s) loads position p + s of such a group (p past the stream
+  // reloads its last group).
+  constexpr int WR = SWIGLU ? 2 * CW : CW;
+  constexpr int kLanesPerRow = KC / 8;
+  constexpr int kRowsPerLoad = 64 / kLanesPerRow;
+  constexpr int kLoadsW = WR / kRowsPerLoad;
+  const int lrow = lane / kLanesPerRow;
+  const int lpiece = lane % kLanesPerRow;
+  // Row pointers of the tile being loaded: tile index lt (clamped to the
+  // last one, whose chunks are reloaded past the stream), chunk lc.
+  const int32_t my_tiles = (ntiles - static_cast<int32_t>(blockIdx.x) + groups - 1) / groups;
+  const T *wsrc[kLoadsW];
+  auto point_w = [&](int32_t lt) {
+    const int32_t n0 = (static_cast<int32_t>(blockIdx.x) + min(lt, my_tiles - 1) * groups) * CW;
+#pragma unroll
+    for (int i = 0; i < kLoadsW; ++i) {
+      const int tr = kRowsPerLoad * i + lrow;  // tile row: gate rows [0, CW), then up rows
+      const int64_t row = SWIGLU ? (tr < CW ? 0 : n) + min(n0 + (tr % CW), n - 1) : min(n0 + tr, n - 1);
+      wsrc[i] = w + row * w_stride + k0 + 8 * lpiece;
+    }
+  };
+  int32_t lt = 0, lc = 0;
+  point_w(0);
+  // Chunk lc + s of the tile being loaded; past the stream the last tile's
+  // last group again.
+  auto load_w = [&](int s, vec8(&r)[kLoadsW]) {
+    const int32_t c = (lt < my_tiles ? lc : nch - INFL) + s;
+#pragma unroll
+    for (int i = 0; i < kLoadsW; ++i) r[i] = *reinterpret_cast<const vec8 *>(wsrc[i] + c * KC);
+  };
+  auto next_group = [&]() {
+    lc += INFL;
+    if (lc == nch) {
+      lc = 0;
+      ++lt;
+      point_w(lt);
+    }
+  };
+
+  // x quarter: XR rows x kq (XL loads per lane, lane: 8 consecutive
+  // elements); rows past m read row m - 1.  All of them go out before the
+  // weight prefetch and are written while it is in flight.
+  vec8 wr[INFL][kLoadsW];
+  {
+    vec8 xb[XL];
+#pragma unroll
+    for (int j = 0; j < XL; ++j) {
+      constexpr int kPerRow = kq / 8;  // lanes' pieces per row
+      const int row = (64 * j + lane) / kPerRow;
+      const int col = 8 * ((64 * j + lane) % kPerRow);
+      xb[j] = *reinterpret_cast<const vec8 *>(x + static_cast<int64_t>(min(row, m - 1)) * x_stride + k0 + col);
+    }
+#pragma unroll
+    for (int s = 0; s < INFL; ++s) load_w(s, wr[s]);
+    next_group();
+    __asm__ volatile("" ::: "memory");  // every load above is issued before the first store
+#pragma unroll
+    for (int j = 0; j < XL; ++j) {
+      constexpr int kPerRow = kq / 8;
+      const int row = (64 * j + lane) / kPerRow;
+      const int col = 8 * ((64 * j + lane) % kPerRow);
+      *reinterpret_cast<vec8 *>(xq + row * xs + col) = xb[j];
+    }
+  }
+  __asm__ volatile("" ::: "memory");  // this wavefront's x stores precede its operand reads
+
+  f32x4 acc[MT][NT], accu[SWIGLU ? MT : 1][NT];
+  float ssq[EPI == kEpiNorm ? MT : 1];
+#pragma unroll
+  for (int i = 0; i < (EPI == kEpiNorm ? MT : 1); ++i) ssq[i] = 0.f;
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int ct = 0; ct < NT; ++ct) {
+        acc[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (SWIGLU) accu[mt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+  };
+  zero_acc();
+  auto compute = [&](int32_t c, const vec8(&r)[kLoadsW], bool first) {
+    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < kLoadsW; ++i)
+      *reinterpret_cast<vec8 *>(wl + kstream_lds_offset<KC>(kRowsPerLoad * i + lrow, lpiece)) = r[i];
+    __asm__ volatile("" ::: "memory");
+    const T *xa = xq + l16 * xs + c * KC + 8 * q4;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const int piece = 4 * s + q4;
+      vec8 b[NT], bu[NT];
+#pragma unroll
+      for (int ct = 0; ct < NT; ++ct) {
+        b[ct] = *reinterpret_cast<const vec8 *>(wl + kstream_lds_offset<KC>(16 * ct + l16, piece));
+        if constexpr (SWIGLU)
+          bu[ct] = *reinterpret_cast<const vec8 *>(wl + kstream_lds_offset<KC>(CW + 16 * ct + l16, piece));
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const vec8 a = *reinterpret_cast<const vec8 *>(xa + 16 * mt * xs + 32 * s);
+#pragma unroll
+        for (int ct = 0; ct < NT; ++ct) {
+          acc[mt][ct] = M::mma(a, b[ct], acc[mt][ct]);
+          if constexpr (SWIGLU) accu[mt][ct] = M::mma(a, bu[ct], accu[mt][ct]);
+        }
+        if constexpr (EPI == kEpiNorm)
+          if (first) ssq[mt] = dot8<T>(a, a, ssq[mt]);
+      }
+    }
+    __asm__ volatile("" ::: "memory");
+  };
+
+  // Every workgroup has a tile (the host keeps groups <= ntiles): no path
+  // skips the stream, so the prefetch above stays ahead of the x stores.
+  int32_t tile = 0, c0 = 0;
+  for (;;) {
+    const bool first = tile == 0;
+#pragma unroll
+    for (int s = 0; s < INFL; ++s) {
+      compute(c0 + s, wr[s], first);
+      load_w(s, wr[s]);
+    }
+    next_group();
+    c0 += INFL;
+    if (c0 < nch) continue;
+    // Tile done: the four wavefront tiles meet in LDS (as linear_kstream_kernel's epilogue).
+    __syncthreads();  // every wavefront's operand reads are done (the sums reuse the staging)
+    if constexpr (EPI == kEpiNorm) {
+      if (first) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          float v = ssq[mt];
+          v += __shfl_xor(v, 16, 64);
+          v += __shfl_xor(v, 32, 64);
+          if (q4 == 0) ssq_rows[wave * XR + 16 * mt + l16] = v;
+        }
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < NT; ++ct)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          tiles[((wave * kTiles) * NT + ct) * kItems + (mt * 4 + r) * 64 + lane] = acc[mt][ct][r];
+          if constexpr (SWIGLU)
+            tiles[((wave * kTiles + 1) * NT + ct) * kItems + (mt * 4 + r) * 64 + lane] = accu[mt][ct][r];
+        }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NT * kItems / 256; ++j) {
+      const int it = threadIdx.x + 256 * j;
+      const int ct = it / kItems;
+      const int item = it - ct * kItems;
+      float sum = 0.f, sumu = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < 4; ++wv) {
+        sum += tiles[((wv * kTiles) * NT + ct) * kItems + item];
+        if constexpr (SWIGLU) sumu += tiles[((wv * kTiles + 1) * NT + ct) * kItems + item];
+      }
+      const int mt = item >> 8;
+      const int r = (item >> 6) & 3;
+      const int il = item & 63;
+      const int32_t row = 16 * mt + 4 * (il >> 4) + r;
+      if constexpr (EPI == kEpiNorm) {
+        const float sq = ((ssq_rows[row] + ssq_rows[XR + row]) + ssq_rows[2 * XR + row]) +
+                         ssq_rows[3 * XR + row];
+        const float scale = rsqrtf(sq / static_cast<float>(k) + extra.eps);
+        sum *= scale;
+        sumu *= scale;
+      }
+      // Rounded outputs (before the residual add) wait in LDS for the stores
+      // after the stream: [tile][XR][CW].
+      T out;
+      if constexpr (SWIGLU)
+        out = from_float<T>(swiglu_act(to_float(from_float<T>(sum)), to_float(from_float<T>(sumu))));
+      else
+        out = from_float<T>(sum);
+      outs[tile * XR * CW + row * CW + 16 * ct + (il & 15)] = out;
+    }
+    __syncthreads();  // the sums are read before the next tile writes them
+    zero_acc();
+    c0 = 0;
+    if (++tile == my_tiles) break;
+  }
+  // Stores after the stream (a store inside it would leave the loads'
+  // wait counts unknown at the loop head).
+  for (int32_t e = threadIdx.x; e < my_tiles * XR * CW; e += 256) {
+    const int32_t tile = e / (XR * CW);
+    const int32_t rc = e - tile * XR * CW;
+    const int32_t row = rc / CW;
+    const int32_t col = (static_cast<int32_t>(blockIdx.x) + tile * groups) * CW + (rc - row * CW);
+    if (row >= m || col >= n) continue;
+    T out = outs[e];
+    if constexpr (EPI == kEpiResidual)
+      out = from_float<T>(to_float(out) +
+                          to_float(extra.residual[static_cast<int64_t>(row) * extra.residual_stride + col]));
+    y[static_cast<int64_t>(row) * y_stride + col] = out;
+  }
+}
+
 template <typename T, int MT, int KC, bool SWIGLU, int NT, int EPI>
 void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
                     int64_t y_stride, int32_t m, int32_t n, int32_t k, const KstreamExtra<T> &extra,
@@ -587,6 +850,60 @@ void launch_kstream(const void *x, int64_t x_stride, const void *w, int64_t w_st
                      static_cast<T *>(y), y_stride, m, n, k, k_per_wave, extra);
 }
 
+// The activation-resident SwiGLU + RMSNorm launch (linear_xres_kernel):
+// 32-row blocks (MT 2), one 16-column tile per step (NT 1), eight 64-k
+// chunks in flight, 128 column groups per row block (one workgroup per
+// compute unit at 64 rows, each holding at most kXresMaxTiles tiles' outputs
+// in LDS).  Taken for 49-64 rows at K = 2048 (K quarters of 512) when the
+// tiles fit: gate|up + SwiGLU of TinyLlama at 64 rows, 17.3 -> 15.9 us
+// (MI355X, graph-timed, bit-identical); at 17-48 rows it is slower than
+// the K-split form (32 rows 13.5 against 15.7).
+constexpr int kXresMt = 2;
+constexpr int kXresNt = 1;
+constexpr int kXresInflight = 8;
+constexpr int kXresKq = 512;
+constexpr int kXresMaxTiles = 4;
+constexpr int kXresGroups = 128;
+
+size_t xres_lds_bytes(size_t elem) {
+  constexpr int XR = 16 * kXresMt, CW = 16 * kXresNt;
+  const size_t stage = static_cast<size_t>(4) * 2 * CW * 64 * elem;
+  const size_t sums = static_cast<size_t>(4) * 2 * kXresNt * kXresMt * 256 * 4;
+  return static_cast<size_t>(4) * XR * (kXresKq + 8) * elem + (stage > sums ? stage : sums) +
+         static_cast<size_t>(4) * XR * 4 + static_cast<size_t>(kXresMaxTiles) * XR * CW * elem;
+}
+
+bool xres_fits(int32_t m, int32_t n, int32_t k) {
+  const int32_t ntiles = (n + 16 * kXresNt - 1) / (16 * kXresNt);
+  return m > 48 && m <= 64 && k == 4 * kXresKq && ntiles >= kXresGroups &&
+         (ntiles + kXresGroups - 1) / kXresGroups <= kXresMaxTiles;
+}
+
+template <typename T>
+void launch_xres_swiglu_norm(const void *x, int64_t x_stride, const void *w, int64_t w_stride,
+                             void *y, int64_t y_stride, int32_t m, int32_t n, int32_t k,
+                             const KstreamExtra<T> &extra, hipStream_t stream) {
+  auto kernel = &linear_xres_kernel<T, kXresMt, kXresNt, true, kEpiNorm, kXresInflight, kXresKq,
+                                    kXresMaxTiles>;
+  const size_t lds = xres_lds_bytes(sizeof(T));
+  // Raise the kernel's dynamic LDS limit once per device (a failure shows up
+  // as a launch error).
+  constexpr int kMaxDevices = 64;
+  static std::atomic<bool> raised[kMaxDevices];
+  int device = 0;
+  if (hipGetDevice(&device) == hipSuccess && device >= 0 && device < kMaxDevices &&
+      !raised[device].load(std::memory_order_acquire)) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(lds)) == hipSuccess)
+      raised[device].store(true, std::memory_order_release);
+  }
+  const unsigned row_blocks = static_cast<unsigned>((m + 16 * kXresMt - 1) / (16 * kXresMt));
+  hipLaunchKernelGGL(kernel, dim3(kXresGroups, row_blocks), dim3(256), lds, stream,
+                     static_cast<const T *>(x), x_stride, static_cast<const T *>(w), w_stride,
+                     static_cast<T *>(y), y_stride, m, n, k, kXresGroups, extra);
+}
+
 // Chunk 64 for the SwiGLU form and above 32 rows, else 128.  A workgroup
 // reads 16 (MT + NT) rows of K (x rows and weight rows; twice NT weight
 // rows for SwiGLU), so fewer rows per workgroup means fewer re-reads of x;
@@ -603,6 +920,12 @@ template <typename T, bool SWIGLU, int EPI>
 void launch_kstream_mt(const void *x, int64_t x_stride, const void *w, int64_t w_stride, void *y,
                        int64_t y_stride, int32_t m, int32_t n, int32_t k,
                        const KstreamExtra<T> &extra, hipStream_t stream) {
+  if constexpr (SWIGLU && EPI == kEpiNorm) {
+    if (xres_fits(m, n, k)) {
+      launch_xres_swiglu_norm<T>(x, x_stride, w, w_stride, y, y_stride, m, n, k, extra, stream);
+      return;
+    }
+  }
   const int32_t row_tiles = (m + 15) / 16;
   // 64-wide chunks above 32 rows (twice the chunks per wavefront, half the
   // staging per chunk), 128 up to 32 rows; bit-identical either way (the

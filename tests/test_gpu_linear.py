@@ -316,6 +316,41 @@ def test_linear_kswiglu_norm_is_the_norm_then_the_mlp_input(device, dtype, rows,
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [49, 57, 64])
+@pytest.mark.parametrize("inter", [2048, 5632, 8192])
+def test_activation_resident_swiglu_norm_equals_the_k_split_form(device, dtype, rows, inter):
+    """At 49-64 rows and K = 2048 the SwiGLU + RMSNorm launch keeps each
+    workgroup's rows of x in LDS and streams only the weight; per row it is
+    bit-identical to the K-split form, which the same call takes in chunks of
+    at most 32 rows (strided x and output rows)."""
+
+    from tensorforge_amd.kernels import fold_norm_gain, linear_swiglu
+
+    eps, k = 1e-5, 2048
+    generator = torch.Generator().manual_seed(rows * 31 + inter)
+    x_wide = (torch.randn(rows, k + 64, generator=generator) * 2.0).to(dtype).to(device)
+    x = x_wide[:, 32:32 + k]
+    w = (torch.randn(2 * inter, k, generator=generator) * 0.05).to(dtype)
+    gain = (1.0 + 0.1 * torch.randn(k, generator=generator)).to(dtype)
+    folded = fold_norm_gain(w.to(device), gain.to(device))
+    wide = torch.full((rows, inter + 8), float("nan"), dtype=dtype, device=device)
+    linear_swiglu(x, folded, output=wide[:, :inter], k_split=True, norm_eps=eps)
+    chunks = torch.full_like(wide, float("nan"))
+    for r0 in range(0, rows, 32):
+        r1 = min(r0 + 32, rows)
+        linear_swiglu(x[r0:r1], folded, output=chunks[r0:r1, :inter], k_split=True, norm_eps=eps)
+    torch.cuda.synchronize()
+    assert torch.equal(wide[:, :inter].view(torch.int16), chunks[:, :inter].view(torch.int16))
+    assert bool(wide[:, inter:].isnan().all())
+    gu = (_rms_scale(x.cpu(), eps) * (x.float().cpu() @ folded.float().cpu().T)).to(dtype).float()
+    g, u = gu[:, :inter], gu[:, inter:]
+    expected = g * torch.sigmoid(g) * u
+    tol = TOLERANCE[dtype]
+    torch.testing.assert_close(wide[:, :inter].float().cpu(), expected, rtol=tol,
+                               atol=tol * float(expected.abs().max()))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows", [1, 33, 64])
 @pytest.mark.parametrize(("n", "k"), [(2048, 2048), (2048, 5632), (100, 96)])
 def test_linear_kstream_residual_is_the_rounded_residual_sum(device, dtype, rows, n, k):
