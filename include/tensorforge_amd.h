@@ -487,7 +487,10 @@ int32_t tf_linear_kstream_norm(const void *x, int64_t x_row_stride, const void *
  * scaled by rsqrt(mean_k(x[i][k]^2) + eps) before the activation, the
  * stacked weight carrying the norm's gain.  Replaces the reference's
  * post-attention RMSNorm followed by the MLP's gate and up projections and
- * SwiGLU (triton_ops.py:179-205; model/layers.py:144-158).
+ * SwiGLU (triton_ops.py:179-205; model/layers.py:144-158).  At 49-64 rows
+ * with k = 2048 (and 2048-8192 intermediate columns) the launch keeps each
+ * workgroup's 32 rows of x in LDS and streams only the weight; the results
+ * are the same bits either way.
  */
 int32_t tf_linear_kswiglu_norm(const void *x, int64_t x_row_stride, const void *gate_up_weight,
                                int64_t weight_row_stride, void *y, int64_t y_row_stride, int32_t m,
